@@ -1,0 +1,202 @@
+#!/usr/bin/env python3
+"""Headline benchmark: the M=1 W4A16 decode GEMV at K=4096, N=14336, g=128.
+
+BASELINE.json's metric is "M=1 W4A16 GEMV us & % HBM peak (4096x14336);
+8B-shape decode tok/s", quoted on configs[1]'s gate/up shape.  A *step* is
+one ``nibblegemm_amd.gemv`` call (M=1) over one batch of synthetic inputs
+(nibbles U{0..15}, scales fp16 U(0.002, 0.02), activations fp16 N(0,1)).
+
+* Inputs are resident in HBM before timing.  Each step reads a different copy
+  of the packed weights and scales from a rotation spanning >= 1 GiB, so no
+  step is served from the 256 MiB Infinity Cache or the L2s.
+* ``--warmup W`` eager steps run untimed, then the K timed steps are captured
+  into one HIP graph (capture executes nothing), replayed once untimed, and
+  replayed once timed between events on the replay stream, bracketed by
+  ``torch.cuda.synchronize()``.  ``ms_per_step`` = elapsed / K.
+* ``value`` = algorithmic bytes per step (K*N/2 + (K/128)*N*2 + 2K + 2N) /
+  ms_per_step, in GB/s.  ``roofline`` prices the same figure against MI355X's
+  8 TB/s; ``cpu_baseline`` times the CPU oracle (dequantize + fp32 matmul,
+  the reference's CPU path) on this host on a bounded sample.
+
+Prints ONE JSON line.  Only ``--gpus 1`` is supported (one GPU per box).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "M=1 W4A16 GEMV µs & % HBM peak (4096x14336); 8B-shape decode tok/s"
+K, N, M, G = 4096, 14336, 1, 128
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(target_s: float) -> dict:
+    """The reference's CPU path (dequantize + fp32 matmul), via the CPU oracle."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O  # noqa: PLC0415  (cpu_baseline leg only)
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(os.cpu_count() or 1, 16)
+    one = O.time_reference_path(M, K, N, G, reps=1, threads=threads)
+    reps = int(max(3, min(60, target_s / max(one["total_s"], 1e-3))))
+    r = O.time_reference_path(M, K, N, G, reps=reps, threads=threads)
+    nbytes = K * N // 2 + (K // G) * N * 2 + M * K * 2 + M * N * 2
+    return {
+        "value": round(nbytes / r["total_s"] / 1e9, 3),
+        "unit": "GB/s",
+        "cores": r["threads"],
+        "kind": "port",
+        "sample": (f"oracle dequantize + fp32 matmul (the reference CPU path), M=1 K={K} N={N} "
+                   f"g={G}, median of {reps} reps after 1 warm-up; dequant "
+                   f"{r['dequant_s'] * 1e3:.1f} ms + matmul {r['matmul_s'] * 1e3:.1f} ms "
+                   f"= {r['total_s'] * 1e3:.1f} ms per step"),
+        "ms_per_step": round(r["total_s"] * 1e3, 3),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--skip-extras", action="store_true",
+                    help="skip the copy-bandwidth, hipBLASLt and eager side measurements")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE={world}); "
+              "the W4A16 path has no multi-GPU leg in this build.", file=sys.stderr)
+        return 2
+    steps, warmup = max(1, args.steps), max(0, args.warmup)
+
+    import torch  # noqa: PLC0415
+
+    import nibblegemm_amd as ng  # noqa: PLC0415
+    from nibblegemm_amd import harness as H  # noqa: PLC0415
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    ng.extension()  # fail loudly if the native library is missing
+    dev = torch.device("cuda", 0)
+    log(H.device_summary())
+
+    # ---- synthetic inputs (host-generated, seeded), resident in HBM ----------
+    gen = torch.Generator().manual_seed(0)
+    qu = torch.randint(0, 16, (K, N), generator=gen, dtype=torch.uint8).numpy()
+    qweight = torch.from_numpy(ng.pack_nibbles(qu)).to(dev)
+    scales = (torch.rand((K // G, N), generator=gen) * 0.018 + 0.002).to(torch.float16).to(dev)
+    X = torch.randn((M, K), generator=gen).to(torch.float16).to(dev)
+    rot_w = H.Rotation(qweight)
+    rot_s = [scales] + [scales.clone() for _ in range(rot_w.count - 1)]
+    variants = H.Cycle(ng.QuantizedWeight(rot_w[i], rot_s[i], G, K, N) for i in range(rot_w.count))
+    nbytes = H.total_bytes(M, K, N, G, 4)
+    log(f"rotation: {rot_w.count} copies, {rot_w.total_bytes / 2**30:.2f} GiB of packed weights")
+
+    # ---- warmup (untimed, eager) ---------------------------------------------
+    for i in range(warmup):
+        ng.gemv(X, variants[i])
+    torch.cuda.synchronize()
+
+    # ---- K timed steps: one HIP graph of K calls -------------------------------
+    runner = H.GraphRunner(lambda i: ng.gemv(X, variants[i]), reps=steps, warmup=0)
+    runner.graph.replay()  # untimed: first replay uploads the graph
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    runner.graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    ms_per_step = start.elapsed_time(end) / steps
+    gbps = H.achieved_gbps(nbytes, ms_per_step)
+    log(f"gemv M=1 {K}x{N}: {ms_per_step * 1e3:.2f} us/step, {gbps:.0f} GB/s "
+        f"({100 * gbps / H.HBM_PEAK_GBPS:.1f}% of 8 TB/s)")
+
+    extras = {}
+    if not args.skip_extras:
+        eager = H.bench(lambda i: ng.gemv(X, variants[i]), reps=32, trials=10, warmup=2)
+        extras["eager_us_per_call"] = round(eager.median_ms * 1e3, 2)
+        copy = H.measured_copy_gbps()
+        extras["copy_gbps"] = round(copy, 1)
+        extras["pct_of_copy_bw"] = round(100 * gbps / copy, 1)
+        torch.backends.cuda.matmul.allow_tf32 = False
+        w16 = (torch.randn((K, N), generator=gen) * 0.02).to(torch.float16).to(dev)
+        rot16 = H.Rotation(w16)
+        fp16 = H.bench_graph(lambda i: torch.mm(X, rot16[i]), reps=64, trials=10)
+        extras["hipblaslt_fp16_us"] = round(fp16.median_ms * 1e3, 2)
+        extras["speedup_vs_hipblaslt_fp16"] = round(fp16.median_ms / ms_per_step, 2)
+        fp16_bytes = H.total_bytes(M, K, N, G, 16)
+        extras["byte_ratio_ceiling"] = round(fp16_bytes / nbytes, 3)
+        del rot16, w16
+        log(f"copy {copy:.0f} GB/s; hipBLASLt fp16 {fp16.median_ms * 1e3:.2f} us; "
+            f"eager {eager.median_ms * 1e3:.2f} us/call")
+
+    roofline = {
+        "bound": "hbm",
+        "achieved": round(gbps, 1),
+        "peak": H.HBM_PEAK_GBPS,
+        "unit": "GB/s",
+        "frac": round(gbps / H.HBM_PEAK_GBPS, 4),
+        "traffic": _committed_traffic(),
+    }
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        t0 = time.perf_counter()
+        cpu = cpu_baseline(args.cpu_seconds)
+        log(f"cpu baseline {cpu['value']} GB/s on {cpu['cores']} threads "
+            f"({time.perf_counter() - t0:.1f} s)")
+
+    line = {
+        "metric": METRIC,
+        "value": round(gbps, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(ms_per_step, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "accumulate": "f32",
+        "data": "synthetic",
+        "config": {"workload": f"gemv M={M} K={K} N={N} g={G} (BASELINE configs[1] headline shape)",
+                   "M": M, "K": K, "N": N, "group_size": G},
+        "gemv_us": round(ms_per_step * 1e3, 3),
+        "pct_hbm_peak": round(100 * gbps / H.HBM_PEAK_GBPS, 2),
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        **extras,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def _committed_traffic():
+    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE,
+    scaled by the copy-kernel calibration), committed under profiles/."""
+    path = os.path.join(ROOT, "profiles", "gemv_m1_4096x14336_traffic.json")
+    try:
+        with open(path) as fh:
+            return json.load(fh).get("traffic_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,134 @@
+/*
+ * nibblegemm_amd.h -- C ABI of the MI355X (gfx950) W4A16 kernel library.
+ *
+ * This is the drop-in boundary.  It replaces the reference's pybind11 module
+ * `nibblegemm_cuda` (csrc/bindings.cpp:11-22 in arvindcr4/nibblegemm), whose
+ * three functions took and returned torch tensors.  Here every entry point takes
+ * plain device pointers, shapes and a HIP stream, and returns a status code:
+ *
+ *   nibble_gemv_w4a16   <- gemv_w4a16(X, Wq, S, group_size, version=4,
+ *                                     splits_override=0, threads_override=0)
+ *                          csrc/bindings.cpp:12-15, csrc/gemv_w4a16.cu:341-425
+ *   nibble_gemm_w4a16   <- gemm_w4a16(X, Wq, S, group_size, version=6)
+ *                          csrc/bindings.cpp:16-19, csrc/gemm_w4a16.cu:379-429
+ *   nibble_dequant_w4   <- dequant_w4(Wq, S, group_size, fast=True)
+ *                          csrc/bindings.cpp:20-21, csrc/dequant_kernel.cu:48-74
+ *
+ * Tensor-shape arguments are passed as the reference's tensors would report
+ * them (rows and columns of X, Wq and S), so the library can apply exactly the
+ * reference's host checks (csrc/gemv_w4a16.cu:251-265, csrc/gemm_w4a16.cu:
+ * 381-400, csrc/dequant_kernel.cu:49-52) before any HIP call.  dtype, device
+ * and contiguity are properties of tensors, not of pointers; the caller checks
+ * those (the Python layer in nibblegemm_amd/ops.py does).
+ *
+ * Data layout (all row-major, contiguous):
+ *   X   fp16  [M, K]        activations
+ *   Wq  int32 [K/8, N]      packed nibbles, slot order {0,4,1,5,2,6,3,7} along K,
+ *                           stored value = q + 8 (implicit zero-point 8)
+ *   S   fp16  [K/G, N]      one scale per group of G rows along K
+ *   Y   fp16  [M, N]        output (caller-allocated)
+ *   W   fp16  [K, N]        dequant output (caller-allocated)
+ *
+ * Ownership: inputs are borrowed; outputs and workspace are caller-allocated
+ * (the reference allocated them inside the call, gemv_w4a16.cu:350, :403-408).
+ * The library allocates no device memory and keeps no mutable global state
+ * beyond per-device attribute caches, so calls on different streams and
+ * threads are independent -- except that calls sharing one workspace must be
+ * ordered on one stream.
+ *
+ * Errors: a non-zero status.  nibble_last_error() returns this thread's message
+ * for the most recent failing call (the reference raised c10::Error, seen in
+ * Python as RuntimeError).  Validation failures never touch the GPU.
+ */
+#ifndef NIBBLEGEMM_AMD_H_
+#define NIBBLEGEMM_AMD_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NIBBLE_ABI_VERSION 1
+
+#if defined(__GNUC__) || defined(__clang__)
+#define NIBBLE_API __attribute__((visibility("default")))
+#else
+#define NIBBLE_API
+#endif
+
+enum {
+  NIBBLE_OK = 0,
+  NIBBLE_ERR_INVALID_ARGUMENT = 1, /* a reference TORCH_CHECK would have fired */
+  NIBBLE_ERR_UNSUPPORTED = 2,      /* valid request this kernel does not serve (e.g. gemv M > 8) */
+  NIBBLE_ERR_WORKSPACE = 3,        /* workspace missing, too small or misaligned */
+  NIBBLE_ERR_HIP = 4               /* a HIP runtime call or kernel launch failed */
+};
+
+/* Version of this header the library was built from (NIBBLE_ABI_VERSION). */
+NIBBLE_API int nibble_abi_version(void);
+
+/* Message for the last failing call on the calling thread ("" if none). */
+NIBBLE_API const char* nibble_last_error(void);
+
+/*
+ * Decode-regime matmul Y = X @ dequant(Wq, S), M <= 8 for versions 3 and 4.
+ *
+ * version           0 = scalar fp32 reference kernel (one thread per output);
+ *                   1 = scalar decode, packed word reused for its 8 k;
+ *                   2, 3 = the streaming kernel with one K split;
+ *                   4 = the streaming kernel with split-K (default).
+ * splits_override   0 = heuristic; else the number of K splits (version 4).
+ * threads_override  0 = heuristic; else workgroup size in {64,128,256,512,1024}.
+ * workspace         version 4 with more than one split needs
+ *                   nibble_gemv_workspace_bytes(...) bytes, 256-byte aligned.
+ *                   Its first nibble_gemv_counter_bytes(...) bytes must be zero
+ *                   before the first call; every call leaves them zero again.
+ *                   May be NULL when the query returns 0.
+ * stream            hipStream_t (NULL = the null stream of the current device).
+ */
+NIBBLE_API int nibble_gemv_w4a16(const void* X, int64_t x_rows, int64_t x_cols,
+                      const void* Wq, int64_t wq_rows, int64_t wq_cols,
+                      const void* S, int64_t s_rows, int64_t s_cols,
+                      int64_t group_size, int64_t version, int64_t splits_override,
+                      int64_t threads_override, void* Y, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
+/* Bytes of workspace nibble_gemv_w4a16 needs for these arguments (0 if none).
+ * Uses the device's CU count for the split heuristic, so it may make one HIP
+ * attribute query; returns 0 for arguments the launcher would reject. */
+NIBBLE_API size_t nibble_gemv_workspace_bytes(int64_t M, int64_t K, int64_t N, int64_t group_size,
+                                   int64_t version, int64_t splits_override,
+                                   int64_t threads_override, void* stream);
+
+/* Leading bytes of that workspace that must be zero on entry (split counters). */
+NIBBLE_API size_t nibble_gemv_counter_bytes(int64_t M, int64_t K, int64_t N, int64_t group_size,
+                                 int64_t version, int64_t splits_override,
+                                 int64_t threads_override, void* stream);
+
+/*
+ * Prefill-regime matmul on CDNA4 MFMA (any M >= 1).  version 6 (default) or 7
+ * (alternate tile shape; same numerics).  Requires K % 32 == 0, N even,
+ * group_size in {64, 128} and M*N, M*K, K*N < 2^31 (the reference's checks).
+ */
+NIBBLE_API int nibble_gemm_w4a16(const void* X, int64_t x_rows, int64_t x_cols,
+                      const void* Wq, int64_t wq_rows, int64_t wq_cols,
+                      const void* S, int64_t s_rows, int64_t s_cols,
+                      int64_t group_size, int64_t version, void* Y, void* stream);
+
+/*
+ * Dense fp16 W [K, N] from packed weights, bit-exact with the reference's
+ * dequantize(): W[k][n] = fp16_rne((nibble - 8) * S[k / G][n]).
+ * fast != 0 selects the magic-exponent decode, fast == 0 the scalar
+ * shift/mask/convert decode; both give identical bits.  K = wq_rows * 8.
+ */
+NIBBLE_API int nibble_dequant_w4(const void* Wq, int64_t wq_rows, int64_t wq_cols,
+                      const void* S, int64_t s_rows, int64_t s_cols,
+                      int64_t group_size, int fast, void* W, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NIBBLEGEMM_AMD_H_ */

@@ -1,0 +1,39 @@
+"""nibblegemm_amd -- W4A16 (INT4 weight, fp16 activation) kernels for AMD
+Instinct MI355X (gfx950).
+
+Drop-in for the Python surface of arvindcr4/nibblegemm
+(python/nibblegemm/__init__.py:19-38): the packed format and its helpers, the
+kernel entry points, the batch-size dispatch and ``QuantLinear``.  The kernels
+are hand-written HIP behind the C ABI in ``include/nibblegemm_amd.h``.
+
+GPTQ (``gptq_quantize``, ``quantize_model_gptq``, ``HessianAccumulator``,
+``find_decoder_blocks``) and the Triton baseline of the reference are not part
+of this package.
+"""
+
+from .ops import DECODE_MAX_M, QuantLinear, dequant, extension, gemm, gemv, matmul
+from .quant import (
+    QuantizedWeight,
+    dequantize,
+    pack_nibbles,
+    quantize,
+    reference_matmul,
+    unpack_nibbles,
+)
+
+__all__ = [
+    "DECODE_MAX_M",
+    "QuantLinear",
+    "QuantizedWeight",
+    "dequant",
+    "dequantize",
+    "extension",
+    "gemm",
+    "gemv",
+    "matmul",
+    "pack_nibbles",
+    "quantize",
+    "reference_matmul",
+    "unpack_nibbles",
+]
+__version__ = "0.1.0"

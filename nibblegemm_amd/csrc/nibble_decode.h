@@ -1,0 +1,97 @@
+// INT4 -> fp16 decode primitives for gfx950.
+//
+// Packed format: one 32-bit word holds 8 consecutive k of one column.  Logical
+// offset k lives in nibble slot {0,4,1,5,2,6,3,7}[k] (even k in slots 0..3, odd
+// k in slots 4..7; python/nibblegemm/quant.py:28-50 in the reference), and the
+// stored value is q + 8.
+//
+// Fast decode (the fp16 magic-exponent method): 0x6400 is fp16 1024.0 and the
+// ten mantissa bits below it count in units of 1, so OR-ing a nibble n into the
+// low mantissa bits gives exactly 1024 + n; OR-ing it one nibble higher gives
+// 1024 + 16n.  One v_and_or_b32 ((a & mask) | 0x64006400) extracts two nibbles
+// that sit 16 bits apart straight into a packed half2.  Because of the slot
+// interleave, the four masks/shifts below hand back k = (0,1), (2,3), (4,5),
+// (6,7) in that order:
+//
+//   (q      & 0x000f000f) | magic -> slots 0,4 -> k 0,1  as 1024 + n
+//   (q      & 0x00f000f0) | magic -> slots 1,5 -> k 2,3  as 1024 + 16n
+//   (q >> 8 & 0x000f000f) | magic -> slots 2,6 -> k 4,5  as 1024 + n
+//   (q >> 8 & 0x00f000f0) | magic -> slots 3,7 -> k 6,7  as 1024 + 16n
+//
+// The bias 1024 and the zero-point 8 come off in one v_pk_add_f16 (-1032) for
+// the low pairs and one v_pk_fma_f16 (x/16 - 72) for the high pairs.  Every
+// intermediate is an integer <= 1264, exactly representable in fp16, so the
+// result is the exact n - 8.  9 VALU ops decode 8 weights.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace nibble {
+
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
+
+constexpr uint32_t kMaskLo = 0x000f000fu;
+constexpr uint32_t kMaskHi = 0x00f000f0u;
+constexpr uint32_t kMagic = 0x64006400u;  // two copies of fp16 1024.0
+
+__device__ __forceinline__ h2_t as_h2(uint32_t v) { return __builtin_bit_cast(h2_t, v); }
+__device__ __forceinline__ uint32_t as_u32(h2_t v) { return __builtin_bit_cast(uint32_t, v); }
+
+// (a & mask) | magic -- selected as a single v_and_or_b32.
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t magic) {
+  return (a & mask) | magic;
+}
+
+// The four raw magic-biased pairs of one word: k (0,1) and (4,5) as 1024 + n,
+// k (2,3) and (6,7) as 1024 + 16n.
+__device__ __forceinline__ void decode8_raw(uint32_t q, uint32_t (&r)[4]) {
+  const uint32_t qh = q >> 8;
+  r[0] = and_or(q, kMaskLo, kMagic);
+  r[1] = and_or(q, kMaskHi, kMagic);
+  r[2] = and_or(qh, kMaskLo, kMagic);
+  r[3] = and_or(qh, kMaskHi, kMagic);
+}
+
+// Exact (n - 8) for k = 0..7 as four half2 in ascending k.
+__device__ __forceinline__ void decode8(uint32_t q, h2_t (&out)[4]) {
+  uint32_t r[4];
+  decode8_raw(q, r);
+  const h2_t bias_lo = {(_Float16)1032.0f, (_Float16)1032.0f};
+  const h2_t mul_hi = {(_Float16)0.0625f, (_Float16)0.0625f};
+  const h2_t bias_hi = {(_Float16)-72.0f, (_Float16)-72.0f};
+  out[0] = as_h2(r[0]) - bias_lo;
+  out[1] = __builtin_elementwise_fma(as_h2(r[1]), mul_hi, bias_hi);
+  out[2] = as_h2(r[2]) - bias_lo;
+  out[3] = __builtin_elementwise_fma(as_h2(r[3]), mul_hi, bias_hi);
+}
+
+// decode8 followed by one round-to-nearest-even fp16 multiply by the group
+// scale: fp16((n - 8) * s), bit-identical to the reference dequantize().
+__device__ __forceinline__ void decode8_scaled(uint32_t q, h2_t scale2, h2_t (&out)[4]) {
+  decode8(q, out);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) out[i] = out[i] * scale2;
+}
+
+// Scalar decode of logical offset k (0..7): shift, mask, subtract the
+// zero-point.  Slot formula from csrc/dequant.cuh:94-99 in the reference.
+__device__ __forceinline__ int nibble_value(uint32_t q, int k) {
+  const int slot = (k & 1) ? (4 + (k >> 1)) : (k >> 1);
+  return static_cast<int>((q >> (4 * slot)) & 0xFu) - 8;
+}
+
+// Buffer resource for raw buffer loads on gfx9: base, stride 0, byte extent,
+// and the gfx9 data-format dword.  Loads past `bytes` return zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+
+}  // namespace nibble

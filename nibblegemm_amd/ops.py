@@ -1,0 +1,230 @@
+"""Kernel entry points and the drop-in ``QuantLinear``.
+
+Mirrors ``python/nibblegemm/ops.py`` of arvindcr4/nibblegemm (names, defaults,
+dispatch rule and error types), over the C ABI in ``include/nibblegemm_amd.h``
+instead of a pybind11 torch extension:
+
+* tensors are validated here exactly as the reference's ``TORCH_CHECK``s did
+  (dtype, device, contiguity, rank: ``RuntimeError``); shape checks run inside
+  the library and come back as a status that is raised as ``RuntimeError``;
+* outputs are allocated here with torch on X's device (Wq's for ``dequant``),
+  as the reference allocated them in C++;
+* kernels launch on torch's current stream of that device, so calls compose
+  with torch ops and can be recorded into CUDA/HIP graphs;
+* the split-K workspace of ``gemv`` comes from a cache of zeroed buffers keyed
+  by (device, stream, graph capture): the kernel returns its counter region to
+  zero at the end of every call, so a buffer is zeroed once and then reused.
+  Inside a graph capture the first call allocates and zeroes a buffer for that
+  capture, so the zeroing is part of the graph and every replay starts from
+  zero; that buffer stays cached (one per capture) for the life of the process.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from typing import Dict, Optional, Tuple
+
+import torch
+
+from . import _native
+from .quant import QuantizedWeight, quantize  # noqa: F401  (re-exported)
+
+#: Batch sizes at or below this go to the bandwidth-bound decode kernel
+#: (reference ops.py:30).
+DECODE_MAX_M = 8
+
+_lock = threading.Lock()
+_workspaces: Dict[Tuple[int, int, int], torch.Tensor] = {}
+_ws_plan: Dict[tuple, Tuple[int, int]] = {}
+
+_get_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def extension():
+    """The loaded native binding (reference ops.py:33-56 JIT-built its extension
+    here; this package is built in-tree ahead of time and only loads it)."""
+    return _native.binding()
+
+
+def _raise(rc: int, ext) -> None:
+    raise RuntimeError(f"nibblegemm_amd: {ext.last_error()} (status {rc})")
+
+
+def _stream(device: torch.device) -> int:
+    if _get_raw_stream is not None:
+        return _get_raw_stream(device.index if device.index is not None else torch.cuda.current_device())
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _check_matmul_inputs(X: torch.Tensor, Wq: torch.Tensor, S: torch.Tensor) -> None:
+    """The dtype/device/layout half of check_inputs (reference
+    csrc/gemv_w4a16.cu:251-258, csrc/gemm_w4a16.cu:381-386)."""
+    if not (X.is_cuda and Wq.is_cuda and S.is_cuda):
+        raise RuntimeError("all tensors must live on the GPU")
+    if X.dtype != torch.float16:
+        raise RuntimeError("activations must be fp16")
+    if S.dtype != torch.float16:
+        raise RuntimeError("scales must be fp16")
+    if Wq.dtype != torch.int32:
+        raise RuntimeError("packed weights must be int32")
+    if not (X.is_contiguous() and Wq.is_contiguous() and S.is_contiguous()):
+        raise RuntimeError("inputs must be contiguous")
+    if X.dim() != 2 or Wq.dim() != 2 or S.dim() != 2:
+        raise RuntimeError("expected 2-D inputs")
+    if not (X.device == Wq.device == S.device):
+        raise RuntimeError("all tensors must live on the same device")
+
+
+_hip = None
+
+
+def _capture_id(stream: int) -> int:
+    """0 outside graph capture, else the HIP capture id of ``stream``."""
+    if not torch.cuda.is_current_stream_capturing():
+        return 0
+    global _hip
+    if _hip is None:
+        lib = ctypes.CDLL("libamdhip64.so.7")  # the runtime torch already loaded
+        lib.hipStreamGetCaptureInfo.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_int),
+                                                ctypes.POINTER(ctypes.c_ulonglong)]
+        lib.hipStreamGetCaptureInfo.restype = ctypes.c_int
+        _hip = lib
+    status, cid = ctypes.c_int(0), ctypes.c_ulonglong(0)
+    rc = _hip.hipStreamGetCaptureInfo(ctypes.c_void_p(stream), ctypes.byref(status), ctypes.byref(cid))
+    if rc != 0:
+        raise RuntimeError(f"hipStreamGetCaptureInfo failed ({rc})")
+    return int(cid.value) or -1
+
+
+def _gemv_workspace(ext, device: torch.device, stream: int, M: int, K: int, N: int, g: int,
+                    version: int, splits: int, threads: int) -> Tuple[Optional[torch.Tensor], int]:
+    key = (M, K, N, g, version, splits, threads, device.index)
+    plan = _ws_plan.get(key)
+    if plan is None:
+        plan = ext.gemv_workspace_bytes(M, K, N, g, version, splits, threads, stream)
+        _ws_plan[key] = plan
+    nbytes = plan[0]
+    if nbytes == 0:
+        return None, 0
+    wkey = (device.index, stream, _capture_id(stream))
+    buf = _workspaces.get(wkey)
+    if buf is None or buf.numel() < nbytes:
+        with _lock:
+            buf = _workspaces.get(wkey)
+            if buf is None or buf.numel() < nbytes:
+                size = max(nbytes, 1 << 20)
+                buf = torch.zeros(size, dtype=torch.uint8, device=device)
+                _workspaces[wkey] = buf
+    return buf, buf.numel()
+
+
+def dequant(qw: QuantizedWeight, fast: bool = True) -> torch.Tensor:
+    """Expand packed INT4 to a dense ``[K, N]`` fp16 matrix on the device
+    (reference ops.py:59-61 -> csrc/dequant_kernel.cu:48-74)."""
+    ext = extension()
+    Wq, S = qw.qweight, qw.scales
+    if not (Wq.is_cuda and S.is_cuda):
+        raise RuntimeError("tensors must live on the GPU")
+    if Wq.dtype != torch.int32:
+        raise RuntimeError("packed weights must be int32")
+    if S.dtype != torch.float16:
+        raise RuntimeError("scales must be fp16")
+    if not (Wq.is_contiguous() and S.is_contiguous()):
+        raise RuntimeError("inputs must be contiguous")
+    if Wq.dim() != 2 or S.dim() != 2:
+        raise RuntimeError("expected 2-D inputs")
+    rows, N = Wq.shape
+    out = torch.empty((rows * 8, N), dtype=torch.float16, device=Wq.device)
+    rc = ext.dequant(Wq.data_ptr(), rows, N, S.data_ptr(), S.shape[0], S.shape[1],
+                     qw.group_size, 1 if fast else 0, out.data_ptr(), _stream(Wq.device))
+    if rc:
+        _raise(rc, ext)
+    return out
+
+
+def gemv(X: torch.Tensor, qw: QuantizedWeight, version: int = 4, splits: int = 0,
+         block_threads: int = 0) -> torch.Tensor:
+    """Decode-regime matmul (reference ops.py:64-74).
+
+    ``version``: 0/1 scalar fp32 kernels, 2/3 streaming kernel with one K split,
+    4 (default) streaming kernel with split-K.  ``splits`` and ``block_threads``
+    override the launch geometry (0 = heuristic); ``block_threads`` is a
+    multiple of the 64-lane wave.  Versions 3 and 4 serve M <= 8.
+    """
+    ext = extension()
+    Wq, S = qw.qweight, qw.scales
+    _check_matmul_inputs(X, Wq, S)
+    M, K = X.shape
+    N = Wq.shape[1]
+    dev = X.device
+    stream = _stream(dev)
+    Y = torch.empty((M, N), dtype=torch.float16, device=dev)
+    ws, ws_bytes = None, 0
+    if version == 4 and 0 < M <= DECODE_MAX_M:
+        ws, ws_bytes = _gemv_workspace(ext, dev, stream, M, K, N, qw.group_size, version, splits,
+                                       block_threads)
+    rc = ext.gemv(X.data_ptr(), M, K, Wq.data_ptr(), Wq.shape[0], N, S.data_ptr(), S.shape[0],
+                  S.shape[1], qw.group_size, version, splits, block_threads, Y.data_ptr(),
+                  ws.data_ptr() if ws is not None else None, ws_bytes, stream)
+    if rc:
+        _raise(rc, ext)
+    return Y
+
+
+def gemm(X: torch.Tensor, qw: QuantizedWeight, version: int = 6) -> torch.Tensor:
+    """Prefill-regime matmul on MFMA (reference ops.py:77-86).  ``version`` 6
+    (default) or 7 select two tile shapes with identical numerics."""
+    ext = extension()
+    Wq, S = qw.qweight, qw.scales
+    _check_matmul_inputs(X, Wq, S)
+    M, K = X.shape
+    N = Wq.shape[1]
+    dev = X.device
+    Y = torch.empty((M, N), dtype=torch.float16, device=dev)
+    rc = ext.gemm(X.data_ptr(), M, K, Wq.data_ptr(), Wq.shape[0], N, S.data_ptr(), S.shape[0],
+                  S.shape[1], qw.group_size, version, Y.data_ptr(), _stream(dev))
+    if rc:
+        _raise(rc, ext)
+    return Y
+
+
+def matmul(X: torch.Tensor, qw: QuantizedWeight, splits: int = 0,
+           block_threads: int = 0) -> torch.Tensor:
+    """``X @ dequant(qw)``, dispatching on batch size (reference ops.py:89-104):
+    M <= DECODE_MAX_M goes to ``gemv(version=4)``, larger M to ``gemm``."""
+    if X.dim() != 2:
+        raise ValueError(f"expected a 2-D activation matrix, got {tuple(X.shape)}")
+    if X.size(1) != qw.K:
+        raise ValueError(f"K mismatch: activations have {X.size(1)}, weights have {qw.K}")
+    if X.size(0) <= DECODE_MAX_M:
+        return gemv(X, qw, version=4, splits=splits, block_threads=block_threads)
+    return gemm(X, qw)
+
+
+class QuantLinear(torch.nn.Module):
+    """Drop-in replacement for ``nn.Linear`` with INT4 weights (reference
+    ops.py:107-135).  Buffers ``qweight``, ``scales`` and ``bias`` keep the
+    reference's names, so state dicts carry over unchanged."""
+
+    def __init__(self, qw: QuantizedWeight, bias: Optional[torch.Tensor] = None):
+        super().__init__()
+        self.register_buffer("qweight", qw.qweight)
+        self.register_buffer("scales", qw.scales)
+        self.register_buffer("bias", bias if bias is not None else None)
+        self.group_size, self.K, self.N = qw.group_size, qw.K, qw.N
+
+    @classmethod
+    def from_linear(cls, linear: torch.nn.Linear, group_size: int = 128) -> "QuantLinear":
+        # nn.Linear stores [out, in]; the kernels consume [in, out].
+        qw = quantize(linear.weight.data.t().contiguous(), group_size)
+        bias = linear.bias.data.clone() if linear.bias is not None else None
+        return cls(qw.to(linear.weight.device), bias)
+
+    def _qw(self) -> QuantizedWeight:
+        return QuantizedWeight(self.qweight, self.scales, self.group_size, self.K, self.N)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        shape = x.shape
+        y = matmul(x.reshape(-1, shape[-1]).contiguous(), self._qw())
+        y = y.reshape(*shape[:-1], self.N)
+        return y + self.bias if self.bias is not None else y

@@ -1,0 +1,142 @@
+"""Packed INT4 weight format: quantiser, packer and host-side decode.
+
+Drop-in for ``python/nibblegemm/quant.py`` of arvindcr4/nibblegemm: same names,
+same array shapes and dtypes, same errors.
+
+Format (reference quant.py:8-54)
+--------------------------------
+``W`` is ``[K, N]`` and consumed as ``Y = X @ W`` (K is the reduction axis).
+
+* Groups of ``group_size`` rows along K share one fp16 scale per column.
+* Symmetric INT4: ``q = clamp(round_half_even(w / scale), -8, 7)``, stored as
+  ``q + 8`` in ``[0, 15]``; there is no zero-point tensor.
+* ``scale = max(max|w| / 7, 1e-8)`` per group and column (plain max-abs).
+* Eight nibbles along K share one 32-bit word: ``qweight`` is int32
+  ``[K // 8, N]``.  Logical offset ``k`` of a word lives in nibble slot
+  ``SLOT_FOR_K[k] = [0, 4, 1, 5, 2, 6, 3, 7]`` (even k in slots 0..3, odd k in
+  slots 4..7), the order in which the kernels' mask-and-or decode emits fp16
+  pairs in ascending k.
+
+Host code only: packing happens at quantisation time, ``dequantize`` and
+``reference_matmul`` reproduce the reference's definitions for callers' own
+checks.  The kernel entry points in :mod:`nibblegemm_amd.ops` never call them.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+#: ``SLOT_FOR_K[k]`` is the nibble slot that stores logical offset ``k`` (0..7).
+SLOT_FOR_K = np.array([0, 4, 1, 5, 2, 6, 3, 7], dtype=np.int64)
+#: Inverse permutation: ``K_FOR_SLOT[s]`` is the logical offset held by slot ``s``.
+K_FOR_SLOT = np.argsort(SLOT_FOR_K)
+
+QMIN, QMAX = -8, 7
+ZERO_POINT = 8
+PACK_FACTOR = 8
+
+
+@dataclass(frozen=True)
+class QuantizedWeight:
+    """Packed INT4 weights plus their fp16 group scales (reference quant.py:60-78)."""
+
+    qweight: torch.Tensor  # int32 [K // 8, N], nibble-interleaved
+    scales: torch.Tensor  # fp16  [K // G, N]
+    group_size: int
+    K: int
+    N: int
+
+    def to(self, device) -> "QuantizedWeight":
+        return QuantizedWeight(
+            self.qweight.to(device), self.scales.to(device), self.group_size, self.K, self.N
+        )
+
+    @property
+    def weight_bytes(self) -> int:
+        """Bytes of weight traffic a perfect kernel must read (packed + scales)."""
+        return self.qweight.numel() * 4 + self.scales.numel() * 2
+
+
+def quantize(W: torch.Tensor, group_size: int = 128, clip_search: bool = False) -> QuantizedWeight:
+    """Round-to-nearest quantise a ``[K, N]`` weight to packed group-wise INT4.
+
+    Reference quant.py:127-161.  ``clip_search`` (the reference's MSE clipping
+    search, off by default there and documented as lowering model quality) is
+    not provided; asking for it raises ``NotImplementedError``.
+    """
+    if clip_search:
+        raise NotImplementedError("clip_search is not provided by nibblegemm_amd")
+    if W.ndim != 2:
+        raise ValueError(f"expected a 2-D weight, got shape {tuple(W.shape)}")
+    K, N = W.shape
+    if K % group_size:
+        raise ValueError(f"K={K} must be divisible by group_size={group_size}")
+    if group_size % PACK_FACTOR:
+        raise ValueError(f"group_size={group_size} must be divisible by {PACK_FACTOR}")
+
+    w = W.detach().float()
+    groups = w.reshape(K // group_size, group_size, N)
+    # Clamp away exact zeros so all-zero groups stay finite.
+    scale = (groups.abs().amax(dim=1) / QMAX).clamp(min=1e-8)
+    q = torch.round(groups / scale.unsqueeze(1)).clamp(QMIN, QMAX)
+    qu = (q + ZERO_POINT).reshape(K, N).to(torch.uint8).cpu().numpy()
+
+    return QuantizedWeight(
+        qweight=torch.from_numpy(pack_nibbles(qu)),
+        scales=scale.to(torch.float16).cpu().contiguous(),
+        group_size=group_size,
+        K=K,
+        N=N,
+    )
+
+
+def pack_nibbles(qu: np.ndarray) -> np.ndarray:
+    """Pack ``uint8 [K, N]`` values in ``[0, 15]`` into ``int32 [K // 8, N]``.
+
+    Works in uint32 so the top nibble cannot trip signed overflow, then views
+    the result as int32 (the dtype the kernels take).  Reference quant.py:164-182.
+    """
+    qu = np.asarray(qu)
+    K, N = qu.shape
+    if K % PACK_FACTOR:
+        raise ValueError(f"K={K} must be divisible by {PACK_FACTOR}")
+    if qu.max(initial=0) > 15:
+        raise ValueError("quantised values must fit in 4 bits")
+
+    blocks = qu.reshape(K // PACK_FACTOR, PACK_FACTOR, N).astype(np.uint32)
+    packed = np.zeros((K // PACK_FACTOR, N), dtype=np.uint32)
+    for k_off in range(PACK_FACTOR):
+        packed |= (blocks[:, k_off, :] & np.uint32(0xF)) << np.uint32(4 * int(SLOT_FOR_K[k_off]))
+    return packed.view(np.int32)
+
+
+def unpack_nibbles(packed: np.ndarray, K: int) -> np.ndarray:
+    """Inverse of :func:`pack_nibbles`; returns ``uint8 [K, N]`` in ``[0, 15]``
+    (reference quant.py:185-196)."""
+    p = np.ascontiguousarray(packed).view(np.uint32)
+    rows, N = p.shape
+    if rows * PACK_FACTOR != K:
+        raise ValueError(f"packed rows={rows} inconsistent with K={K}")
+    out = np.empty((rows, PACK_FACTOR, N), dtype=np.uint8)
+    for k_off in range(PACK_FACTOR):
+        out[:, k_off, :] = ((p >> np.uint32(4 * int(SLOT_FOR_K[k_off]))) & np.uint32(0xF)).astype(np.uint8)
+    return out.reshape(K, N)
+
+
+def dequantize(qw: QuantizedWeight) -> torch.Tensor:
+    """The ``[K, N]`` fp16 weight the kernels model, on the host:
+    ``fp16((nibble - 8) * fp32(scale))`` (reference quant.py:199-204).
+    The device kernel for the same result is :func:`nibblegemm_amd.ops.dequant`."""
+    qu = unpack_nibbles(qw.qweight.cpu().numpy(), qw.K)
+    q = torch.from_numpy(qu.astype(np.int16)).float() - ZERO_POINT
+    scale = qw.scales.float().cpu().repeat_interleave(qw.group_size, dim=0)
+    return (q * scale).to(torch.float16)
+
+
+def reference_matmul(X: torch.Tensor, qw: QuantizedWeight) -> torch.Tensor:
+    """fp32-accumulated ``X @ dequantize(qw)`` rounded to fp16, on X's device
+    (reference quant.py:207-215)."""
+    W = dequantize(qw).to(X.device).float()
+    return (X.float() @ W).to(torch.float16)

@@ -1,0 +1,187 @@
+"""The C-ABI library: it loads, exports what include/nibblegemm_amd.h declares,
+and rejects every argument the reference's host checks reject -- all before
+any HIP call, so this runs on a machine without a GPU.
+
+The pointer values passed here are never dereferenced: every call either
+fails validation (which happens before any HIP call) or is the M > 8 case that
+the launcher refuses before touching the device.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+import nibblegemm_amd as ng
+from nibblegemm_amd import _native
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "nibblegemm_amd.h")
+
+OK, INVALID, UNSUPPORTED, WORKSPACE, HIP = 0, 1, 2, 3, 4
+P = 1 << 20  # aligned, never dereferenced
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    return re.findall(r"NIBBLE_API\s+[\w\s\*]+?\b(nibble_\w+)\s*\(", text)
+
+
+def test_header_declares_the_entry_points():
+    names = set(declared_functions())
+    assert {"nibble_abi_version", "nibble_last_error", "nibble_gemv_w4a16",
+            "nibble_gemv_workspace_bytes", "nibble_gemv_counter_bytes", "nibble_gemm_w4a16",
+            "nibble_dequant_w4"} <= names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(_native.LIBRARY_PATH)
+    for name in declared_functions():
+        assert hasattr(lib, name), f"{name} not exported"
+    lib.nibble_abi_version.restype = ctypes.c_int
+    version = int(re.search(r"#define NIBBLE_ABI_VERSION (\d+)", open(HEADER).read()).group(1))
+    assert lib.nibble_abi_version() == version
+
+
+def test_binding_loads_and_matches_abi():
+    ext = ng.extension()
+    assert ext.abi_version() == _native.ABI_VERSION
+
+
+def gemv(ext, M, K, N, g=128, wq_rows=None, s_rows=None, s_cols=None, version=4, splits=0,
+         threads=0, ptr=P):
+    wq_rows = K // 8 if wq_rows is None else wq_rows
+    s_rows = (K // g if g else 0) if s_rows is None else s_rows
+    s_cols = N if s_cols is None else s_cols
+    return ext.gemv(ptr, M, K, ptr, wq_rows, N, ptr, s_rows, s_cols, g, version, splits, threads,
+                    ptr, None, 0, None)
+
+
+@pytest.mark.parametrize("kwargs,needle", [
+    (dict(M=1, K=256, N=128, wq_rows=31), "packed weight rows"),
+    (dict(M=1, K=256, N=128, s_rows=3), "scale rows"),
+    (dict(M=1, K=256, N=128, s_cols=132), "scale columns"),
+    (dict(M=1, K=256, N=130), "multiple of 4"),
+    (dict(M=1, K=256, N=128, g=32, s_rows=8), "group_size"),
+    (dict(M=1, K=256, N=128, version=5), "version"),
+    (dict(M=1, K=256, N=128, ptr=P + 2), "misaligned"),
+    (dict(M=1, K=256, N=128, ptr=0), "null"),
+])
+def test_gemv_rejections(kwargs, needle):
+    ext = ng.extension()
+    rc = gemv(ext, **kwargs)
+    assert rc == INVALID
+    assert needle in ext.last_error()
+
+
+@pytest.mark.parametrize("version", [3, 4])
+def test_gemv_rejects_m_above_8(version):
+    ext = ng.extension()
+    assert gemv(ext, 9, 256, 132, version=version) == UNSUPPORTED
+    assert "M <= 8" in ext.last_error()
+
+
+def test_gemv_threads_override_validated():
+    ext = ng.extension()
+    assert gemv(ext, 1, 256, 128, threads=96) == INVALID
+    assert "block_threads" in ext.last_error()
+
+
+def test_gemv_workspace_formula():
+    ext = ng.extension()
+    # 1024 / 64 = 16 groups split 16 ways over one 256-column slab:
+    # 256 bytes of counters (padded), then 16 x M x N fp32 partials.
+    ws, counters = ext.gemv_workspace_bytes(1, 1024, 256, 64, 4, 16, 0, None)
+    assert counters == 256
+    assert ws == 256 + 16 * 1 * 256 * 4
+    # floor-then-trim: 32 groups asked for 27 splits -> 1 group each -> 32 splits
+    ws, counters = ext.gemv_workspace_bytes(2, 4096, 512, 128, 4, 27, 0, None)
+    assert counters == 256 and ws == 256 + 32 * 2 * 512 * 4
+    # a single split needs no workspace
+    assert ext.gemv_workspace_bytes(1, 1024, 256, 64, 4, 1, 0, None) == (0, 0)
+    assert ext.gemv_workspace_bytes(1, 1024, 256, 64, 3, 0, 0, None) == (0, 0)
+    # invalid requests report zero
+    assert ext.gemv_workspace_bytes(9, 1024, 256, 64, 4, 4, 0, None) == (0, 0)
+    assert ext.gemv_workspace_bytes(1, 1024, 256, 32, 4, 4, 0, None) == (0, 0)
+
+
+def gemm(ext, M, K, N, g=128, wq_rows=None, s_rows=None, s_cols=None, version=6, ptr=P):
+    wq_rows = K // 8 if wq_rows is None else wq_rows
+    s_rows = K // g if s_rows is None else s_rows
+    s_cols = N if s_cols is None else s_cols
+    return ext.gemm(ptr, M, K, ptr, wq_rows, N, ptr, s_rows, s_cols, g, version, ptr, None)
+
+
+@pytest.mark.parametrize("kwargs,needle", [
+    (dict(M=16, K=256, N=128, wq_rows=31), "packed weight rows"),
+    (dict(M=16, K=264, N=128, g=8, s_rows=33), "multiple of 32"),
+    (dict(M=16, K=256, N=127), "even"),
+    (dict(M=16, K=256, N=128, g=32, s_rows=8), "group_size"),
+    (dict(M=16, K=256, N=128, s_rows=1), "scale rows"),
+    (dict(M=16, K=256, N=128, s_cols=130), "scale columns"),
+    (dict(M=16, K=256, N=128, version=5), "version"),
+    (dict(M=1 << 20, K=4096, N=1024), "32-bit indexing"),
+    (dict(M=16, K=256, N=128, ptr=P + 8), "misaligned"),
+])
+def test_gemm_rejections(kwargs, needle):
+    ext = ng.extension()
+    assert gemm(ext, **kwargs) == INVALID
+    assert needle in ext.last_error()
+
+
+@pytest.mark.parametrize("args,needle", [
+    ((P, 32, 128, P, 3, 128, 128), "scale rows"),
+    ((P, 32, 128, P, 2, 132, 128), "scale columns"),
+    ((P, 32, 128, P, 2, 128, 100), "group_size"),
+    ((P, 32, 128, P, 1, 128, 192), "divisible"),
+    ((0, 32, 128, P, 2, 128, 128), "null"),
+])
+def test_dequant_rejections(args, needle):
+    ext = ng.extension()
+    wq, rows, n, s, sr, sc, g = args
+    assert ext.dequant(wq, rows, n, s, sr, sc, g, 1, P, None) == INVALID
+    assert needle in ext.last_error()
+
+
+def test_binding_rejects_wrong_arity():
+    ext = ng.extension()
+    with pytest.raises(TypeError):
+        ext.gemv(1, 2, 3)
+
+
+# --------------------------------------------------------------------------
+# Python layer: errors raised before any device work
+# --------------------------------------------------------------------------
+def _cpu_case(M=1, K=256, N=128, g=128):
+    qw = ng.quantize(torch.randn(K, N) * 0.02, group_size=g)
+    X = torch.randn(M, K).half()
+    return X, qw
+
+
+def test_matmul_rejects_k_mismatch_and_rank():
+    X, qw = _cpu_case()
+    with pytest.raises(ValueError):
+        ng.matmul(torch.randn(1, 128).half(), qw)
+    with pytest.raises(ValueError):
+        ng.matmul(X.reshape(1, 1, 256), qw)
+
+
+def test_kernels_refuse_host_tensors():
+    X, qw = _cpu_case()
+    with pytest.raises(RuntimeError, match="GPU"):
+        ng.gemv(X, qw)
+    with pytest.raises(RuntimeError, match="GPU"):
+        ng.gemm(X, qw)
+    with pytest.raises(RuntimeError, match="GPU"):
+        ng.dequant(qw)
+
+
+def test_library_loads_only_one_hip_runtime():
+    """The library resolves libamdhip64 to the runtime torch already loaded."""
+    ng.extension()
+    maps = [l for l in open("/proc/self/maps") if "libamdhip64" in l]
+    paths = {l.split()[-1] for l in maps}
+    assert len(paths) <= 1, paths

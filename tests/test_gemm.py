@@ -1,0 +1,119 @@
+"""Parity of the MFMA prefill GEMM with the reference path.
+
+Edge cases follow the reference's tests/test_gemm.py (M on, just past and far
+past tile boundaries; N with masked columns), then the BASELINE prefill and
+handover configs at full size -- checked on sampled rows, since the CPU oracle
+cannot do 2048 x 4096 x 14336 in seconds.
+
+Bounds: north-star ``max|y - ref| <= 1e-2 * rms(ref)`` and the reference's
+``max|y - ref| / mean|ref| < 3e-2`` (tests/test_gemm.py:34 there).  The LDS B
+tile holds exactly the oracle's dequantized fp16 values and MFMA accumulates
+in fp32, so only summation order and the final fp16 rounding differ.
+"""
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import nibblegemm_amd as ng
+from cases import host, oracle_y, oracle_y_rows, quantized, rel_err, rms_err, synthetic, to_dev_qw
+
+pytestmark = pytest.mark.gpu
+
+RMS_TOL = 1e-2
+REL_TOL = 3e-2
+K = 256
+M_VALUES = [1, 17, 64, 65, 128, 1000]
+N_VALUES = [128, 132]
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "w4a16_golden.npz")
+
+
+@pytest.mark.parametrize("version", [6, 7])
+@pytest.mark.parametrize("M", M_VALUES)
+@pytest.mark.parametrize("N", N_VALUES)
+@pytest.mark.parametrize("group_size", [64, 128])
+def test_gemm_matches_reference(version, M, N, group_size):
+    X, packed, scales, Xd, qw = quantized(M, K, N, group_size)
+    y = ng.gemm(Xd, qw, version=version)
+    assert y.shape == (M, N) and y.dtype == torch.float16
+    ref = oracle_y(X, packed, scales, K, group_size)
+    assert rms_err(host(y), ref) <= RMS_TOL
+    assert rel_err(host(y), ref) < REL_TOL
+
+
+@pytest.mark.parametrize("M", [16, 64, 512])
+def test_matmul_dispatches_to_gemm_above_the_crossover(M):
+    _, _, _, Xd, qw = quantized(M, K, 128, 128, seed=1)
+    assert M > ng.DECODE_MAX_M
+    assert torch.equal(ng.matmul(Xd, qw), ng.gemm(Xd, qw))
+
+
+@pytest.mark.parametrize("M", [9, 33, 200])
+@pytest.mark.parametrize("K_,N", [(512, 130), (1024, 4102), (192, 64)])
+def test_gemm_odd_shapes(M, K_, N):
+    g = 64 if K_ % 128 else 128
+    X, packed, scales, Xd, qw = synthetic(M, K_, N, g, seed=M + N)
+    ref = oracle_y(X, packed, scales, K_, g)
+    for version in (6, 7):
+        assert rms_err(host(ng.gemm(Xd, qw, version=version)), ref) <= RMS_TOL
+
+
+def test_versions_agree():
+    _, _, _, Xd, qw = synthetic(300, 1024, 640, 128, seed=3)
+    a, b = host(ng.gemm(Xd, qw, version=6)), host(ng.gemm(Xd, qw, version=7))
+    assert rel_err(a, b) < REL_TOL
+
+
+@pytest.mark.parametrize("M", [16, 32])
+def test_small_batch_config_gemm_leg(M):
+    """BASELINE config 3 at M > 8 (the MFMA side of the handover), full size."""
+    X, packed, scales, Xd, qw = synthetic(M, 4096, 14336, 128, seed=200 + M)
+    y = host(ng.matmul(Xd, qw))
+    assert rms_err(y, oracle_y(X, packed, scales, 4096, 128)) <= RMS_TOL
+
+
+@pytest.mark.parametrize("M", [128, 512, 2048])
+@pytest.mark.parametrize("K_,N", [(4096, 14336), (14336, 4096)])
+def test_prefill_configs_sampled_rows(M, K_, N):
+    """BASELINE config 4 at full size; the oracle checks 12 sampled rows
+    (first, last, both sides of every 128-row tile edge it hits, random)."""
+    X, packed, scales, Xd, qw = synthetic(M, K_, N, 128, seed=300 + M + N)
+    y = host(ng.gemm(Xd, qw))
+    rng = np.random.default_rng(M)
+    rows = sorted(set([0, 1, 127, M - 1] + [int(r) for r in rng.integers(0, M, size=8)]))
+    rows = [r for r in rows if r < M]
+    ref = oracle_y_rows(X, rows, packed, scales, K_, 128)
+    assert rms_err(y[rows], ref) <= RMS_TOL
+    assert np.all(np.isfinite(y))
+
+
+def test_gemm_is_deterministic():
+    _, _, _, Xd, qw = synthetic(257, 2048, 1024, 128, seed=5)
+    a = ng.gemm(Xd, qw)
+    b = ng.gemm(Xd, qw)
+    assert torch.equal(a, b)
+
+
+def test_golden_vectors():
+    z = np.load(GOLDEN)
+    for name in sorted({k.split("/")[0] for k in z.files if not k.startswith("sweep")}):
+        M, K_, N, g, _ = z[f"{name}/meta"].tolist()
+        qw = to_dev_qw(z[f"{name}/qweight"], z[f"{name}/scales"], K_, N, g)
+        X = torch.from_numpy(z[f"{name}/X"].view(np.float16).copy()).cuda()
+        ref = z[f"{name}/Y"].view(np.float16).astype(np.float32)
+        for version in (6, 7):
+            assert rms_err(host(ng.gemm(X, qw, version=version)), ref) <= RMS_TOL, (name, version)
+
+
+def test_empty_batch():
+    _, _, _, Xd, qw = quantized(4, 256, 128, 128, seed=8)
+    assert ng.gemm(Xd[:0], qw).shape == (0, 128)
+
+
+def test_gemm_rejects_bad_version():
+    _, _, _, Xd, qw = quantized(16, 256, 128, 128, seed=9)
+    with pytest.raises(RuntimeError):
+        ng.gemm(Xd, qw, version=5)

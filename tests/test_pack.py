@@ -1,0 +1,86 @@
+"""On-disk nibble format of the package (reference tests/test_pack.py intents).
+
+CPU only: pins the layout every kernel decodes.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import nibblegemm_amd as ng
+from nibblegemm_amd.quant import PACK_FACTOR, SLOT_FOR_K
+
+EXPECTED_SLOT_FOR_K = [0, 4, 1, 5, 2, 6, 3, 7]
+
+
+def test_slot_table_is_the_documented_permutation():
+    assert list(SLOT_FOR_K) == EXPECTED_SLOT_FOR_K
+    assert list(ng.quant.K_FOR_SLOT) == [0, 2, 4, 6, 1, 3, 5, 7]
+
+
+def test_nibble_slot_assignment_is_pinned():
+    qu = np.arange(PACK_FACTOR, dtype=np.uint8).reshape(PACK_FACTOR, 1)
+    word = int(ng.pack_nibbles(qu).view(np.uint32)[0, 0])
+    for k, slot in enumerate(EXPECTED_SLOT_FOR_K):
+        assert (word >> (4 * slot)) & 0xF == k
+    assert word == 0x75316420
+
+
+@pytest.mark.parametrize("shape", [(8, 1), (8, 4), (256, 64), (128, 130), (1024, 3), (2048, 1)])
+def test_pack_unpack_is_an_involution(shape):
+    K, N = shape
+    qu = np.random.default_rng(K * 31 + N).integers(0, 16, size=shape, dtype=np.uint8)
+    packed = ng.pack_nibbles(qu)
+    assert packed.dtype == np.int32
+    assert packed.shape == (K // PACK_FACTOR, N)
+    assert np.array_equal(ng.unpack_nibbles(packed, K), qu)
+
+
+def test_top_nibble_sets_the_sign_bit():
+    qu = np.zeros((8, 1), np.uint8)
+    qu[7, 0] = 15  # k = 7 lives in slot 7, bits 28..31
+    assert int(ng.pack_nibbles(qu)[0, 0]) == -(1 << 31) + (7 << 28)
+
+
+def test_pack_rejects_values_above_15():
+    qu = np.zeros((8, 4), dtype=np.uint8)
+    qu[5, 2] = 16
+    with pytest.raises(ValueError):
+        ng.pack_nibbles(qu)
+
+
+def test_pack_rejects_k_not_divisible_by_8():
+    with pytest.raises(ValueError):
+        ng.pack_nibbles(np.zeros((12, 4), dtype=np.uint8))
+
+
+def test_unpack_rejects_inconsistent_k():
+    packed = ng.pack_nibbles(np.zeros((16, 4), dtype=np.uint8))
+    with pytest.raises(ValueError):
+        ng.unpack_nibbles(packed, 24)
+
+
+@pytest.mark.parametrize("K,group_size", [(192, 128), (100, 64), (8, 128), (130, 128)])
+def test_quantize_rejects_k_not_divisible_by_group(K, group_size):
+    with pytest.raises(ValueError):
+        ng.quantize(torch.randn(K, 8), group_size=group_size)
+
+
+def test_quantize_rejects_non_2d_weight():
+    with pytest.raises(ValueError):
+        ng.quantize(torch.randn(4, 128, 8), group_size=128)
+
+
+def test_quantize_rejects_group_not_multiple_of_8():
+    with pytest.raises(ValueError):
+        ng.quantize(torch.randn(120, 8), group_size=12)
+
+
+def test_quantized_weight_bytes_and_to():
+    qw = ng.quantize(torch.randn(256, 16) * 0.02, group_size=128)
+    assert qw.qweight.shape == (32, 16) and qw.qweight.dtype == torch.int32
+    assert qw.scales.shape == (2, 16) and qw.scales.dtype == torch.float16
+    assert qw.weight_bytes == 32 * 16 * 4 + 2 * 16 * 2
+    qw2 = qw.to("cpu")
+    assert torch.equal(qw2.qweight, qw.qweight) and (qw2.K, qw2.N, qw2.group_size) == (256, 16, 128)
