@@ -95,9 +95,9 @@ NIBBLE_API int nibble_gemv_w4a16(const void* X, int64_t x_rows, int64_t x_cols,
                       int64_t threads_override, void* Y, void* workspace,
                       size_t workspace_bytes, void* stream);
 
-/* Bytes of workspace nibble_gemv_w4a16 needs for these arguments (0 if none).
- * Uses the device's CU count for the split heuristic, so it may make one HIP
- * attribute query; returns 0 for arguments the launcher would reject. */
+/* Bytes of workspace nibble_gemv_w4a16 needs for these arguments (0 if none,
+ * and 0 for arguments the launcher would reject).  Pure host computation:
+ * `stream` is accepted for symmetry with the launcher and is not used. */
 NIBBLE_API size_t nibble_gemv_workspace_bytes(int64_t M, int64_t K, int64_t N, int64_t group_size,
                                    int64_t version, int64_t splits_override,
                                    int64_t threads_override, void* stream);

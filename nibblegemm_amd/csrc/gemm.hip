@@ -185,11 +185,17 @@ int validate_gemm(const void* X, int64_t x_rows, int64_t x_cols, const void* Wq,
   NIBBLE_CHECK(M * N < lim && M * K < lim && K * N < lim,
                "shape too large for 32-bit indexing in the prefill kernel");
   NIBBLE_CHECK(ceil_div(M, 64) < 65536, "M too large");
-  if (M > 0 && N > 0) {
-    NIBBLE_CHECK(X != nullptr && Wq != nullptr && S != nullptr && Y != nullptr, "null pointer");
-    NIBBLE_CHECK(aligned(X, 16) && aligned(Wq, 4) && aligned(S, 2) && aligned(Y, 2),
-                 "misaligned pointer (X needs 16-byte alignment)");
-  }
+  // Only operands that hold elements are dereferenced (empty tensors may
+  // carry a null data pointer).
+  const bool x_used = M * K > 0 && N > 0;
+  const bool w_used = K * N > 0 && M > 0;
+  const bool y_used = M * N > 0;
+  NIBBLE_CHECK((!x_used || X != nullptr) && (!w_used || (Wq != nullptr && S != nullptr)) &&
+                   (!y_used || Y != nullptr),
+               "null pointer");
+  NIBBLE_CHECK((!x_used || aligned(X, 16)) && (!w_used || (aligned(Wq, 4) && aligned(S, 2))) &&
+                   (!y_used || aligned(Y, 2)),
+               "misaligned pointer (X needs 16-byte alignment)");
   return NIBBLE_OK;
 }
 

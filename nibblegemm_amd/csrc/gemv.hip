@@ -2,24 +2,34 @@
 //
 // Reference: csrc/gemv_w4a16.cu (kernels v0-v4 :30-244, host :251-425).
 //
-// The streaming kernel (versions 2, 3, 4) is one launch:
+// The streaming kernel (versions 2, 3, 4) runs the dot products on CDNA4
+// matrix cores (v_mfma_f32_16x16x32_f16) and is one launch:
 //
-//  * Workgroup = WAVES wave64s over one 256-column slab (each lane owns 4
-//    adjacent columns, i.e. one 16-byte word quad per packed row, so a wave
-//    reads 1 KiB contiguous per row) and one K split of whole quant groups.
-//  * Wave w of the workgroup takes groups gb+w, gb+w+WAVES, ... of its split.
-//    Per group it issues all GROUP/8 dwordx4 buffer loads up front (SGPR row
-//    offsets, no per-load VALU address math), then decodes each word with the
-//    0x6400 magic-exponent trick (v_and_or_b32) and accumulates x*w with
-//    v_dot2_f32_f16 into fp32 group sums.  X is wave-uniform and is read with
-//    scalar loads.  The group scale multiplies the fp32 group sum.
-//  * Waves are reduced through LDS in wave order.  With one split the
-//    workgroup writes fp16 Y directly.  With several, each workgroup writes an
-//    fp32 partial [split, M, N], and the last workgroup of each slab to finish
-//    (agent-scope counter) sums the partials in split order and writes Y --
-//    deterministic, and no second launch (the reference ran reduce_splits as a
-//    separate kernel, :237-244, :418-423).  That workgroup resets the counter
-//    to zero, so the counter region stays zero between calls.
+//  * A workgroup owns a 64-column strip and one K split (whole quant groups);
+//    its WAVES waves take the split's groups round-robin.  Per 32-k chunk a
+//    lane issues one dwordx4 buffer load: 4 adjacent columns of one packed
+//    row, so a wave reads 4 rows x 256 contiguous bytes.  Lane l's word for
+//    column 4*(l%16)+j is exactly the B operand of MFMA j in B-column slot
+//    l%16 and k block l/16 -- no shuffles.
+//  * Each word is decoded with the 0x6400 magic-exponent trick, one
+//    v_and_or_b32 per half2 (1024 + n or 1024 + 16n, see decode8_biased).  The
+//    bias and the 1/16 are not removed per weight: activations are pre-scaled
+//    (x/16 at k % 8 in {2,3,6,7}) and one extra MFMA per chunk against a
+//    constant correction adds -1032 / -1152 times the activations, which is
+//    the same for every column.  5 VALU ops per packed word, whatever M is.
+//  * Row m of the MFMA A operand is activation row m (rows >= M read as
+//    zero), so M = 1..8 costs the same matrix-core work as M = 1.
+//  * Per quant group the fp32 MFMA tile is scaled by the column's fp16 scale
+//    into fp32 totals; loads of the next group are in flight meanwhile
+//    (double-buffered registers).
+//  * Waves are summed through LDS in wave order.  With one split the
+//    workgroup writes fp16 Y directly.  With several, each workgroup writes
+//    an fp32 partial [split, M, N] with device-coherent stores, and the last
+//    workgroup of the strip (agent-scope counter) sums the partials in split
+//    order and writes Y -- deterministic, and no second launch (the reference
+//    ran reduce_splits as a separate kernel, :237-244, :418-423).  That
+//    workgroup resets the counter, so the counter region stays zero between
+//    calls.
 //
 // Versions 0 and 1 are scalar fp32 kernels, one thread per output (the
 // reference's v0/v1, :30-72): an on-device reference, not a fast path.
@@ -32,7 +42,7 @@ namespace nibble {
 
 namespace {
 
-constexpr int kSlabCols = 256;  // 64 lanes x 4 columns
+constexpr int kStripCols = 64;  // 16 lanes x 4 columns
 
 struct GemvArgs {
   const _Float16* X;
@@ -40,139 +50,187 @@ struct GemvArgs {
   const _Float16* S;
   _Float16* Y;
   float* partial;      // [splits, M, N] fp32, used when splits > 1
-  uint32_t* counters;  // [slabs], zero on entry and on exit
+  uint32_t* counters;  // [strips], zero on entry and on exit
   int M, K, N;
   int groups_per_split;
   int splits;
 };
 
+__device__ __forceinline__ f4_t mfma16(h8_t a, h8_t b, f4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
 template <int MT, int GROUP, int WAVES>
-__global__ __launch_bounds__(WAVES * 64) void gemv_stream_kernel(GemvArgs a) {
-  constexpr int WORDS = GROUP / 8;  // packed rows per quant group
-  __shared__ f4_t red[WAVES][MT][64];
+__global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs a) {
+  constexpr int CPG = GROUP / 32;              // 32-k chunks per quant group
+  constexpr int LANE_ROWS = MT < 4 ? MT : 4;   // output rows a lane can hold
+  __shared__ f4_t red[WAVES][MT][16];          // [wave][row][column quad]
   __shared__ int s_last;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int slab = blockIdx.x;
+  const int strip = blockIdx.x;
   const int split = blockIdx.y;
-  const int n0 = slab * kSlabCols + lane * 4;
-  const bool active = n0 < a.N;
+  const int q = lane & 15;   // B column slot (column quad) and A row
+  const int kb = lane >> 4;  // 8-k block within a 32-k chunk
+  const int col = strip * kStripCols + 4 * q;
+  const bool col_ok = col < a.N;
+  const uint32_t row_bytes = static_cast<uint32_t>(a.N) * 4u;
+
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.Wq, static_cast<uint32_t>(a.K / 8) * row_bytes);
+  const __amdgpu_buffer_rsrc_t rx =
+      make_rsrc(a.X, static_cast<uint32_t>(a.M) * static_cast<uint32_t>(a.K) * 2u);
+  const __amdgpu_buffer_rsrc_t rs =
+      make_rsrc(a.S, static_cast<uint32_t>(a.K / GROUP) * static_cast<uint32_t>(a.N) * 2u);
+  const uint32_t voff_w = col_ok ? kb * row_bytes + static_cast<uint32_t>(col) * 4u : kOutOfRange;
+  const uint32_t voff_x =
+      q < a.M ? (static_cast<uint32_t>(q) * a.K + 8u * kb) * 2u : kOutOfRange;
+  const uint32_t voff_s = col_ok ? static_cast<uint32_t>(col) * 2u : kOutOfRange;
+
+  struct Stage {
+    h8_t x[CPG];
+    h4_t s;
+    u4_t w[CPG];
+  };
+  // Loads of group g.  A prefetch past the split re-reads the split's last
+  // group (just loaded, so an L2 hit) instead of being predicated off: the
+  // loads stay unconditional and identical on every path, which lets the
+  // compiler keep exact in-order wait counts across the loop back-edge
+  // (a per-lane "disabled" offset made it drain every load at the top of
+  // each iteration).
   const int total_groups = a.K / GROUP;
   const int gb = split * a.groups_per_split;
   const int ge = min(gb + a.groups_per_split, total_groups);
-  const uint32_t row_bytes = static_cast<uint32_t>(a.N) * 4u;
-  // Inactive lanes (past N in the last slab) point outside the buffer
-  // resource, so their loads return zero without touching memory.
-  const uint32_t voff = active ? static_cast<uint32_t>(n0) * 4u : 0x80000000u;
+  auto load = [&](Stage& st, int g, bool enabled) {
+    g = enabled ? g : ge - 1;
+    const uint32_t vx = voff_x, vs = voff_s, vw = voff_w;
+    const uint32_t kx = static_cast<uint32_t>(g) * GROUP * 2u;
+    const uint32_t kw = static_cast<uint32_t>(g) * (GROUP / 8) * row_bytes;
+#pragma unroll
+    for (int c = 0; c < CPG; ++c)
+      st.x[c] = __builtin_bit_cast(h8_t, __builtin_amdgcn_raw_buffer_load_b128(rx, vx, kx + c * 64, 0));
+    st.s = __builtin_bit_cast(
+        h4_t, __builtin_amdgcn_raw_buffer_load_b64(rs, vs, static_cast<uint32_t>(g) * a.N * 2u, 0));
+#pragma unroll
+    for (int c = 0; c < CPG; ++c)
+      st.w[c] = __builtin_bit_cast(
+          u4_t, __builtin_amdgcn_raw_buffer_load_b128(rw, vw, kw + c * 4 * row_bytes, 0));
+  };
 
-  float acc[MT][4];
+  f4_t tot[4];
 #pragma unroll
-  for (int m = 0; m < MT; ++m)
-#pragma unroll
-    for (int c = 0; c < 4; ++c) acc[m][c] = 0.0f;
+  for (int j = 0; j < 4; ++j) tot[j] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-  for (int g = gb + wave; g < ge; g += WAVES) {
-    const uint32_t* gbase = a.Wq + static_cast<size_t>(g) * WORDS * a.N;
-    const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(gbase, WORDS * row_bytes);
-    u4_t w[WORDS];
+  const DecodeConsts dk = decode_consts();
+  const h8_t xscale = biased_x_scale();
+  const h8_t bcorr = biased_correction();
+  auto compute = [&](const Stage& st) {
+    h8_t xs[CPG];
 #pragma unroll
-    for (int j = 0; j < WORDS; ++j)
-      w[j] = __builtin_bit_cast(
-          u4_t, __builtin_amdgcn_raw_buffer_load_b128(rsrc, voff, j * row_bytes, 0));
-
-    h4_t sc = {0, 0, 0, 0};
-    if (active) sc = *reinterpret_cast<const h4_t*>(a.S + static_cast<size_t>(g) * a.N + n0);
-
-    float gs[MT][4];
+    for (int c = 0; c < CPG; ++c) xs[c] = st.x[c] * xscale;
+    f4_t corr = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int m = 0; m < MT; ++m)
+    for (int c = 0; c < CPG; ++c) corr = mfma16(xs[c], bcorr, corr);
+    f4_t acc[4];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) gs[m][c] = 0.0f;
-
+    for (int j = 0; j < 4; ++j) acc[j] = corr;
 #pragma unroll
-    for (int j = 0; j < WORDS; ++j) {
-      h2_t d[4][4];
+    for (int c = 0; c < CPG; ++c)
 #pragma unroll
-      for (int c = 0; c < 4; ++c) decode8(w[j][c], d[c]);
+      for (int j = 0; j < 4; ++j) acc[j] = mfma16(xs[c], decode8_biased(st.w[c][j], dk), acc[j]);
 #pragma unroll
-      for (int m = 0; m < MT; ++m) {
-        if (m < a.M) {
-          const h8_t xv = *reinterpret_cast<const h8_t*>(a.X + static_cast<size_t>(m) * a.K +
-                                                         g * GROUP + j * 8);
-          const h2_t xp[4] = {{xv[0], xv[1]}, {xv[2], xv[3]}, {xv[4], xv[5]}, {xv[6], xv[7]}};
+    for (int j = 0; j < 4; ++j) {
+      const float sj = static_cast<float>(st.s[j]);
 #pragma unroll
-          for (int c = 0; c < 4; ++c)
-#pragma unroll
-            for (int t = 0; t < 4; ++t)
-              gs[m][c] = __builtin_amdgcn_fdot2(d[c][t], xp[t], gs[m][c], false);
-        }
-      }
+      for (int i = 0; i < LANE_ROWS; ++i) tot[j][i] = __builtin_fmaf(sj, acc[j][i], tot[j][i]);
     }
-#pragma unroll
-    for (int m = 0; m < MT; ++m)
-#pragma unroll
-      for (int c = 0; c < 4; ++c) acc[m][c] = __builtin_fmaf(gs[m][c], (float)sc[c], acc[m][c]);
+  };
+
+  // Groups gb + wave, gb + wave + WAVES, ... with the next group's loads in
+  // flight while the current one is computed.  The scheduling barriers keep the compiler from sinking the prefetch
+  // below the compute it is meant to overlap.
+  Stage s0, s1;
+  int g = gb + wave;
+  if (g < ge) {
+    load(s0, g, true);
+    while (true) {
+      const int g1 = g + WAVES;
+      load(s1, g1, g1 < ge);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(s0);
+      __builtin_amdgcn_sched_barrier(0);
+      if (g1 >= ge) break;
+      const int g2 = g1 + WAVES;
+      load(s0, g2, g2 < ge);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(s1);
+      __builtin_amdgcn_sched_barrier(0);
+      if (g2 >= ge) break;
+      g = g2;
+    }
   }
 
-  // Cross-wave reduction in LDS, summed in wave order.
+  // Lane (q, kb) holds rows 4*kb + i of columns col + j.  Sum the waves in
+  // LDS in wave order.
 #pragma unroll
-  for (int m = 0; m < MT; ++m) red[wave][m][lane] = f4_t{acc[m][0], acc[m][1], acc[m][2], acc[m][3]};
+  for (int i = 0; i < LANE_ROWS; ++i) {
+    const int r = 4 * kb + i;
+    if (r < MT) red[wave][r][q] = f4_t{tot[0][i], tot[1][i], tot[2][i], tot[3][i]};
+  }
   __syncthreads();
 
   const bool direct = a.splits == 1;
-  for (int it = threadIdx.x; it < MT * 64; it += WAVES * 64) {
-    const int m = it >> 6, l = it & 63;
-    const int col = slab * kSlabCols + l * 4;
-    if (m >= a.M || col >= a.N) continue;
-    f4_t s = red[0][m][l];
+  const int t = threadIdx.x;
+  const int r = t >> 4, qq = t & 15;
+  const int ocol = strip * kStripCols + 4 * qq;
+  const bool owner = t < MT * 16 && r < a.M && ocol < a.N;
+  if (owner) {
+    f4_t sum = red[0][r][qq];
 #pragma unroll
     for (int w = 1; w < WAVES; ++w) {
-      const f4_t v = red[w][m][l];
-      s[0] += v[0];
-      s[1] += v[1];
-      s[2] += v[2];
-      s[3] += v[3];
+      const f4_t v = red[w][r][qq];
+      sum[0] += v[0];
+      sum[1] += v[1];
+      sum[2] += v[2];
+      sum[3] += v[3];
     }
     if (direct) {
-      const h4_t y = {(_Float16)s[0], (_Float16)s[1], (_Float16)s[2], (_Float16)s[3]};
-      *reinterpret_cast<h4_t*>(a.Y + static_cast<size_t>(m) * a.N + col) = y;
+      const h4_t y = {(_Float16)sum[0], (_Float16)sum[1], (_Float16)sum[2], (_Float16)sum[3]};
+      *reinterpret_cast<h4_t*>(a.Y + static_cast<size_t>(r) * a.N + ocol) = y;
     } else {
-      *reinterpret_cast<f4_t*>(a.partial + (static_cast<size_t>(split) * a.M + m) * a.N + col) = s;
+      float* dst = a.partial + (static_cast<size_t>(split) * a.M + r) * a.N + ocol;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) store_coherent(dst + c, sum[c]);
     }
   }
   if (direct) return;
 
-  // Publish this split's partial; the last workgroup of the slab reduces.
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  // Publish this split's partial; the last workgroup of the strip reduces.
+  // The partials were written with device-coherent stores; waiting for them
+  // to complete orders them before the counter update without the whole-L2
+  // write-back / invalidate an agent-scope fence costs on a multi-XCD device.
+  wait_vm_stores();
   __syncthreads();
   if (threadIdx.x == 0) {
     const uint32_t prev =
-        __hip_atomic_fetch_add(a.counters + slab, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_add(a.counters + strip, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_last = (prev == static_cast<uint32_t>(a.splits - 1));
   }
   __syncthreads();
   if (!s_last) return;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
 
-  for (int it = threadIdx.x; it < MT * 64; it += WAVES * 64) {
-    const int m = it >> 6, l = it & 63;
-    const int col = slab * kSlabCols + l * 4;
-    if (m >= a.M || col >= a.N) continue;
-    f4_t s = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (owner) {
+    f4_t sum = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int sp = 0; sp < a.splits; ++sp) {
-      const f4_t v =
-          *reinterpret_cast<const f4_t*>(a.partial + (static_cast<size_t>(sp) * a.M + m) * a.N + col);
-      s[0] += v[0];
-      s[1] += v[1];
-      s[2] += v[2];
-      s[3] += v[3];
+      const float* src = a.partial + (static_cast<size_t>(sp) * a.M + r) * a.N + ocol;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) sum[c] += load_coherent(src + c);
     }
-    const h4_t y = {(_Float16)s[0], (_Float16)s[1], (_Float16)s[2], (_Float16)s[3]};
-    *reinterpret_cast<h4_t*>(a.Y + static_cast<size_t>(m) * a.N + col) = y;
+    const h4_t y = {(_Float16)sum[0], (_Float16)sum[1], (_Float16)sum[2], (_Float16)sum[3]};
+    *reinterpret_cast<h4_t*>(a.Y + static_cast<size_t>(r) * a.N + ocol) = y;
   }
   if (threadIdx.x == 0)
-    __hip_atomic_store(a.counters + slab, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(a.counters + strip, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Versions 0 and 1: one thread per (m, n), scalar decode, fp32 weights
@@ -209,8 +267,8 @@ __global__ __launch_bounds__(256) void gemv_scalar_kernel(const _Float16* __rest
 // Launch geometry of the streaming kernel.
 struct Plan {
   int mt = 1;
-  int waves = 4;
-  int slabs = 0;
+  int waves = 8;
+  int strips = 0;
   int splits = 1;
   int groups_per_split = 0;
   size_t counter_bytes = 0;
@@ -219,47 +277,36 @@ struct Plan {
 
 int mt_for(int64_t M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8; }
 
-// Largest wave count the LDS reduction buffer allows for MT rows (<= 32 KiB).
-int max_waves_for(int mt) { return std::min(16, 32 / mt); }
+constexpr int kDefaultWaves = 4;
+// Quant groups per wave a split aims for.  Measured on MI355X at M = 1 and 4:
+// one split is best up to K = 32 * 128 (the cross-workgroup reduction costs
+// more than it spreads), and larger K is split so each wave streams about
+// eight groups -- 14336 x 4096 is fastest at 4 splits, 8192 x 8192 at 2.
+constexpr int kGroupsPerWave = 8;
 
-int default_waves(int mt) { return std::min(4, max_waves_for(mt)); }
-
-// Split heuristic for MI355X: aim for ~8 resident waves per CU in total
-// (counted in wave-groups: one wave streams one quant group at a time), with
-// the K range of each split a whole number of waves' worth of groups.
+// Split heuristic: whole K in one workgroup per 64-column strip unless a wave
+// would have to stream more than kGroupsPerWave groups, in which case K is
+// split evenly.  Overrides follow the reference: splits are floor-then-trimmed
+// (csrc/gemv_w4a16.cu:398-401); versions 2 and 3 use one split.
 int plan_stream(int64_t M, int64_t K, int64_t N, int64_t G, int64_t version, int64_t splits_override,
-                int64_t threads_override, int cus, Plan* p) {
+                int64_t threads_override, Plan* p) {
   p->mt = mt_for(M);
-  if (threads_override > 0) {
-    p->waves = static_cast<int>(threads_override / 64);
-    if (p->waves > max_waves_for(p->mt))
-      return fail(NIBBLE_ERR_UNSUPPORTED, "block_threads=%lld too large for M=%lld (max %d)",
-                  (long long)threads_override, (long long)M, max_waves_for(p->mt) * 64);
-  } else {
-    p->waves = default_waves(p->mt);
-  }
-  p->slabs = static_cast<int>(ceil_div(N, kSlabCols));
+  p->waves = threads_override > 0 ? static_cast<int>(threads_override / 64) : kDefaultWaves;
+  p->strips = static_cast<int>(ceil_div(N, kStripCols));
   const int groups = static_cast<int>(K / G);
   int gps = groups;  // groups per split
   if (version == 4 && splits_override > 0) {
-    // Floor, then trim empty splits (csrc/gemv_w4a16.cu:398-401).
     const int want = static_cast<int>(std::min<int64_t>(splits_override, groups));
     gps = std::max(1, groups / want);
   } else if (version == 4) {
-    const int64_t target_waves = static_cast<int64_t>(cus) * 8;
-    const int64_t per_split = static_cast<int64_t>(p->slabs) * p->waves;
-    int64_t want = ceil_div(target_waves, per_split);
-    want = std::max<int64_t>(1, std::min<int64_t>(want, ceil_div(groups, p->waves)));
-    // A whole number of waves' worth of groups per split.
-    int64_t g = ceil_div(groups, want);
-    g = ceil_div(g, p->waves) * p->waves;
-    gps = static_cast<int>(std::min<int64_t>(g, groups));
+    const int want = static_cast<int>(ceil_div(groups, kGroupsPerWave * p->waves));
+    gps = static_cast<int>(ceil_div(groups, std::max(1, want)));
   }
   const int splits = static_cast<int>(ceil_div(groups, gps));
   p->splits = splits;
   p->groups_per_split = gps;
   if (splits > 1) {
-    p->counter_bytes = align_up(static_cast<size_t>(p->slabs) * 4, 256);
+    p->counter_bytes = align_up(static_cast<size_t>(p->strips) * 4, 256);
     p->workspace_bytes = p->counter_bytes + static_cast<size_t>(splits) * M * N * 4;
   } else {
     p->counter_bytes = 0;
@@ -270,25 +317,13 @@ int plan_stream(int64_t M, int64_t K, int64_t N, int64_t G, int64_t version, int
 
 template <int MT, int GROUP>
 hipError_t launch_mt(const GemvArgs& a, const Plan& p, hipStream_t stream) {
-  dim3 grid(p.slabs, p.splits);
+  dim3 grid(p.strips, p.splits);
   switch (p.waves) {
-    case 1: gemv_stream_kernel<MT, GROUP, 1><<<grid, 64, 0, stream>>>(a); break;
-    case 2: gemv_stream_kernel<MT, GROUP, 2><<<grid, 128, 0, stream>>>(a); break;
-    case 4: gemv_stream_kernel<MT, GROUP, 4><<<grid, 256, 0, stream>>>(a); break;
-    case 8:
-      if constexpr (MT <= 4) {
-        gemv_stream_kernel<MT, GROUP, 8><<<grid, 512, 0, stream>>>(a);
-        break;
-      } else {
-        return hipErrorInvalidValue;
-      }
-    case 16:
-      if constexpr (MT <= 2) {
-        gemv_stream_kernel<MT, GROUP, 16><<<grid, 1024, 0, stream>>>(a);
-        break;
-      } else {
-        return hipErrorInvalidValue;
-      }
+    case 1: gemv_mfma_kernel<MT, GROUP, 1><<<grid, 64, 0, stream>>>(a); break;
+    case 2: gemv_mfma_kernel<MT, GROUP, 2><<<grid, 128, 0, stream>>>(a); break;
+    case 4: gemv_mfma_kernel<MT, GROUP, 4><<<grid, 256, 0, stream>>>(a); break;
+    case 8: gemv_mfma_kernel<MT, GROUP, 8><<<grid, 512, 0, stream>>>(a); break;
+    case 16: gemv_mfma_kernel<MT, GROUP, 16><<<grid, 1024, 0, stream>>>(a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -329,13 +364,23 @@ int validate_gemv(const void* X, int64_t x_rows, int64_t x_cols, const void* Wq,
   NIBBLE_CHECK(version >= 0 && version <= 4, "version must be 0..4, got %lld", (long long)version);
   NIBBLE_CHECK(K < (int64_t(1) << 31) && N < (int64_t(1) << 31) && x_rows < (int64_t(1) << 31),
                "dimension too large");
-  NIBBLE_CHECK((K / 8) * N * 4 < (int64_t(1) << 32) || version <= 1,
-               "packed weights too large for 32-bit buffer offsets");
-  if (x_rows * K > 0 || x_rows * N > 0) {
-    NIBBLE_CHECK(X != nullptr && Wq != nullptr && S != nullptr && Y != nullptr, "null pointer");
-    NIBBLE_CHECK(aligned(X, 16) && aligned(Wq, 16) && aligned(S, 8) && aligned(Y, 8),
-                 "misaligned pointer (X and Wq need 16-byte, S and Y 8-byte alignment)");
-  }
+  // The streaming kernel addresses each operand through a buffer resource
+  // with 32-bit offsets and keeps 2^31 and up as its "read nothing" offset.
+  const int64_t lim = int64_t(1) << 31;
+  NIBBLE_CHECK(version <= 1 || ((K / 8) * N * 4 < lim && std::min<int64_t>(x_rows, 8) * K * 2 < lim &&
+                                (K / group_size) * N * 2 < lim),
+               "operands too large for 32-bit buffer offsets");
+  // Only operands that hold elements are dereferenced (empty tensors may
+  // carry a null data pointer).
+  const bool x_used = x_rows * K > 0 && x_rows * N > 0;
+  const bool w_used = K * N > 0 && x_rows > 0;
+  const bool y_used = x_rows * N > 0;
+  NIBBLE_CHECK((!x_used || X != nullptr) && (!w_used || (Wq != nullptr && S != nullptr)) &&
+                   (!y_used || Y != nullptr),
+               "null pointer");
+  NIBBLE_CHECK((!x_used || aligned(X, 16)) && (!w_used || (aligned(Wq, 16) && aligned(S, 8))) &&
+                   (!y_used || aligned(Y, 8)),
+               "misaligned pointer (X and Wq need 16-byte, S and Y 8-byte alignment)");
   return NIBBLE_OK;
 }
 
@@ -345,14 +390,8 @@ using namespace nibble;
 
 namespace {
 int gemv_plan(int64_t M, int64_t K, int64_t N, int64_t G, int64_t version, int64_t splits_override,
-              int64_t threads_override, hipStream_t stream, Plan* p) {
-  int cus = 256;
-  if (version == 4 && splits_override <= 0) {
-    int dev = 0;
-    NIBBLE_HIP(stream_device(stream, &dev));
-    NIBBLE_HIP(cu_count(dev, &cus));
-  }
-  return plan_stream(M, K, N, G, version, splits_override, threads_override, cus, p);
+              int64_t threads_override, Plan* p) {
+  return plan_stream(M, K, N, G, version, splits_override, threads_override, p);
 }
 }  // namespace
 
@@ -363,8 +402,8 @@ extern "C" size_t nibble_gemv_workspace_bytes(int64_t M, int64_t K, int64_t N, i
   if (group_size != 64 && group_size != 128) return 0;
   if (K % group_size != 0) return 0;
   Plan p;
-  if (gemv_plan(M, K, N, group_size, version, splits_override, threads_override,
-                static_cast<hipStream_t>(stream), &p) != NIBBLE_OK)
+  (void)stream;
+  if (gemv_plan(M, K, N, group_size, version, splits_override, threads_override, &p) != NIBBLE_OK)
     return 0;
   return p.workspace_bytes;
 }
@@ -376,8 +415,8 @@ extern "C" size_t nibble_gemv_counter_bytes(int64_t M, int64_t K, int64_t N, int
   if (group_size != 64 && group_size != 128) return 0;
   if (K % group_size != 0) return 0;
   Plan p;
-  if (gemv_plan(M, K, N, group_size, version, splits_override, threads_override,
-                static_cast<hipStream_t>(stream), &p) != NIBBLE_OK)
+  (void)stream;
+  if (gemv_plan(M, K, N, group_size, version, splits_override, threads_override, &p) != NIBBLE_OK)
     return 0;
   return p.counter_bytes;
 }
@@ -442,7 +481,7 @@ extern "C" int nibble_gemv_w4a16(const void* X, int64_t x_rows, int64_t x_cols, 
   }
 
   Plan p;
-  rc = gemv_plan(M, K, N, group_size, version, splits_override, threads_override, stream, &p);
+  rc = gemv_plan(M, K, N, group_size, version, splits_override, threads_override, &p);
   if (rc != NIBBLE_OK) return rc;
   if (p.workspace_bytes > 0) {
     if (workspace == nullptr || workspace_bytes < p.workspace_bytes)

@@ -44,19 +44,38 @@ constexpr uint32_t kMagic = 0x64006400u;  // two copies of fp16 1024.0
 __device__ __forceinline__ h2_t as_h2(uint32_t v) { return __builtin_bit_cast(h2_t, v); }
 __device__ __forceinline__ uint32_t as_u32(h2_t v) { return __builtin_bit_cast(uint32_t, v); }
 
-// (a & mask) | magic -- selected as a single v_and_or_b32.
+// (a & mask) | magic -- selected as one v_and_or_b32 when the mask and the
+// magic are register operands.
 __device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t magic) {
   return (a & mask) | magic;
 }
 
+// The decode constants as opaque register values.  gfx9 VOP3 encodings take
+// no 32-bit literal, so with the constants visible the compiler splits every
+// and-or into a v_and_b32 and a v_or_b32 with literal operands; hiding them
+// behind empty asm statements (which emit nothing) leaves it an SGPR mask and
+// a VGPR magic, and it selects the single v_and_or_b32 itself -- with the
+// usual hazard tracking towards the MFMAs that consume the result.
+struct DecodeConsts {
+  uint32_t lo, hi, magic;
+};
+__device__ __forceinline__ DecodeConsts decode_consts() {
+  DecodeConsts c;
+  asm("" : "=s"(c.lo) : "0"(kMaskLo));
+  asm("" : "=s"(c.hi) : "0"(kMaskHi));
+  asm("" : "=v"(c.magic) : "0"(kMagic));
+  return c;
+}
+
 // The four raw magic-biased pairs of one word: k (0,1) and (4,5) as 1024 + n,
 // k (2,3) and (6,7) as 1024 + 16n.
-__device__ __forceinline__ void decode8_raw(uint32_t q, uint32_t (&r)[4]) {
+__device__ __forceinline__ void decode8_raw(uint32_t q, uint32_t (&r)[4],
+                                            const DecodeConsts& k = decode_consts()) {
   const uint32_t qh = q >> 8;
-  r[0] = and_or(q, kMaskLo, kMagic);
-  r[1] = and_or(q, kMaskHi, kMagic);
-  r[2] = and_or(qh, kMaskLo, kMagic);
-  r[3] = and_or(qh, kMaskHi, kMagic);
+  r[0] = and_or(q, k.lo, k.magic);
+  r[1] = and_or(q, k.hi, k.magic);
+  r[2] = and_or(qh, k.lo, k.magic);
+  r[3] = and_or(qh, k.hi, k.magic);
 }
 
 // Exact (n - 8) for k = 0..7 as four half2 in ascending k.
@@ -80,11 +99,58 @@ __device__ __forceinline__ void decode8_scaled(uint32_t q, h2_t scale2, h2_t (&o
   for (int i = 0; i < 4; ++i) out[i] = out[i] * scale2;
 }
 
+// The four magic-biased pairs of one word as eight fp16 in ascending k, i.e.
+// one MFMA B-operand lane: k (0,1) and (4,5) hold 1024 + n, k (2,3) and (6,7)
+// hold 1024 + 16n.  5 VALU ops for 8 weights.
+__device__ __forceinline__ h8_t decode8_biased(uint32_t q, const DecodeConsts& k) {
+  uint32_t r[4];
+  decode8_raw(q, r, k);
+  const u4_t v = {r[0], r[1], r[2], r[3]};
+  return __builtin_bit_cast(h8_t, v);
+}
+
+// Companions of decode8_biased for an MFMA dot product.  With activations
+// pre-scaled by kBiasedXScale (x/16 at k % 8 in {2,3,6,7}), the biased weights
+// plus kBiasedCorrection give back exactly x * (n - 8) per element:
+//   k in {0,1,4,5}:  x    * ((1024 + n)   - 1032) = x * (n - 8)
+//   k in {2,3,6,7}:  x/16 * ((1024 + 16n) - 1152) = x * (n - 8)
+// so sum_k x~ * biased + sum_k x~ * correction is the exact-weight dot
+// product; the second sum does not depend on the column, so one MFMA
+// against the constant correction serves every column of a chunk.
+__device__ __forceinline__ h8_t biased_x_scale() {
+  const _Float16 a = (_Float16)1.0f, b = (_Float16)0.0625f;
+  return h8_t{a, a, b, b, a, a, b, b};
+}
+__device__ __forceinline__ h8_t biased_correction() {
+  const _Float16 a = (_Float16)-1032.0f, b = (_Float16)-1152.0f;
+  return h8_t{a, a, b, b, a, a, b, b};
+}
+
 // Scalar decode of logical offset k (0..7): shift, mask, subtract the
 // zero-point.  Slot formula from csrc/dequant.cuh:94-99 in the reference.
 __device__ __forceinline__ int nibble_value(uint32_t q, int k) {
   const int slot = (k & 1) ? (4 + (k >> 1)) : (k >> 1);
   return static_cast<int>((q >> (4 * slot)) & 0xFu) - 8;
+}
+
+// Device-coherent (agent-scope, relaxed) accesses for data exchanged between
+// workgroups of one launch.  On a multi-XCD device each XCD has its own L2;
+// these bypass its non-coherent copy instead of writing back / invalidating
+// the whole L2 the way an agent-scope fence does.
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_coherent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Waits until every outstanding vector-memory access of this wave (loads and
+// stores; gfx9 counts both in vmcnt) has completed.  A compiler barrier on
+// both sides keeps memory operations from moving across it.
+__device__ __forceinline__ void wait_vm_stores() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
 // Buffer resource for raw buffer loads on gfx9: base, stride 0, byte extent,
@@ -93,5 +159,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
                                            0x00020000);
 }
+
+// A lane offset no buffer resource of this library reaches (every resource is
+// < 2^31 bytes, checked on the host): loads through it return zero without
+// touching memory.
+constexpr uint32_t kOutOfRange = 0x80000000u;
 
 }  // namespace nibble

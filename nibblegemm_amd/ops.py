@@ -12,7 +12,7 @@ instead of a pybind11 torch extension:
 * kernels launch on torch's current stream of that device, so calls compose
   with torch ops and can be recorded into CUDA/HIP graphs;
 * the split-K workspace of ``gemv`` comes from a cache of zeroed buffers keyed
-  by (device, stream, graph capture): the kernel returns its counter region to
+  by (device, stream, graph capture, counter-region size): the kernel returns its counter region to
   zero at the end of every call, so a buffer is zeroed once and then reused.
   Inside a graph capture the first call allocates and zeroes a buffer for that
   capture, so the zeroing is part of the graph and every replay starts from
@@ -34,15 +34,56 @@ from .quant import QuantizedWeight, quantize  # noqa: F401  (re-exported)
 DECODE_MAX_M = 8
 
 _lock = threading.Lock()
-_workspaces: Dict[Tuple[int, int, int], torch.Tensor] = {}
+_workspaces: Dict[Tuple[int, int, int, int], torch.Tensor] = {}
 _ws_plan: Dict[tuple, Tuple[int, int]] = {}
 
 _get_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
 
-def extension():
-    """The loaded native binding (reference ops.py:33-56 JIT-built its extension
-    here; this package is built in-tree ahead of time and only loads it)."""
+class _Extension:
+    """What ``extension()`` returns: the reference extension module's three
+    tensor-level functions, with its argument names and defaults
+    (csrc/bindings.cpp:11-22), over the C ABI.  Attributes it does not define
+    (the pointer-level calls ``gemv``, ``gemm``, ``dequant``,
+    ``gemv_workspace_bytes``, ``last_error``, ``abi_version``) resolve to the
+    CPython binding."""
+
+    def __init__(self, binding):
+        self._binding = binding
+
+    def __getattr__(self, name):
+        return getattr(self._binding, name)
+
+    @staticmethod
+    def _qw(Wq: torch.Tensor, S: torch.Tensor, group_size: int) -> QuantizedWeight:
+        rows = Wq.shape[0] if Wq.dim() == 2 else 0
+        cols = Wq.shape[1] if Wq.dim() == 2 else 0
+        return QuantizedWeight(Wq, S, int(group_size), rows * 8, cols)
+
+    def gemv_w4a16(self, X, Wq, S, group_size, version=4, splits_override=0, threads_override=0):
+        return gemv(X, self._qw(Wq, S, group_size), version, splits_override, threads_override)
+
+    def gemm_w4a16(self, X, Wq, S, group_size, version=6):
+        return gemm(X, self._qw(Wq, S, group_size), version)
+
+    def dequant_w4(self, Wq, S, group_size, fast=True):
+        return dequant(self._qw(Wq, S, group_size), fast)
+
+
+_extension: Optional[_Extension] = None
+
+
+def extension() -> _Extension:
+    """The loaded native extension (reference ops.py:33-56 JIT-built it on first
+    use; this package is built in-tree ahead of time and only loads it).
+    Raises RuntimeError, naming the build command, when it is not built."""
+    global _extension
+    if _extension is None:
+        _extension = _Extension(_native.binding())
+    return _extension
+
+
+def _bind():
     return _native.binding()
 
 
@@ -103,10 +144,13 @@ def _gemv_workspace(ext, device: torch.device, stream: int, M: int, K: int, N: i
     if plan is None:
         plan = ext.gemv_workspace_bytes(M, K, N, g, version, splits, threads, stream)
         _ws_plan[key] = plan
-    nbytes = plan[0]
+    nbytes, counter_bytes = plan
     if nbytes == 0:
         return None, 0
-    wkey = (device.index, stream, _capture_id(stream))
+    # One buffer per counter-region size: a plan's fp32 partials start right
+    # after its counters, so a plan with fewer counters would overwrite the
+    # (zero) counters of a plan with more if they shared a buffer.
+    wkey = (device.index, stream, _capture_id(stream), counter_bytes)
     buf = _workspaces.get(wkey)
     if buf is None or buf.numel() < nbytes:
         with _lock:
@@ -121,7 +165,7 @@ def _gemv_workspace(ext, device: torch.device, stream: int, M: int, K: int, N: i
 def dequant(qw: QuantizedWeight, fast: bool = True) -> torch.Tensor:
     """Expand packed INT4 to a dense ``[K, N]`` fp16 matrix on the device
     (reference ops.py:59-61 -> csrc/dequant_kernel.cu:48-74)."""
-    ext = extension()
+    ext = _bind()
     Wq, S = qw.qweight, qw.scales
     if not (Wq.is_cuda and S.is_cuda):
         raise RuntimeError("tensors must live on the GPU")
@@ -151,7 +195,7 @@ def gemv(X: torch.Tensor, qw: QuantizedWeight, version: int = 4, splits: int = 0
     override the launch geometry (0 = heuristic); ``block_threads`` is a
     multiple of the 64-lane wave.  Versions 3 and 4 serve M <= 8.
     """
-    ext = extension()
+    ext = _bind()
     Wq, S = qw.qweight, qw.scales
     _check_matmul_inputs(X, Wq, S)
     M, K = X.shape
@@ -174,7 +218,7 @@ def gemv(X: torch.Tensor, qw: QuantizedWeight, version: int = 4, splits: int = 0
 def gemm(X: torch.Tensor, qw: QuantizedWeight, version: int = 6) -> torch.Tensor:
     """Prefill-regime matmul on MFMA (reference ops.py:77-86).  ``version`` 6
     (default) or 7 select two tile shapes with identical numerics."""
-    ext = extension()
+    ext = _bind()
     Wq, S = qw.qweight, qw.scales
     _check_matmul_inputs(X, Wq, S)
     M, K = X.shape

@@ -92,7 +92,7 @@ def test_gemv_threads_override_validated():
 
 def test_gemv_workspace_formula():
     ext = ng.extension()
-    # 1024 / 64 = 16 groups split 16 ways over one 256-column slab:
+    # 1024 / 64 = 16 groups split 16 ways over four 64-column strips:
     # 256 bytes of counters (padded), then 16 x M x N fp32 partials.
     ws, counters = ext.gemv_workspace_bytes(1, 1024, 256, 64, 4, 16, 0, None)
     assert counters == 256
@@ -103,6 +103,15 @@ def test_gemv_workspace_formula():
     # a single split needs no workspace
     assert ext.gemv_workspace_bytes(1, 1024, 256, 64, 4, 1, 0, None) == (0, 0)
     assert ext.gemv_workspace_bytes(1, 1024, 256, 64, 3, 0, 0, None) == (0, 0)
+    # default plan at the BASELINE decode shapes (pure host arithmetic):
+    # one split up to 32 quant groups, then ~8 groups per wave of 4
+    assert ext.gemv_workspace_bytes(1, 4096, 14336, 128, 4, 0, 0, None) == (0, 0)
+    assert ext.gemv_workspace_bytes(1, 4096, 4096, 128, 4, 0, 0, None) == (0, 0)
+    assert ext.gemv_workspace_bytes(1, 14336, 4096, 128, 4, 0, 0, None) == (256 + 4 * 4096 * 4, 256)
+    assert ext.gemv_workspace_bytes(1, 8192, 8192, 128, 4, 0, 0, None) == (256 + 2 * 8192 * 4, 256)
+    # 14336 / 64 = 224 strips of counters need 896 bytes, padded to 1024
+    assert ext.gemv_workspace_bytes(2, 16384, 14336, 128, 4, 0, 0, None) == (
+        1024 + 4 * 2 * 14336 * 4, 1024)
     # invalid requests report zero
     assert ext.gemv_workspace_bytes(9, 1024, 256, 64, 4, 4, 0, None) == (0, 0)
     assert ext.gemv_workspace_bytes(1, 1024, 256, 32, 4, 4, 0, None) == (0, 0)
@@ -185,3 +194,22 @@ def test_library_loads_only_one_hip_runtime():
     maps = [l for l in open("/proc/self/maps") if "libamdhip64" in l]
     paths = {l.split()[-1] for l in maps}
     assert len(paths) <= 1, paths
+
+
+def test_extension_exposes_the_reference_module_functions():
+    """``extension()`` offers the reference module's tensor-level functions
+    (csrc/bindings.cpp:11-22) with the same argument names and defaults."""
+    import inspect  # noqa: PLC0415
+
+    ext = ng.extension()
+    sig = inspect.signature(ext.gemv_w4a16)
+    assert list(sig.parameters) == ["X", "Wq", "S", "group_size", "version", "splits_override",
+                                    "threads_override"]
+    assert sig.parameters["version"].default == 4
+    assert inspect.signature(ext.gemm_w4a16).parameters["version"].default == 6
+    assert inspect.signature(ext.dequant_w4).parameters["fast"].default is True
+    X, qw = _cpu_case()
+    with pytest.raises(RuntimeError, match="GPU"):
+        ext.gemv_w4a16(X, qw.qweight, qw.scales, 128)
+    with pytest.raises(RuntimeError, match="GPU"):
+        ext.dequant_w4(qw.qweight, qw.scales, 128)

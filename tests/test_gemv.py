@@ -118,9 +118,9 @@ def test_split_k_is_deterministic_and_counters_return_to_zero():
     from nibblegemm_amd import ops
 
     stream = torch.cuda.current_stream().cuda_stream
-    buf = ops._workspaces[(Xd.device.index, stream, 0)]
     counter_bytes = ng.extension().gemv_workspace_bytes(2, 4096, 4096, 128, 4, 0, 0, stream)[1]
     assert counter_bytes > 0
+    buf = ops._workspaces[(Xd.device.index, stream, 0, counter_bytes)]
     assert int(buf[:counter_bytes].count_nonzero()) == 0
 
 
