@@ -108,7 +108,7 @@ def test_gemv_workspace_formula():
     assert ext.gemv_workspace_bytes(1, 4096, 14336, 128, 4, 0, 0, None) == (0, 0)
     assert ext.gemv_workspace_bytes(1, 4096, 4096, 128, 4, 0, 0, None) == (0, 0)
     assert ext.gemv_workspace_bytes(1, 14336, 4096, 128, 4, 0, 0, None) == (256 + 4 * 4096 * 4, 256)
-    assert ext.gemv_workspace_bytes(1, 8192, 8192, 128, 4, 0, 0, None) == (256 + 2 * 8192 * 4, 256)
+    assert ext.gemv_workspace_bytes(1, 8192, 8192, 128, 4, 0, 0, None) == (512 + 2 * 8192 * 4, 512)
     # 14336 / 64 = 224 strips of counters need 896 bytes, padded to 1024
     assert ext.gemv_workspace_bytes(2, 16384, 14336, 128, 4, 0, 0, None) == (
         1024 + 4 * 2 * 14336 * 4, 1024)
