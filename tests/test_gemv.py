@@ -110,7 +110,8 @@ def test_block_threads_override(threads):
 
 
 def test_split_k_is_deterministic_and_counters_return_to_zero():
-    _, _, _, Xd, qw = synthetic(2, 4096, 4096, 128, seed=4)
+    # 14336 x 4096 is split over workgroups by the default plan (112 groups)
+    _, _, _, Xd, qw = synthetic(2, 14336, 4096, 128, seed=4)
     ys = [ng.gemv(Xd, qw) for _ in range(5)]
     torch.cuda.synchronize()
     for y in ys[1:]:
@@ -118,7 +119,7 @@ def test_split_k_is_deterministic_and_counters_return_to_zero():
     from nibblegemm_amd import ops
 
     stream = torch.cuda.current_stream().cuda_stream
-    counter_bytes = ng.extension().gemv_workspace_bytes(2, 4096, 4096, 128, 4, 0, 0, stream)[1]
+    counter_bytes = ng.extension().gemv_workspace_bytes(2, 14336, 4096, 128, 4, 0, 0, stream)[1]
     assert counter_bytes > 0
     buf = ops._workspaces[(Xd.device.index, stream, 0, counter_bytes)]
     assert int(buf[:counter_bytes].count_nonzero()) == 0
