@@ -2,7 +2,9 @@
 """Headline benchmark: the M=1 W4A16 decode GEMV at K=4096, N=14336, g=128.
 
 BASELINE.json's metric is "M=1 W4A16 GEMV us & % HBM peak (4096x14336);
-8B-shape decode tok/s", quoted on configs[1]'s gate/up shape.  A *step* is
+8B-shape decode tok/s", quoted on configs[1]'s gate/up shape; the second half
+(configs[4], the Llama-3-8B-shaped decode step) is reported under
+``decode_8b`` by :mod:`nibblegemm_amd.decode_step`.  A *step* is
 one ``nibblegemm_amd.gemv`` call (M=1) over one batch of synthetic inputs
 (nibbles U{0..15}, scales fp16 U(0.002, 0.02), activations fp16 N(0,1)).
 
@@ -72,6 +74,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--skip-extras", action="store_true",
                     help="skip the copy-bandwidth, hipBLASLt and eager side measurements")
+    ap.add_argument("--skip-decode-step", action="store_true",
+                    help="skip the 8B-shaped decode step (BASELINE config 5)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -145,6 +149,19 @@ def main() -> int:
         log(f"copy {copy:.0f} GB/s; hipBLASLt fp16 {fp16.median_ms * 1e3:.2f} us; "
             f"eager {eager.median_ms * 1e3:.2f} us/call")
 
+    decode = None
+    if not args.skip_decode_step:
+        from nibblegemm_amd import decode_step  # noqa: PLC0415
+
+        del variants, rot_w, rot_s
+        torch.cuda.empty_cache()
+        t0 = time.perf_counter()
+        decode = decode_step.run(32)
+        log(f"8B decode step: {decode['projections']['graph_tok_s']} tok/s graph "
+            f"({decode['projections']['launches']} launches), fused "
+            f"{decode['fused']['graph_tok_s']} tok/s ({decode['fused']['launches']} launches); "
+            f"{time.perf_counter() - t0:.1f} s")
+
     roofline = {
         "bound": "hbm",
         "achieved": round(gbps, 1),
@@ -181,6 +198,7 @@ def main() -> int:
         "pct_hbm_peak": round(100 * gbps / H.HBM_PEAK_GBPS, 2),
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "decode_8b": decode,
         **extras,
     }
     print(json.dumps(line), flush=True)

@@ -50,7 +50,7 @@
 extern "C" {
 #endif
 
-#define NIBBLE_ABI_VERSION 1
+#define NIBBLE_ABI_VERSION 2
 
 #if defined(__GNUC__) || defined(__clang__)
 #define NIBBLE_API __attribute__((visibility("default")))
@@ -111,11 +111,23 @@ NIBBLE_API size_t nibble_gemv_counter_bytes(int64_t M, int64_t K, int64_t N, int
  * Prefill-regime matmul on CDNA4 MFMA (any M >= 1).  version 6 (default) or 7
  * (alternate tile shape; same numerics).  Requires K % 32 == 0, N even,
  * group_size in {64, 128} and M*N, M*K, K*N < 2^31 (the reference's checks).
+ * Batches of M <= 32 (with N % 4 == 0) run the weight-streaming kernel of
+ * the GEMV, which may split K: `workspace` follows the same rules as for
+ * nibble_gemv_w4a16, sized by nibble_gemm_workspace_bytes(...) (0 for M > 32,
+ * where it may be NULL).
  */
 NIBBLE_API int nibble_gemm_w4a16(const void* X, int64_t x_rows, int64_t x_cols,
                       const void* Wq, int64_t wq_rows, int64_t wq_cols,
                       const void* S, int64_t s_rows, int64_t s_cols,
-                      int64_t group_size, int64_t version, void* Y, void* stream);
+                      int64_t group_size, int64_t version, void* Y,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace nibble_gemm_w4a16 needs (0 if none) and its leading zeroed
+ * counter bytes.  Pure host computation; `stream` is not used. */
+NIBBLE_API size_t nibble_gemm_workspace_bytes(int64_t M, int64_t K, int64_t N, int64_t group_size,
+                                   int64_t version, void* stream);
+NIBBLE_API size_t nibble_gemm_counter_bytes(int64_t M, int64_t K, int64_t N, int64_t group_size,
+                                 int64_t version, void* stream);
 
 /*
  * Dense fp16 W [K, N] from packed weights, bit-exact with the reference's

@@ -14,9 +14,11 @@ of this package.
 from .ops import DECODE_MAX_M, QuantLinear, dequant, extension, gemm, gemv, matmul
 from .quant import (
     QuantizedWeight,
+    concat_columns,
     dequantize,
     pack_nibbles,
     quantize,
+    quantize_device,
     reference_matmul,
     unpack_nibbles,
 )
@@ -25,6 +27,7 @@ __all__ = [
     "DECODE_MAX_M",
     "QuantLinear",
     "QuantizedWeight",
+    "concat_columns",
     "dequant",
     "dequantize",
     "extension",
@@ -33,6 +36,7 @@ __all__ = [
     "matmul",
     "pack_nibbles",
     "quantize",
+    "quantize_device",
     "reference_matmul",
     "unpack_nibbles",
 ]

@@ -68,20 +68,35 @@ static PyObject* py_gemv_ws(PyObject* self, PyObject* const* a, Py_ssize_t n) {
   return Py_BuildValue("(nn)", (Py_ssize_t)ws, (Py_ssize_t)cb);
 }
 
-/* gemm(X, xr, xc, Wq, wr, wc, S, sr, sc, g, version, Y, stream) */
+/* gemm(X, xr, xc, Wq, wr, wc, S, sr, sc, g, version, Y, ws, ws_bytes, stream) */
 static PyObject* py_gemm(PyObject* self, PyObject* const* a, Py_ssize_t n) {
   (void)self;
-  if (!nargs_is(n, 13, "gemm")) return NULL;
-  void *X, *Wq, *S, *Y, *stream;
-  long long xr, xc, wr, wc, sr, sc, g, ver;
+  if (!nargs_is(n, 15, "gemm")) return NULL;
+  void *X, *Wq, *S, *Y, *ws, *stream;
+  long long xr, xc, wr, wc, sr, sc, g, ver, wsb;
   if (!take_ptr(a[0], &X) || !take_i64(a[1], &xr) || !take_i64(a[2], &xc) ||
       !take_ptr(a[3], &Wq) || !take_i64(a[4], &wr) || !take_i64(a[5], &wc) ||
       !take_ptr(a[6], &S) || !take_i64(a[7], &sr) || !take_i64(a[8], &sc) ||
       !take_i64(a[9], &g) || !take_i64(a[10], &ver) || !take_ptr(a[11], &Y) ||
-      !take_ptr(a[12], &stream))
+      !take_ptr(a[12], &ws) || !take_i64(a[13], &wsb) || !take_ptr(a[14], &stream))
     return NULL;
-  int rc = nibble_gemm_w4a16(X, xr, xc, Wq, wr, wc, S, sr, sc, g, ver, Y, stream);
+  int rc = nibble_gemm_w4a16(X, xr, xc, Wq, wr, wc, S, sr, sc, g, ver, Y, ws,
+                             (size_t)(wsb < 0 ? 0 : wsb), stream);
   return PyLong_FromLong(rc);
+}
+
+/* gemm_workspace_bytes(M, K, N, g, version, stream) */
+static PyObject* py_gemm_ws(PyObject* self, PyObject* const* a, Py_ssize_t n) {
+  (void)self;
+  if (!nargs_is(n, 6, "gemm_workspace_bytes")) return NULL;
+  long long M, K, N, g, ver;
+  void* stream;
+  if (!take_i64(a[0], &M) || !take_i64(a[1], &K) || !take_i64(a[2], &N) || !take_i64(a[3], &g) ||
+      !take_i64(a[4], &ver) || !take_ptr(a[5], &stream))
+    return NULL;
+  size_t ws = nibble_gemm_workspace_bytes(M, K, N, g, ver, stream);
+  size_t cb = nibble_gemm_counter_bytes(M, K, N, g, ver, stream);
+  return Py_BuildValue("(nn)", (Py_ssize_t)ws, (Py_ssize_t)cb);
 }
 
 /* dequant(Wq, wr, wc, S, sr, sc, g, fast, W, stream) */
@@ -116,6 +131,8 @@ static PyMethodDef kMethods[] = {
     {"gemv_workspace_bytes", (PyCFunction)(void (*)(void))py_gemv_ws, METH_FASTCALL,
      "(nibble_gemv_workspace_bytes, nibble_gemv_counter_bytes)"},
     {"gemm", (PyCFunction)(void (*)(void))py_gemm, METH_FASTCALL, "nibble_gemm_w4a16"},
+    {"gemm_workspace_bytes", (PyCFunction)(void (*)(void))py_gemm_ws, METH_FASTCALL,
+     "(nibble_gemm_workspace_bytes, nibble_gemm_counter_bytes)"},
     {"dequant", (PyCFunction)(void (*)(void))py_dequant, METH_FASTCALL, "nibble_dequant_w4"},
     {"last_error", py_last_error, METH_NOARGS, "nibble_last_error"},
     {"abi_version", py_abi_version, METH_NOARGS, "nibble_abi_version"},

@@ -24,6 +24,7 @@
 
 #include "nibble_common.h"
 #include "nibble_decode.h"
+#include "stream_matmul.h"
 
 namespace nibble {
 
@@ -203,10 +204,41 @@ int validate_gemm(const void* X, int64_t x_rows, int64_t x_cols, const void* Wq,
 
 using namespace nibble;
 
+namespace {
+// Small batches go to the weight-streaming kernel: each weight byte is read
+// once and multiplied against all M rows (one or two 16-row MFMA tiles),
+// where a 64/128-row tile would leave most of the device idle and re-decode
+// the weights per row tile.  Measured on MI355X at K=4096, N=14336: M=16
+// takes 82 us through the tile kernel, ~9 us streaming.
+bool gemm_streams(int64_t M, int64_t K, int64_t N, int64_t G) {
+  return M >= 1 && M <= kStreamMaxM && K > 0 && N > 0 && N % 4 == 0 && K % G == 0;
+}
+}  // namespace
+
+extern "C" size_t nibble_gemm_workspace_bytes(int64_t M, int64_t K, int64_t N, int64_t group_size,
+                                              int64_t version, void* stream) {
+  (void)stream;
+  if ((version != 6 && version != 7) || (group_size != 64 && group_size != 128)) return 0;
+  if (!gemm_streams(M, K, N, group_size)) return 0;
+  StreamPlan p;
+  if (plan_stream(M, K, N, group_size, true, 0, 0, &p) != NIBBLE_OK) return 0;
+  return p.workspace_bytes;
+}
+
+extern "C" size_t nibble_gemm_counter_bytes(int64_t M, int64_t K, int64_t N, int64_t group_size,
+                                            int64_t version, void* stream) {
+  (void)stream;
+  if ((version != 6 && version != 7) || (group_size != 64 && group_size != 128)) return 0;
+  if (!gemm_streams(M, K, N, group_size)) return 0;
+  StreamPlan p;
+  if (plan_stream(M, K, N, group_size, true, 0, 0, &p) != NIBBLE_OK) return 0;
+  return p.counter_bytes;
+}
+
 extern "C" int nibble_gemm_w4a16(const void* X, int64_t x_rows, int64_t x_cols, const void* Wq,
                                  int64_t wq_rows, int64_t wq_cols, const void* S, int64_t s_rows,
                                  int64_t s_cols, int64_t group_size, int64_t version, void* Y,
-                                 void* stream_) {
+                                 void* workspace, size_t workspace_bytes, void* stream_) {
   int rc = validate_gemm(X, x_rows, x_cols, Wq, wq_rows, wq_cols, S, s_rows, s_cols, group_size,
                          version, Y);
   if (rc != NIBBLE_OK) return rc;
@@ -216,15 +248,23 @@ extern "C" int nibble_gemm_w4a16(const void* X, int64_t x_rows, int64_t x_cols, 
   DeviceGuard guard;
   int dev = 0;
   NIBBLE_HIP(guard.enter(stream, &dev));
+  if (K == 0) {
+    NIBBLE_HIP(fill_zero_f16(Y, M * N, stream));
+    return ok();
+  }
+  if (gemm_streams(M, K, N, group_size) && stream_supported(X, Wq, S, Y, M, K, N, group_size)) {
+    StreamPlan p;
+    rc = plan_stream(M, K, N, group_size, true, 0, 0, &p);
+    if (rc != NIBBLE_OK) return rc;
+    rc = launch_stream(X, Wq, S, Y, M, K, N, group_size, p, workspace, workspace_bytes, stream,
+                       "gemm (streaming) kernel launch");
+    return rc == NIBBLE_OK ? ok() : rc;
+  }
   const auto* x = static_cast<const _Float16*>(X);
   const auto* w = static_cast<const uint32_t*>(Wq);
   const auto* s = static_cast<const _Float16*>(S);
   auto* y = static_cast<_Float16*>(Y);
   hipError_t e;
-  if (K == 0) {
-    NIBBLE_HIP(fill_zero_f16(Y, M * N, stream));
-    return ok();
-  }
   if (version == 7)
     e = launch_tile<64, 128>(x, w, s, y, M, K, N, group_size, stream);
   else

@@ -37,6 +37,7 @@
 
 #include "nibble_common.h"
 #include "nibble_decode.h"
+#include "stream_matmul.h"
 
 namespace nibble {
 
@@ -62,16 +63,18 @@ __device__ __forceinline__ f4_t mfma16(h8_t a, h8_t b, f4_t c) {
 
 template <int MT, int GROUP, int WAVES>
 __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs a) {
-  constexpr int CPG = GROUP / 32;              // 32-k chunks per quant group
-  constexpr int LANE_ROWS = MT < 4 ? MT : 4;   // output rows a lane can hold
-  __shared__ f4_t red[WAVES][MT][16];          // [wave][row][column quad]
+  constexpr int CPG = GROUP / 32;                  // 32-k chunks per quant group
+  constexpr int TILES = (MT + 15) / 16;            // 16-row MFMA A tiles
+  constexpr int LANE_ROWS = MT < 4 ? MT : 4;       // output rows a lane holds per tile
+  constexpr int THREADS = WAVES * 64;
+  __shared__ f4_t red[WAVES][MT][16];              // [wave][row][column quad]
   __shared__ int s_last;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int strip = blockIdx.x;
   const int split = blockIdx.y;
-  const int q = lane & 15;   // B column slot (column quad) and A row
+  const int q = lane & 15;   // B column slot (column quad) and A row within a tile
   const int kb = lane >> 4;  // 8-k block within a 32-k chunk
   const int col = strip * kStripCols + 4 * q;
   const bool col_ok = col < a.N;
@@ -83,12 +86,16 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs a) {
   const __amdgpu_buffer_rsrc_t rs =
       make_rsrc(a.S, static_cast<uint32_t>(a.K / GROUP) * static_cast<uint32_t>(a.N) * 2u);
   const uint32_t voff_w = col_ok ? kb * row_bytes + static_cast<uint32_t>(col) * 4u : kOutOfRange;
-  const uint32_t voff_x =
-      q < a.M ? (static_cast<uint32_t>(q) * a.K + 8u * kb) * 2u : kOutOfRange;
   const uint32_t voff_s = col_ok ? static_cast<uint32_t>(col) * 2u : kOutOfRange;
+  uint32_t voff_x[TILES];
+#pragma unroll
+  for (int t = 0; t < TILES; ++t) {
+    const int m = 16 * t + q;
+    voff_x[t] = m < a.M ? (static_cast<uint32_t>(m) * a.K + 8u * kb) * 2u : kOutOfRange;
+  }
 
   struct Stage {
-    h8_t x[CPG];
+    h8_t x[TILES][CPG];
     h4_t s;
     u4_t w[CPG];
   };
@@ -103,52 +110,68 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs a) {
   const int ge = min(gb + a.groups_per_split, total_groups);
   auto load = [&](Stage& st, int g, bool enabled) {
     g = enabled ? g : ge - 1;
-    const uint32_t vx = voff_x, vs = voff_s, vw = voff_w;
     const uint32_t kx = static_cast<uint32_t>(g) * GROUP * 2u;
     const uint32_t kw = static_cast<uint32_t>(g) * (GROUP / 8) * row_bytes;
 #pragma unroll
-    for (int c = 0; c < CPG; ++c)
-      st.x[c] = __builtin_bit_cast(h8_t, __builtin_amdgcn_raw_buffer_load_b128(rx, vx, kx + c * 64, 0));
+    for (int t = 0; t < TILES; ++t)
+#pragma unroll
+      for (int c = 0; c < CPG; ++c)
+        st.x[t][c] = __builtin_bit_cast(
+            h8_t, __builtin_amdgcn_raw_buffer_load_b128(rx, voff_x[t], kx + c * 64, 0));
     st.s = __builtin_bit_cast(
-        h4_t, __builtin_amdgcn_raw_buffer_load_b64(rs, vs, static_cast<uint32_t>(g) * a.N * 2u, 0));
+        h4_t, __builtin_amdgcn_raw_buffer_load_b64(rs, voff_s, static_cast<uint32_t>(g) * a.N * 2u, 0));
 #pragma unroll
     for (int c = 0; c < CPG; ++c)
       st.w[c] = __builtin_bit_cast(
-          u4_t, __builtin_amdgcn_raw_buffer_load_b128(rw, vw, kw + c * 4 * row_bytes, 0));
+          u4_t, __builtin_amdgcn_raw_buffer_load_b128(rw, voff_w, kw + c * 4 * row_bytes, 0));
   };
 
-  f4_t tot[4];
+  f4_t tot[TILES][4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) tot[j] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int t = 0; t < TILES; ++t)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) tot[t][j] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
   const DecodeConsts dk = decode_consts();
   const h8_t xscale = biased_x_scale();
   const h8_t bcorr = biased_correction();
   auto compute = [&](const Stage& st) {
-    h8_t xs[CPG];
+    h8_t xs[TILES][CPG];
+    f4_t acc[TILES][4];
 #pragma unroll
-    for (int c = 0; c < CPG; ++c) xs[c] = st.x[c] * xscale;
-    f4_t corr = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int t = 0; t < TILES; ++t) {
 #pragma unroll
-    for (int c = 0; c < CPG; ++c) corr = mfma16(xs[c], bcorr, corr);
-    f4_t acc[4];
+      for (int c = 0; c < CPG; ++c) xs[t][c] = st.x[t][c] * xscale;
+      f4_t corr = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[j] = corr;
+      for (int c = 0; c < CPG; ++c) corr = mfma16(xs[t][c], bcorr, corr);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[t][j] = corr;
+    }
+    // One decode per word serves every tile.
 #pragma unroll
     for (int c = 0; c < CPG; ++c)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[j] = mfma16(xs[c], decode8_biased(st.w[c][j], dk), acc[j]);
+      for (int j = 0; j < 4; ++j) {
+        const h8_t b = decode8_biased(st.w[c][j], dk);
+#pragma unroll
+        for (int t = 0; t < TILES; ++t) acc[t][j] = mfma16(xs[t][c], b, acc[t][j]);
+      }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const float sj = static_cast<float>(st.s[j]);
 #pragma unroll
-      for (int i = 0; i < LANE_ROWS; ++i) tot[j][i] = __builtin_fmaf(sj, acc[j][i], tot[j][i]);
+      for (int t = 0; t < TILES; ++t)
+#pragma unroll
+        for (int i = 0; i < LANE_ROWS; ++i)
+          tot[t][j][i] = __builtin_fmaf(sj, acc[t][j][i], tot[t][j][i]);
     }
   };
 
   // Groups gb + wave, gb + wave + WAVES, ... with the next group's loads in
-  // flight while the current one is computed.  The scheduling barriers keep the compiler from sinking the prefetch
-  // below the compute it is meant to overlap.
+  // flight while the current one is computed.  The scheduling barriers keep
+  // the compiler from sinking the prefetch below the compute it is meant to
+  // overlap.
   Stage s0, s1;
   int g = gb + wave;
   if (g < ge) {
@@ -170,21 +193,23 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs a) {
     }
   }
 
-  // Lane (q, kb) holds rows 4*kb + i of columns col + j.  Sum the waves in
-  // LDS in wave order.
+  // Lane (q, kb) holds rows 16*t + 4*kb + i of columns col + j.  Sum the
+  // waves in LDS in wave order.
 #pragma unroll
-  for (int i = 0; i < LANE_ROWS; ++i) {
-    const int r = 4 * kb + i;
-    if (r < MT) red[wave][r][q] = f4_t{tot[0][i], tot[1][i], tot[2][i], tot[3][i]};
-  }
+  for (int t = 0; t < TILES; ++t)
+#pragma unroll
+    for (int i = 0; i < LANE_ROWS; ++i) {
+      const int r = 16 * t + 4 * kb + i;
+      if (r < MT) red[wave][r][q] = f4_t{tot[t][0][i], tot[t][1][i], tot[t][2][i], tot[t][3][i]};
+    }
   __syncthreads();
 
+  // Thread e of the workgroup owns (row e / 16, column quad e % 16).
   const bool direct = a.splits == 1;
-  const int t = threadIdx.x;
-  const int r = t >> 4, qq = t & 15;
-  const int ocol = strip * kStripCols + 4 * qq;
-  const bool owner = t < MT * 16 && r < a.M && ocol < a.N;
-  if (owner) {
+  for (int e = threadIdx.x; e < MT * 16; e += THREADS) {
+    const int r = e >> 4, qq = e & 15;
+    const int ocol = strip * kStripCols + 4 * qq;
+    if (r >= a.M || ocol >= a.N) continue;
     f4_t sum = red[0][r][qq];
 #pragma unroll
     for (int w = 1; w < WAVES; ++w) {
@@ -219,7 +244,10 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs a) {
   __syncthreads();
   if (!s_last) return;
 
-  if (owner) {
+  for (int e = threadIdx.x; e < MT * 16; e += THREADS) {
+    const int r = e >> 4, qq = e & 15;
+    const int ocol = strip * kStripCols + 4 * qq;
+    if (r >= a.M || ocol >= a.N) continue;
     f4_t sum = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int sp = 0; sp < a.splits; ++sp) {
       const float* src = a.partial + (static_cast<size_t>(sp) * a.M + r) * a.N + ocol;
@@ -264,18 +292,13 @@ __global__ __launch_bounds__(256) void gemv_scalar_kernel(const _Float16* __rest
   Y[static_cast<size_t>(m) * N + n] = (_Float16)acc;
 }
 
-// Launch geometry of the streaming kernel.
-struct Plan {
-  int mt = 1;
-  int waves = 8;
-  int strips = 0;
-  int splits = 1;
-  int groups_per_split = 0;
-  size_t counter_bytes = 0;
-  size_t workspace_bytes = 0;
-};
+int mt_for(int64_t M) {
+  return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : M <= 8 ? 8 : M <= 16 ? 16 : 32;
+}
 
-int mt_for(int64_t M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8; }
+// Largest workgroup the LDS reduction buffer (waves x rows x 256 B) allows
+// within 64 KiB.
+int max_waves_for(int mt) { return std::min(16, 256 / mt); }
 
 constexpr int kDefaultWaves = 4;
 // Quant groups per wave a split aims for.  Measured on MI355X at M = 1 and 4:
@@ -284,21 +307,61 @@ constexpr int kDefaultWaves = 4;
 // eight groups -- 14336 x 4096 is fastest at 4 splits, 8192 x 8192 at 2.
 constexpr int kGroupsPerWave = 8;
 
+template <int MT, int GROUP>
+hipError_t launch_mt(const GemvArgs& a, const StreamPlan& p, hipStream_t stream) {
+  dim3 grid(p.strips, p.splits);
+  switch (p.waves) {
+    case 1: gemv_mfma_kernel<MT, GROUP, 1><<<grid, 64, 0, stream>>>(a); break;
+    case 2: gemv_mfma_kernel<MT, GROUP, 2><<<grid, 128, 0, stream>>>(a); break;
+    case 4: gemv_mfma_kernel<MT, GROUP, 4><<<grid, 256, 0, stream>>>(a); break;
+    case 8: gemv_mfma_kernel<MT, GROUP, 8><<<grid, 512, 0, stream>>>(a); break;
+    case 16:
+      if constexpr (MT <= 16) {
+        gemv_mfma_kernel<MT, GROUP, 16><<<grid, 1024, 0, stream>>>(a);
+        break;
+      } else {
+        return hipErrorInvalidValue;
+      }
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+template <int GROUP>
+hipError_t launch_group(const GemvArgs& a, const StreamPlan& p, hipStream_t stream) {
+  switch (p.mt) {
+    case 1: return launch_mt<1, GROUP>(a, p, stream);
+    case 2: return launch_mt<2, GROUP>(a, p, stream);
+    case 4: return launch_mt<4, GROUP>(a, p, stream);
+    case 8: return launch_mt<8, GROUP>(a, p, stream);
+    case 16: return launch_mt<16, GROUP>(a, p, stream);
+    default: return launch_mt<32, GROUP>(a, p, stream);
+  }
+}
+
+}  // namespace
+
 // Split heuristic: whole K in one workgroup per 64-column strip unless a wave
 // would have to stream more than kGroupsPerWave groups, in which case K is
 // split evenly.  Overrides follow the reference: splits are floor-then-trimmed
-// (csrc/gemv_w4a16.cu:398-401); versions 2 and 3 use one split.
-int plan_stream(int64_t M, int64_t K, int64_t N, int64_t G, int64_t version, int64_t splits_override,
-                int64_t threads_override, Plan* p) {
+// (csrc/gemv_w4a16.cu:398-401).
+int plan_stream(int64_t M, int64_t K, int64_t N, int64_t G, bool split_k, int64_t splits_override,
+                int64_t threads_override, StreamPlan* p) {
+  if (M < 1 || M > kStreamMaxM || K <= 0 || N <= 0 || (G != 64 && G != 128) || K % G != 0)
+    return fail(NIBBLE_ERR_INVALID_ARGUMENT, "no streaming plan for M=%lld K=%lld N=%lld G=%lld",
+                (long long)M, (long long)K, (long long)N, (long long)G);
   p->mt = mt_for(M);
   p->waves = threads_override > 0 ? static_cast<int>(threads_override / 64) : kDefaultWaves;
+  if (p->waves > max_waves_for(p->mt))
+    return fail(NIBBLE_ERR_UNSUPPORTED, "block_threads=%lld too large for M=%lld (max %d)",
+                (long long)threads_override, (long long)M, max_waves_for(p->mt) * 64);
   p->strips = static_cast<int>(ceil_div(N, kStripCols));
   const int groups = static_cast<int>(K / G);
   int gps = groups;  // groups per split
-  if (version == 4 && splits_override > 0) {
+  if (split_k && splits_override > 0) {
     const int want = static_cast<int>(std::min<int64_t>(splits_override, groups));
     gps = std::max(1, groups / want);
-  } else if (version == 4) {
+  } else if (split_k) {
     const int want = static_cast<int>(ceil_div(groups, kGroupsPerWave * p->waves));
     gps = static_cast<int>(ceil_div(groups, std::max(1, want)));
   }
@@ -315,30 +378,43 @@ int plan_stream(int64_t M, int64_t K, int64_t N, int64_t G, int64_t version, int
   return NIBBLE_OK;
 }
 
-template <int MT, int GROUP>
-hipError_t launch_mt(const GemvArgs& a, const Plan& p, hipStream_t stream) {
-  dim3 grid(p.strips, p.splits);
-  switch (p.waves) {
-    case 1: gemv_mfma_kernel<MT, GROUP, 1><<<grid, 64, 0, stream>>>(a); break;
-    case 2: gemv_mfma_kernel<MT, GROUP, 2><<<grid, 128, 0, stream>>>(a); break;
-    case 4: gemv_mfma_kernel<MT, GROUP, 4><<<grid, 256, 0, stream>>>(a); break;
-    case 8: gemv_mfma_kernel<MT, GROUP, 8><<<grid, 512, 0, stream>>>(a); break;
-    case 16: gemv_mfma_kernel<MT, GROUP, 16><<<grid, 1024, 0, stream>>>(a); break;
-    default: return hipErrorInvalidValue;
-  }
-  return hipGetLastError();
+bool stream_supported(const void* X, const void* Wq, const void* S, const void* Y, int64_t M,
+                      int64_t K, int64_t N, int64_t G) {
+  const int64_t lim = int64_t(1) << 31;
+  return N % 4 == 0 && aligned(X, 16) && aligned(Wq, 16) && aligned(S, 8) && aligned(Y, 8) &&
+         (K / 8) * N * 4 < lim && M * K * 2 < lim && (K / G) * N * 2 < lim;
 }
 
-template <int GROUP>
-hipError_t launch_group(const GemvArgs& a, const Plan& p, hipStream_t stream) {
-  switch (p.mt) {
-    case 1: return launch_mt<1, GROUP>(a, p, stream);
-    case 2: return launch_mt<2, GROUP>(a, p, stream);
-    case 4: return launch_mt<4, GROUP>(a, p, stream);
-    default: return launch_mt<8, GROUP>(a, p, stream);
+int launch_stream(const void* X, const void* Wq, const void* S, void* Y, int64_t M, int64_t K,
+                  int64_t N, int64_t G, const StreamPlan& p, void* workspace,
+                  size_t workspace_bytes, hipStream_t stream, const char* who) {
+  if (p.workspace_bytes > 0) {
+    if (workspace == nullptr || workspace_bytes < p.workspace_bytes)
+      return fail(NIBBLE_ERR_WORKSPACE, "%s needs %zu bytes of workspace, got %zu", who,
+                  p.workspace_bytes, workspace == nullptr ? size_t(0) : workspace_bytes);
+    if (!aligned(workspace, 256))
+      return fail(NIBBLE_ERR_WORKSPACE, "workspace must be 256-byte aligned");
   }
+  GemvArgs a;
+  a.X = static_cast<const _Float16*>(X);
+  a.Wq = static_cast<const uint32_t*>(Wq);
+  a.S = static_cast<const _Float16*>(S);
+  a.Y = static_cast<_Float16*>(Y);
+  a.counters = p.splits > 1 ? static_cast<uint32_t*>(workspace) : nullptr;
+  a.partial = p.splits > 1
+                  ? reinterpret_cast<float*>(static_cast<char*>(workspace) + p.counter_bytes)
+                  : nullptr;
+  a.M = static_cast<int>(M);
+  a.K = static_cast<int>(K);
+  a.N = static_cast<int>(N);
+  a.groups_per_split = p.groups_per_split;
+  a.splits = p.splits;
+  hipError_t e = G == 128 ? launch_group<128>(a, p, stream) : launch_group<64>(a, p, stream);
+  if (e != hipSuccess) return hip_fail(e, who);
+  return NIBBLE_OK;
 }
 
+namespace {
 }  // namespace
 
 // Mirrors check_inputs (csrc/gemv_w4a16.cu:251-265) on shapes; pure host code.
@@ -389,21 +465,25 @@ int validate_gemv(const void* X, int64_t x_rows, int64_t x_cols, const void* Wq,
 using namespace nibble;
 
 namespace {
+// The streaming plan for a gemv call (versions 2-4, M <= 8).
 int gemv_plan(int64_t M, int64_t K, int64_t N, int64_t G, int64_t version, int64_t splits_override,
-              int64_t threads_override, Plan* p) {
-  return plan_stream(M, K, N, G, version, splits_override, threads_override, p);
+              int64_t threads_override, StreamPlan* p) {
+  return plan_stream(M, K, N, G, version == 4, splits_override, threads_override, p);
+}
+
+bool gemv_plannable(int64_t M, int64_t K, int64_t N, int64_t G, int64_t version) {
+  return version >= 2 && version <= 4 && M > 0 && M <= 8 && N > 0 && K > 0 &&
+         (G == 64 || G == 128) && K % G == 0;
 }
 }  // namespace
 
 extern "C" size_t nibble_gemv_workspace_bytes(int64_t M, int64_t K, int64_t N, int64_t group_size,
                                               int64_t version, int64_t splits_override,
                                               int64_t threads_override, void* stream) {
-  if (version < 2 || version > 4 || M <= 0 || M > 8 || N <= 0 || K <= 0) return 0;
-  if (group_size != 64 && group_size != 128) return 0;
-  if (K % group_size != 0) return 0;
-  Plan p;
   (void)stream;
-  if (gemv_plan(M, K, N, group_size, version, splits_override, threads_override, &p) != NIBBLE_OK)
+  StreamPlan p;
+  if (!gemv_plannable(M, K, N, group_size, version) ||
+      gemv_plan(M, K, N, group_size, version, splits_override, threads_override, &p) != NIBBLE_OK)
     return 0;
   return p.workspace_bytes;
 }
@@ -411,12 +491,10 @@ extern "C" size_t nibble_gemv_workspace_bytes(int64_t M, int64_t K, int64_t N, i
 extern "C" size_t nibble_gemv_counter_bytes(int64_t M, int64_t K, int64_t N, int64_t group_size,
                                             int64_t version, int64_t splits_override,
                                             int64_t threads_override, void* stream) {
-  if (version < 2 || version > 4 || M <= 0 || M > 8 || N <= 0 || K <= 0) return 0;
-  if (group_size != 64 && group_size != 128) return 0;
-  if (K % group_size != 0) return 0;
-  Plan p;
   (void)stream;
-  if (gemv_plan(M, K, N, group_size, version, splits_override, threads_override, &p) != NIBBLE_OK)
+  StreamPlan p;
+  if (!gemv_plannable(M, K, N, group_size, version) ||
+      gemv_plan(M, K, N, group_size, version, splits_override, threads_override, &p) != NIBBLE_OK)
     return 0;
   return p.counter_bytes;
 }
@@ -480,35 +558,13 @@ extern "C" int nibble_gemv_w4a16(const void* X, int64_t x_rows, int64_t x_cols, 
     return ok();
   }
 
-  Plan p;
+  StreamPlan p;
   rc = gemv_plan(M, K, N, group_size, version, splits_override, threads_override, &p);
   if (rc != NIBBLE_OK) return rc;
-  if (p.workspace_bytes > 0) {
-    if (workspace == nullptr || workspace_bytes < p.workspace_bytes)
-      return fail(NIBBLE_ERR_WORKSPACE, "gemv needs %zu bytes of workspace, got %zu",
-                  p.workspace_bytes, workspace == nullptr ? size_t(0) : workspace_bytes);
-    if (!aligned(workspace, 256)) return fail(NIBBLE_ERR_WORKSPACE, "workspace must be 256-byte aligned");
-  }
-
   DeviceGuard guard;
   int dev = 0;
   NIBBLE_HIP(guard.enter(stream, &dev));
-
-  GemvArgs a;
-  a.X = static_cast<const _Float16*>(X);
-  a.Wq = static_cast<const uint32_t*>(Wq);
-  a.S = static_cast<const _Float16*>(S);
-  a.Y = static_cast<_Float16*>(Y);
-  a.counters = p.splits > 1 ? static_cast<uint32_t*>(workspace) : nullptr;
-  a.partial = p.splits > 1
-                  ? reinterpret_cast<float*>(static_cast<char*>(workspace) + p.counter_bytes)
-                  : nullptr;
-  a.M = static_cast<int>(M);
-  a.K = static_cast<int>(K);
-  a.N = static_cast<int>(N);
-  a.groups_per_split = p.groups_per_split;
-  a.splits = p.splits;
-  hipError_t e = group_size == 128 ? launch_group<128>(a, p, stream) : launch_group<64>(a, p, stream);
-  if (e != hipSuccess) return hip_fail(e, "gemv kernel launch");
-  return ok();
+  rc = launch_stream(X, Wq, S, Y, M, K, N, group_size, p, workspace, workspace_bytes, stream,
+                     "gemv kernel launch");
+  return rc == NIBBLE_OK ? ok() : rc;
 }

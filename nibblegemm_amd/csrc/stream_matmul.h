@@ -1,0 +1,41 @@
+// The weight-streaming MFMA matmul (gemv.hip) as used by both entry points:
+// nibble_gemv_w4a16 (M <= 8) and nibble_gemm_w4a16 for small batches
+// (M <= kStreamMaxM), where streaming each weight once beats tiling.
+#pragma once
+
+#include "nibble_common.h"
+
+namespace nibble {
+
+constexpr int kStreamMaxM = 32;
+
+// Launch geometry.  The split-K workspace (splits > 1) is `counter_bytes` of
+// uint32 counters (zero on entry, left zero) followed by fp32 partials
+// [splits, M, N]; `workspace_bytes` is the total.
+struct StreamPlan {
+  int mt = 1;      // compiled row count: 1, 2, 4, 8, 16 or 32
+  int waves = 4;   // wave64s per workgroup
+  int strips = 0;  // 64-column strips (grid.x)
+  int splits = 1;  // K splits (grid.y)
+  int groups_per_split = 0;
+  size_t counter_bytes = 0;
+  size_t workspace_bytes = 0;
+};
+
+// Pure host arithmetic.  split_k = false forces one split (gemv versions 2
+// and 3); splits_override / threads_override of 0 mean "heuristic".
+int plan_stream(int64_t M, int64_t K, int64_t N, int64_t G, bool split_k, int64_t splits_override,
+                int64_t threads_override, StreamPlan* p);
+
+// Whether the streaming kernel can take these operands: N a multiple of 4,
+// 16-byte X and Wq, 8-byte S and Y, offsets within 31 bits.
+bool stream_supported(const void* X, const void* Wq, const void* S, const void* Y, int64_t M,
+                      int64_t K, int64_t N, int64_t G);
+
+// Checks the workspace against the plan and launches on `stream` (whose
+// device must be current).  Returns a NIBBLE_* status.
+int launch_stream(const void* X, const void* Wq, const void* S, void* Y, int64_t M, int64_t K,
+                  int64_t N, int64_t G, const StreamPlan& p, void* workspace,
+                  size_t workspace_bytes, hipStream_t stream, const char* who);
+
+}  // namespace nibble

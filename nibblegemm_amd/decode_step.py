@@ -1,0 +1,139 @@
+"""Llama-3-8B-shaped batch-1 decode step: every W4A16 projection of 32
+layers, replayed from a HIP graph (the reference's
+``bench/bench_model.py`` layers mode, :43-125).
+
+Like the reference, a step is the projections only: q, k, v, o, gate, up and
+down of every layer (224 ``matmul`` calls at M = 1), each reading activations
+allocated once outside the timed region (bench_model.py:70-86).  Unlike the
+reference, the 32 layers hold 32 *distinct* weight sets.  One INT4 layer is
+~112 MB, which the reference could replay on an A100 because it exceeds that
+part's 40 MB L2 (bench_model.py:50-56); on MI355X it would be served from the
+256 MiB Infinity Cache, so replaying one layer would not measure HBM
+streaming.
+
+Weights are random-init ``randn * 0.02`` (bench_model.py:62), RTN-quantised
+on the GPU by :func:`~nibblegemm_amd.quant.quantize_device` (bit-identical to
+the host quantiser).
+
+The fused variant concatenates q|k|v and gate|up along N
+(:func:`~nibblegemm_amd.quant.concat_columns`), so a layer is 4 launches
+instead of 7: 128 per step instead of 224.  The arithmetic is identical
+(each output column is computed from the same weights, scales and
+activations); it only removes launches.
+
+    python -m nibblegemm_amd.decode_step --layers 32
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import sys
+from typing import Dict, List, Tuple
+
+import torch
+
+from . import harness as H
+from .ops import matmul
+from .quant import QuantizedWeight, concat_columns, quantize_device
+
+LLAMA3_8B = {"hidden": 4096, "kv": 1024, "intermediate": 14336, "layers": 32}
+PROJECTIONS = ("q", "k", "v", "o", "gate", "up", "down")
+
+
+def projection_shapes(cfg=LLAMA3_8B) -> Dict[str, Tuple[int, int]]:
+    """(K, N) of every projection, consumed as ``Y = X @ W`` (bench_model.py:57-59)."""
+    h, kv, inter = cfg["hidden"], cfg["kv"], cfg["intermediate"]
+    return {"q": (h, h), "k": (h, kv), "v": (h, kv), "o": (h, h),
+            "gate": (h, inter), "up": (h, inter), "down": (inter, h)}
+
+
+def build_layers(layers: int, cfg=LLAMA3_8B, group_size: int = 128, device="cuda",
+                 seed: int = 0) -> List[Dict[str, QuantizedWeight]]:
+    """``layers`` distinct sets of RTN-quantised projections, built on the GPU."""
+    gen = torch.Generator(device=device).manual_seed(seed)
+    shapes = projection_shapes(cfg)
+    out = []
+    for _ in range(layers):
+        layer = {}
+        for name in PROJECTIONS:
+            K, N = shapes[name]
+            W = torch.randn((K, N), generator=gen, device=device, dtype=torch.float32) * 0.02
+            layer[name] = quantize_device(W, group_size)
+            del W
+        out.append(layer)
+    return out
+
+
+def fuse(layer: Dict[str, QuantizedWeight]) -> Dict[str, QuantizedWeight]:
+    """q|k|v and gate|up concatenated along N; o and down unchanged."""
+    return {"qkv": concat_columns(layer["q"], layer["k"], layer["v"]), "o": layer["o"],
+            "gate_up": concat_columns(layer["gate"], layer["up"]), "down": layer["down"]}
+
+
+def weight_bytes(layers: List[Dict[str, QuantizedWeight]]) -> int:
+    return sum(qw.weight_bytes for layer in layers for qw in layer.values())
+
+
+class DecodeStep:
+    """One step's matmul calls, with activations allocated once."""
+
+    def __init__(self, layers: List[Dict[str, QuantizedWeight]], device="cuda", seed: int = 1):
+        gen = torch.Generator(device=device).manual_seed(seed)
+        ks = sorted({qw.K for layer in layers for qw in layer.values()})
+        self.acts = {k: torch.randn((1, k), generator=gen, device=device).to(torch.float16)
+                     for k in ks}
+        self.calls = [(self.acts[qw.K], qw) for layer in layers for qw in layer.values()]
+
+    def __call__(self, _i: int = 0) -> None:
+        for x, qw in self.calls:
+            matmul(x, qw)
+
+    @property
+    def launches(self) -> int:
+        return len(self.calls)
+
+
+def measure(layers: List[Dict[str, QuantizedWeight]], trials: int = 10, warmup: int = 3) -> dict:
+    """Eager and graph-replayed time of one step, as the reference reports it
+    (bench_model.py:100-113)."""
+    step = DecodeStep(layers)
+    eager = H.bench(step, reps=1, trials=trials, warmup=warmup)
+    graph = H.bench_graph(step, reps=1, trials=trials, warmup=warmup)
+    nbytes = weight_bytes(layers)
+    return {
+        "launches": step.launches,
+        "weights_gib": round(nbytes / 2**30, 3),
+        "eager_ms": round(eager.median_ms, 4),
+        "graph_ms": round(graph.median_ms, 4),
+        "tok_s": round(1000.0 / eager.median_ms, 1),
+        "graph_tok_s": round(1000.0 / graph.median_ms, 1),
+        "graph_gbps": round(nbytes / (graph.median_ms * 1e-3) / 1e9, 1),
+    }
+
+
+def run(n_layers: int = 32, group_size: int = 128, trials: int = 10) -> dict:
+    layers = build_layers(n_layers, group_size=group_size)
+    nbytes = weight_bytes(layers)
+    res = {"config": f"Llama-3-8B shapes, {n_layers} distinct layers, g={group_size}, M=1",
+           "roofline_tok_s": round(H.HBM_PEAK_GBPS * 1e9 / nbytes, 1)}
+    res["projections"] = measure(layers, trials)
+    fused = [fuse(layer) for layer in layers]
+    res["fused"] = measure(fused, trials)
+    return res
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--layers", type=int, default=32)
+    ap.add_argument("--group-size", type=int, default=128)
+    ap.add_argument("--trials", type=int, default=10)
+    args = ap.parse_args(argv)
+    if not torch.cuda.is_available():
+        print("decode_step needs a GPU", file=sys.stderr)
+        return 1
+    print(json.dumps(run(args.layers, args.group_size, args.trials)), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

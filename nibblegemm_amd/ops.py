@@ -137,13 +137,10 @@ def _capture_id(stream: int) -> int:
     return int(cid.value) or -1
 
 
-def _gemv_workspace(ext, device: torch.device, stream: int, M: int, K: int, N: int, g: int,
-                    version: int, splits: int, threads: int) -> Tuple[Optional[torch.Tensor], int]:
-    key = (M, K, N, g, version, splits, threads, device.index)
-    plan = _ws_plan.get(key)
-    if plan is None:
-        plan = ext.gemv_workspace_bytes(M, K, N, g, version, splits, threads, stream)
-        _ws_plan[key] = plan
+def _workspace(plan: Tuple[int, int], device: torch.device,
+               stream: int) -> Tuple[Optional[torch.Tensor], int]:
+    """A zeroed buffer of at least ``plan[0]`` bytes whose leading
+    ``plan[1]`` bytes (split-K counters) are zero; None if no bytes needed."""
     nbytes, counter_bytes = plan
     if nbytes == 0:
         return None, 0
@@ -160,6 +157,26 @@ def _gemv_workspace(ext, device: torch.device, stream: int, M: int, K: int, N: i
                 buf = torch.zeros(size, dtype=torch.uint8, device=device)
                 _workspaces[wkey] = buf
     return buf, buf.numel()
+
+
+def _gemv_workspace(ext, device: torch.device, stream: int, M: int, K: int, N: int, g: int,
+                    version: int, splits: int, threads: int) -> Tuple[Optional[torch.Tensor], int]:
+    key = ("gemv", M, K, N, g, version, splits, threads)
+    plan = _ws_plan.get(key)
+    if plan is None:
+        plan = ext.gemv_workspace_bytes(M, K, N, g, version, splits, threads, stream)
+        _ws_plan[key] = plan
+    return _workspace(plan, device, stream)
+
+
+def _gemm_workspace(ext, device: torch.device, stream: int, M: int, K: int, N: int, g: int,
+                    version: int) -> Tuple[Optional[torch.Tensor], int]:
+    key = ("gemm", M, K, N, g, version)
+    plan = _ws_plan.get(key)
+    if plan is None:
+        plan = ext.gemm_workspace_bytes(M, K, N, g, version, stream)
+        _ws_plan[key] = plan
+    return _workspace(plan, device, stream)
 
 
 def dequant(qw: QuantizedWeight, fast: bool = True) -> torch.Tensor:
@@ -217,16 +234,20 @@ def gemv(X: torch.Tensor, qw: QuantizedWeight, version: int = 4, splits: int = 0
 
 def gemm(X: torch.Tensor, qw: QuantizedWeight, version: int = 6) -> torch.Tensor:
     """Prefill-regime matmul on MFMA (reference ops.py:77-86).  ``version`` 6
-    (default) or 7 select two tile shapes with identical numerics."""
+    (default) or 7 select two tile shapes with identical numerics; batches of
+    M <= 32 run the GEMV's weight-streaming kernel whatever the version."""
     ext = _bind()
     Wq, S = qw.qweight, qw.scales
     _check_matmul_inputs(X, Wq, S)
     M, K = X.shape
     N = Wq.shape[1]
     dev = X.device
+    stream = _stream(dev)
     Y = torch.empty((M, N), dtype=torch.float16, device=dev)
+    ws, ws_bytes = _gemm_workspace(ext, dev, stream, M, K, N, qw.group_size, version)
     rc = ext.gemm(X.data_ptr(), M, K, Wq.data_ptr(), Wq.shape[0], N, S.data_ptr(), S.shape[0],
-                  S.shape[1], qw.group_size, version, Y.data_ptr(), _stream(dev))
+                  S.shape[1], qw.group_size, version, Y.data_ptr(),
+                  ws.data_ptr() if ws is not None else None, ws_bytes, stream)
     if rc:
         _raise(rc, ext)
     return Y

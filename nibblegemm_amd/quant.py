@@ -92,6 +92,55 @@ def quantize(W: torch.Tensor, group_size: int = 128, clip_search: bool = False) 
     )
 
 
+def quantize_device(W: torch.Tensor, group_size: int = 128) -> QuantizedWeight:
+    """:func:`quantize` without leaving W's device: the same round-to-nearest
+    INT4 and the same packed layout, bit for bit, with ``qweight`` and
+    ``scales`` on W's device.  For building large weight stacks on the GPU
+    (the reference's ``quantize`` always returns host tensors,
+    python/nibblegemm/quant.py:154-161).
+    """
+    if W.ndim != 2:
+        raise ValueError(f"expected a 2-D weight, got shape {tuple(W.shape)}")
+    K, N = W.shape
+    if K % group_size:
+        raise ValueError(f"K={K} must be divisible by group_size={group_size}")
+    if group_size % PACK_FACTOR:
+        raise ValueError(f"group_size={group_size} must be divisible by {PACK_FACTOR}")
+
+    groups = W.detach().float().reshape(K // group_size, group_size, N)
+    amax = groups.abs().amax(dim=1)
+    # A tensor divisor, not the Python scalar 7: on the GPU a scalar divisor is
+    # applied as a multiply by its reciprocal, which can round differently
+    # from the true division the host path performs.
+    scale = (amax / torch.full_like(amax, float(QMAX))).clamp(min=1e-8)
+    q = torch.round(groups / scale.unsqueeze(1)).clamp(QMIN, QMAX)
+    qu = (q + ZERO_POINT).to(torch.int64).reshape(K // PACK_FACTOR, PACK_FACTOR, N)
+    packed = torch.zeros((K // PACK_FACTOR, N), dtype=torch.int64, device=W.device)
+    for k_off in range(PACK_FACTOR):
+        packed |= qu[:, k_off, :] << (4 * int(SLOT_FOR_K[k_off]))
+    # Words with the top bit set are the negative int32 of the same bit pattern.
+    packed = torch.where(packed >= 1 << 31, packed - (1 << 32), packed).to(torch.int32)
+    return QuantizedWeight(packed.contiguous(), scale.to(torch.float16).contiguous(),
+                           group_size, K, N)
+
+
+def concat_columns(*qws: QuantizedWeight) -> QuantizedWeight:
+    """Weights that share K and the group size, side by side as one ``[K, sum N]``
+    weight.  Packing runs along K, so concatenating packed columns and scale
+    columns gives exactly the packed form of the concatenated dense weights;
+    ``X @ concat(W1, W2)`` is ``[X @ W1, X @ W2]`` in one launch (e.g. the q, k
+    and v projections of an attention block, or gate and up of an MLP)."""
+    if not qws:
+        raise ValueError("nothing to concatenate")
+    K, g = qws[0].K, qws[0].group_size
+    for qw in qws:
+        if qw.K != K or qw.group_size != g:
+            raise ValueError("concatenated weights must share K and group_size")
+    return QuantizedWeight(torch.cat([qw.qweight for qw in qws], dim=1).contiguous(),
+                           torch.cat([qw.scales for qw in qws], dim=1).contiguous(),
+                           g, K, sum(qw.N for qw in qws))
+
+
 def pack_nibbles(qu: np.ndarray) -> np.ndarray:
     """Pack ``uint8 [K, N]`` values in ``[0, 15]`` into ``int32 [K // 8, N]``.
 

@@ -34,6 +34,7 @@ def test_header_declares_the_entry_points():
     names = set(declared_functions())
     assert {"nibble_abi_version", "nibble_last_error", "nibble_gemv_w4a16",
             "nibble_gemv_workspace_bytes", "nibble_gemv_counter_bytes", "nibble_gemm_w4a16",
+            "nibble_gemm_workspace_bytes", "nibble_gemm_counter_bytes",
             "nibble_dequant_w4"} <= names
 
 
@@ -90,6 +91,17 @@ def test_gemv_threads_override_validated():
     assert "block_threads" in ext.last_error()
 
 
+def test_gemm_workspace_formula():
+    """Batches of M <= 32 run the streaming kernel (split-K workspace as for
+    gemv); larger M needs none."""
+    ext = ng.extension()
+    assert ext.gemm_workspace_bytes(16, 14336, 4096, 128, 6, None) == (256 + 4 * 16 * 4096 * 4, 256)
+    assert ext.gemm_workspace_bytes(32, 4096, 14336, 128, 7, None) == (0, 0)
+    assert ext.gemm_workspace_bytes(33, 14336, 4096, 128, 6, None) == (0, 0)
+    assert ext.gemm_workspace_bytes(16, 14336, 4098, 128, 6, None) == (0, 0)  # N % 4: tile kernel
+    assert ext.gemm_workspace_bytes(16, 14336, 4096, 128, 5, None) == (0, 0)
+
+
 def test_gemv_workspace_formula():
     ext = ng.extension()
     # 1024 / 64 = 16 groups split 16 ways over four 64-column strips:
@@ -121,7 +133,8 @@ def gemm(ext, M, K, N, g=128, wq_rows=None, s_rows=None, s_cols=None, version=6,
     wq_rows = K // 8 if wq_rows is None else wq_rows
     s_rows = K // g if s_rows is None else s_rows
     s_cols = N if s_cols is None else s_cols
-    return ext.gemm(ptr, M, K, ptr, wq_rows, N, ptr, s_rows, s_cols, g, version, ptr, None)
+    return ext.gemm(ptr, M, K, ptr, wq_rows, N, ptr, s_rows, s_cols, g, version, ptr, None, 0,
+                    None)
 
 
 @pytest.mark.parametrize("kwargs,needle", [

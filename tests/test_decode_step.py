@@ -1,0 +1,51 @@
+"""The config-5 decode-step driver and the device quantiser it relies on."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import nibblegemm_amd as ng
+from nibblegemm_amd import decode_step as D
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("K,N,g", [(4096, 1024, 128), (512, 264, 64), (14336, 128, 128)])
+def test_quantize_device_is_bit_identical_to_the_oracle(oracle, K, N, g):
+    gen = torch.Generator().manual_seed(K + N)
+    W = torch.randn(K, N, generator=gen) * 0.02
+    W[:g, 0] = 0.0                                   # zero group
+    W[:g, 1] = torch.arange(g, dtype=torch.float32)  # exact ties after scaling
+    qw = ng.quantize_device(W.cuda(), group_size=g)
+    assert qw.qweight.is_cuda and qw.scales.is_cuda
+    qu, _, s16 = oracle.quantize_rtn(W.numpy(), g)
+    assert np.array_equal(qw.qweight.cpu().numpy(), oracle.pack_nibbles(qu))
+    assert np.array_equal(qw.scales.cpu().numpy().view(np.uint16), s16.view(np.uint16))
+
+
+def test_concatenated_gemv_equals_the_separate_ones():
+    """q|k|v and gate|up fusion: one launch over 64-column-aligned parts gives
+    the same bits per column as separate launches."""
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    parts = [ng.quantize_device(torch.randn(4096, n, generator=gen, device="cuda") * 0.02)
+             for n in (4096, 1024, 1024)]
+    x = torch.randn(1, 4096, generator=gen, device="cuda").half()
+    fused = ng.matmul(x, ng.concat_columns(*parts))
+    sep = torch.cat([ng.matmul(x, p) for p in parts], dim=1)
+    assert torch.equal(fused, sep)
+
+
+def test_decode_step_runs_and_counts_launches():
+    cfg = {"hidden": 512, "kv": 128, "intermediate": 1024, "layers": 2}
+    layers = D.build_layers(2, cfg=cfg)
+    step = D.DecodeStep(layers)
+    assert step.launches == 14
+    step()
+    fused = D.DecodeStep([D.fuse(layer) for layer in layers])
+    assert fused.launches == 8
+    fused()
+    torch.cuda.synchronize()
+    nbytes = D.weight_bytes(layers)
+    shapes = D.projection_shapes(cfg)
+    assert nbytes == 2 * sum(k * n // 2 + (k // 128) * n * 2 for k, n in shapes.values())

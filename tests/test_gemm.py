@@ -69,7 +69,7 @@ def test_versions_agree():
 
 @pytest.mark.parametrize("M", [16, 32])
 def test_small_batch_config_gemm_leg(M):
-    """BASELINE config 3 at M > 8 (the MFMA side of the handover), full size."""
+    """BASELINE config 3 at M > 8 (the GEMM side of the handover), full size."""
     X, packed, scales, Xd, qw = synthetic(M, 4096, 14336, 128, seed=200 + M)
     y = host(ng.matmul(Xd, qw))
     assert rms_err(y, oracle_y(X, packed, scales, 4096, 128)) <= RMS_TOL
@@ -117,3 +117,23 @@ def test_gemm_rejects_bad_version():
     _, _, _, Xd, qw = quantized(16, 256, 128, 128, seed=9)
     with pytest.raises(RuntimeError):
         ng.gemm(Xd, qw, version=5)
+
+
+@pytest.mark.parametrize("M", [9, 16, 24, 32, 33])
+@pytest.mark.parametrize("K_,N,g", [(4096, 1024, 128), (14336, 512, 128), (1024, 260, 64)])
+def test_small_batch_handover(M, K_, N, g):
+    """M <= 32 runs the weight-streaming kernel (split over K when K is
+    long), M = 33 the tile kernel; both against the oracle."""
+    X, packed, scales, Xd, qw = synthetic(M, K_, N, g, seed=M * 3 + N)
+    ref = oracle_y(X, packed, scales, K_, g)
+    for version in (6, 7):
+        y = host(ng.gemm(Xd, qw, version=version))
+        assert rms_err(y, ref) <= RMS_TOL, version
+        assert rel_err(y, ref) < REL_TOL, version
+
+
+def test_small_batch_split_k_is_deterministic():
+    _, _, _, Xd, qw = synthetic(24, 14336, 1024, 128, seed=77)
+    ys = [ng.gemm(Xd, qw) for _ in range(4)]
+    for y in ys[1:]:
+        assert torch.equal(y, ys[0])

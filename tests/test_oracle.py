@@ -306,3 +306,29 @@ def test_golden_fixtures_regenerate(oracle):
             assert np.array_equal(W.view(np.uint16), z[f"{name}/W"])
         Y = oracle.matmul_f16w(X, W)
         assert np.array_equal(Y.view(np.uint16), z[f"{name}/Y"])
+
+
+# --------------------------------------------------------------------------
+# the package's device-resident quantiser and column concatenation (host run)
+# --------------------------------------------------------------------------
+@pytest.mark.parametrize("g", [64, 128])
+def test_quantize_device_matches_oracle_on_host(oracle, g):
+    W = torch.randn(512, 72, generator=torch.Generator().manual_seed(g + 1)) * 0.02
+    W[:g, 3] = 0.0  # an all-zero group: scale clamps to 1e-8
+    qw = ng.quantize_device(W, group_size=g)
+    qu, _, s16 = oracle.quantize_rtn(W.numpy(), g)
+    assert np.array_equal(qw.qweight.numpy(), oracle.pack_nibbles(qu))
+    assert np.array_equal(qw.scales.numpy().view(np.uint16), s16.view(np.uint16))
+
+
+def test_concat_columns_is_the_packed_form_of_concatenated_weights(oracle):
+    parts = [ng.quantize(torch.randn(256, n, generator=torch.Generator().manual_seed(n)) * 0.02, 128)
+             for n in (64, 8, 132)]
+    cat = ng.concat_columns(*parts)
+    assert (cat.K, cat.N, cat.group_size) == (256, 204, 128)
+    want = np.concatenate([oracle.dequantize(p.qweight.numpy(), p.scales.numpy(), 256, 128)
+                           for p in parts], axis=1)
+    got = oracle.dequantize(cat.qweight.numpy(), cat.scales.numpy(), 256, 128)
+    assert np.array_equal(got.view(np.uint16), want.view(np.uint16))
+    with pytest.raises(ValueError):
+        ng.concat_columns(parts[0], ng.quantize(torch.randn(128, 8), 128))
