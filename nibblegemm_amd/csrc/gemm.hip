@@ -2,25 +2,31 @@
 //
 // Reference: csrc/gemm_w4a16.cu (tile staging :66-146, kernels :151-377, host
 // checks :379-429).  The reference decodes B into shared memory and feeds
-// wmma / mma.sync; here the tile is fed to v_mfma_f32_16x16x32_f16.
+// wmma / mma.sync; here the tile feeds v_mfma_f32_32x32x16_f16.
 //
 // Tile: BM x BN x 32 per workgroup of 4 wave64s (2 x 2), each wave owning a
-// (BM/2) x (BN/2) block of 16 x 16 MFMA tiles.  Per K step:
-//   * A (X, fp16) rows are copied global -> LDS with 16-byte loads, rows past
-//     M zero-filled;
-//   * B: every packed word is exactly 8 consecutive k of one column, i.e. one
-//     MFMA B-operand lane's worth.  Words are loaded a K step ahead into
-//     registers, decoded with the magic-exponent trick, multiplied by the group
-//     scale (one RNE rounding, so the LDS tile holds exactly dequantize()'s fp16
-//     values) and stored n-major (k contiguous) with one 16-byte store;
-//   * each wave reads its A and B operands with ds_read_b128 and issues
-//     (BM/32) x (BN/32) MFMAs with fp32 accumulation.
-// The epilogue converts to fp16 and stores with row/column masks.
+// (BM/2) x (BN/2) block of 32 x 32 MFMA tiles.  Per 32-k step:
+//   * A (X, fp16): 16-byte global loads into registers, rows past M read as
+//     zero, then stored to LDS;
+//   * B: each thread loads BN/64 adjacent packed words of one packed row (a
+//     wave covers one packed row of the tile, 4*BN contiguous bytes).  Every
+//     word is exactly 8 consecutive k of one column: it is decoded with the
+//     magic-exponent trick and multiplied by the group scale (one RNE
+//     rounding, so the LDS tile holds exactly dequantize()'s fp16 values, as
+//     the reference's does, gemm_w4a16.cu:137-146) and stored n-major
+//     (k contiguous) with one 16-byte LDS store -- one MFMA B-operand lane;
+//   * the next step's global loads are issued before the current step's
+//     MFMAs and written to the other LDS buffer after them: one barrier per
+//     step;
+//   * each wave reads its operands with ds_read_b128 (rows padded to 80 bytes,
+//     so the 8 lanes of a read phase hit distinct banks) and issues
+//     (BM/64) x (BN/64) MFMAs per 16 k with fp32 accumulation.
 //
-// MFMA operand layout (16x16x32 f16): lane l supplies row (A) / column (B)
-// l % 16 and the 8 k of block l / 16; the f32 result tile gives lane l column
-// l % 16 and rows 4 * (l / 16) + {0,1,2,3}.
+// MFMA operand layout (32x32x16 f16): lane l supplies row (A) / column (B)
+// l % 32 and the 8 k of block l / 32; result register r of lane l holds
+// column l % 32, row 8 * (r / 4) + 4 * (l / 32) + r % 4.
 #include <algorithm>
+#include <type_traits>
 
 #include "nibble_common.h"
 #include "nibble_decode.h"
@@ -30,32 +36,98 @@ namespace nibble {
 
 namespace {
 
+typedef float f16_t __attribute__((ext_vector_type(16)));
+
 constexpr int BK = 32;
-constexpr int kPad = 8;           // fp16 elements of padding per LDS row
-constexpr int LDK = BK + kPad;    // LDS row pitch in fp16 elements
-constexpr int kGemmThreads = 256; // 4 waves as 2 x 2
+constexpr int kPad = 8;            // fp16 elements of padding per LDS row
+constexpr int LDK = BK + kPad;     // LDS row pitch in fp16 elements (80 bytes)
+constexpr int kGemmThreads = 256;  // 4 waves as 2 x 2
+constexpr int kStages = 4;         // 32-k steps of global loads in flight
 
 template <int BM, int BN>
 struct TileCfg {
-  static constexpr int WM = BM / 2, WN = BN / 2;     // wave tile
-  static constexpr int FM = WM / 16, FN = WN / 16;   // MFMA tiles per wave
-  static constexpr int A_CHUNKS = BM * (BK / 8);     // 16-byte chunks of A per K step
-  static constexpr int A_ITERS = A_CHUNKS / kGemmThreads;
-  static constexpr int B_WORDS = BN * (BK / 8);      // packed words of B per K step
-  static constexpr int B_ITERS = B_WORDS / kGemmThreads;
-  static_assert(A_CHUNKS % kGemmThreads == 0, "A tile must split evenly");
-  static_assert(B_WORDS % kGemmThreads == 0, "B tile must split evenly");
+  static constexpr int WM = BM / 2, WN = BN / 2;    // wave tile
+  static constexpr int TM = WM / 32, TN = WN / 32;  // 32 x 32 MFMA tiles per wave
+  static constexpr int A_ITERS = BM * (BK / 8) / kGemmThreads;  // 16-byte A chunks per thread
+  static constexpr int VB = BN / 64;                // packed words per thread per step
+  static_assert(TM >= 1 && TN >= 1, "wave tile must hold a 32 x 32 MFMA tile");
+  static_assert(A_ITERS >= 1, "A tile must give every thread a chunk");
+  static_assert(VB == 1 || VB == 2 || VB == 4, "B words per thread");
+};
+
+// VB adjacent packed words (and their fp16 scales) of one packed row, as one
+// buffer load each.
+template <int VB>
+struct BWords;
+template <>
+struct BWords<4> {
+  using word_t = u4_t;
+  using scale_t = h4_t;
+  static __device__ __forceinline__ word_t load_w(__amdgpu_buffer_rsrc_t r, uint32_t v, uint32_t s) {
+    return __builtin_bit_cast(u4_t, __builtin_amdgcn_raw_buffer_load_b128(r, v, s, 0));
+  }
+  static __device__ __forceinline__ scale_t load_s(__amdgpu_buffer_rsrc_t r, uint32_t v, uint32_t s) {
+    return __builtin_bit_cast(h4_t, __builtin_amdgcn_raw_buffer_load_b64(r, v, s, 0));
+  }
+  static __device__ __forceinline__ uint32_t word(word_t w, int j) { return w[j]; }
+  static __device__ __forceinline__ _Float16 scale(scale_t x, int j) { return x[j]; }
+};
+template <>
+struct BWords<2> {
+  using word_t = u2_t;
+  using scale_t = h2_t;
+  static __device__ __forceinline__ word_t load_w(__amdgpu_buffer_rsrc_t r, uint32_t v, uint32_t s) {
+    return __builtin_bit_cast(u2_t, __builtin_amdgcn_raw_buffer_load_b64(r, v, s, 0));
+  }
+  static __device__ __forceinline__ scale_t load_s(__amdgpu_buffer_rsrc_t r, uint32_t v, uint32_t s) {
+    return __builtin_bit_cast(h2_t, __builtin_amdgcn_raw_buffer_load_b32(r, v, s, 0));
+  }
+  static __device__ __forceinline__ uint32_t word(word_t w, int j) { return w[j]; }
+  static __device__ __forceinline__ _Float16 scale(scale_t x, int j) { return x[j]; }
+};
+template <>
+struct BWords<1> {
+  using word_t = uint32_t;
+  using scale_t = _Float16;
+  static __device__ __forceinline__ word_t load_w(__amdgpu_buffer_rsrc_t r, uint32_t v, uint32_t s) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, v, s, 0);
+  }
+  static __device__ __forceinline__ scale_t load_s(__amdgpu_buffer_rsrc_t r, uint32_t v, uint32_t s) {
+    return __builtin_bit_cast(_Float16, __builtin_amdgcn_raw_buffer_load_b16(r, v, s, 0));
+  }
+  static __device__ __forceinline__ uint32_t word(word_t w, int) { return w; }
+  static __device__ __forceinline__ _Float16 scale(scale_t x, int) { return x; }
+};
+
+__device__ __forceinline__ f16_t mfma32(h8_t a, h8_t b, f16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+struct TileArgs {
+  const _Float16* X;
+  const uint32_t* Wq;
+  const _Float16* S;
+  _Float16* Y;
+  float* partial;      // [splits, M, N] fp32 when splits > 1
+  uint32_t* counters;  // [tiles], zero on entry and on exit
+  int M, K, N;
+  int steps_per_split;  // 32-k steps per K split
+  int splits;
 };
 
 template <int BM, int BN, int GROUP>
-__global__ __launch_bounds__(kGemmThreads) void gemm_mfma_kernel(const _Float16* __restrict__ X,
-                                                                 const uint32_t* __restrict__ Wq,
-                                                                 const _Float16* __restrict__ S,
-                                                                 _Float16* __restrict__ Y, int M,
-                                                                 int K, int N) {
+__global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(1, 2))) void
+gemm_tile_kernel(TileArgs args) {
   using C = TileCfg<BM, BN>;
-  __shared__ __attribute__((aligned(16))) _Float16 As[BM * LDK];
-  __shared__ __attribute__((aligned(16))) _Float16 Bs[BN * LDK];
+  constexpr int VB = C::VB;
+  __shared__ __attribute__((aligned(16))) _Float16 As[2][BM * LDK];
+  __shared__ __attribute__((aligned(16))) _Float16 Bs[2][BN * LDK];
+  __shared__ int s_last;
+  const _Float16* __restrict__ X = args.X;
+  const uint32_t* __restrict__ Wq = args.Wq;
+  const _Float16* __restrict__ S = args.S;
+  _Float16* __restrict__ Y = args.Y;
+  const int M = args.M, K = args.K, N = args.N;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -65,103 +137,273 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_mfma_kernel(const _Float16*
   const int m0 = blockIdx.y * BM;
   const int n0 = blockIdx.x * BN;
 
-  f4_t acc[C::FM][C::FN];
+  f16_t acc[C::TM][C::TN];
 #pragma unroll
-  for (int i = 0; i < C::FM; ++i)
+  for (int i = 0; i < C::TM; ++i)
 #pragma unroll
-    for (int j = 0; j < C::FN; ++j) acc[i][j] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < C::TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  // B prefetch registers: word and scale for each (packed row, column) this
-  // thread stages.  Element e = tid + it * threads: r8 = e / BN, c = e % BN.
-  uint32_t bq[C::B_ITERS];
-  _Float16 bs[C::B_ITERS];
-  auto prefetch_b = [&](int k0) {
-#pragma unroll
-    for (int it = 0; it < C::B_ITERS; ++it) {
-      const int e = tid + it * kGemmThreads;
-      const int r8 = e / BN, c = e % BN;
-      const int n = n0 + c;
-      const bool ok = n < N;
-      bq[it] = ok ? Wq[static_cast<size_t>(k0 / 8 + r8) * N + n] : 0u;
-      bs[it] = ok ? S[static_cast<size_t>((k0 + r8 * 8) / GROUP) * N + n] : (_Float16)0.0f;
-    }
+  // Staging registers for one 32-k step.  kStages steps are in flight at
+  // once (rotating register sets, indexed only by compile-time constants);
+  // the LDS holds two steps (the one being multiplied and the next).  All
+  // staging is in vector values (no small arrays the compiler could move to
+  // memory), and every load is an unpredicated buffer load: rows past M and
+  // columns past N use an offset outside the buffer and read zero.
+  using BVec = typename BWords<VB>::word_t;
+  using SVec = typename BWords<VB>::scale_t;
+  struct Stage {
+    h8_t a[C::A_ITERS];
+    BVec b;
+    SVec s;
   };
-  auto commit_b = [&]() {
+  // B: thread tid loads packed row (tid / 64) of the step, columns
+  // n0 + VB * (tid % 64) .. + VB - 1.
+  const int b_row = tid >> 6;
+  const int b_col = n0 + VB * (tid & 63);
+  // This workgroup's K split: steps [step0, step0 + ntiles) of 32 k.
+  const int step0 = blockIdx.z * args.steps_per_split;
+  const int ntiles = min(args.steps_per_split, K / BK - step0);
+  const uint32_t row_bytes = static_cast<uint32_t>(N) * 4u;
+  const __amdgpu_buffer_rsrc_t rx =
+      make_rsrc(X, static_cast<uint32_t>(M) * static_cast<uint32_t>(K) * 2u);
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(Wq, static_cast<uint32_t>(K / 8) * row_bytes);
+  const __amdgpu_buffer_rsrc_t rsc =
+      make_rsrc(S, static_cast<uint32_t>(K / GROUP) * static_cast<uint32_t>(N) * 2u);
+  uint32_t voff_a[C::A_ITERS];
 #pragma unroll
-    for (int it = 0; it < C::B_ITERS; ++it) {
-      const int e = tid + it * kGemmThreads;
-      const int r8 = e / BN, c = e % BN;
-      h2_t w[4];
-      const h2_t s2 = {bs[it], bs[it]};
-      decode8_scaled(bq[it], s2, w);
-      h8_t v = {w[0][0], w[0][1], w[1][0], w[1][1], w[2][0], w[2][1], w[3][0], w[3][1]};
-      *reinterpret_cast<h8_t*>(&Bs[c * LDK + r8 * 8]) = v;
-    }
+  for (int it = 0; it < C::A_ITERS; ++it) {
+    const int e = tid + it * kGemmThreads;
+    const int gm = m0 + (e >> 2);
+    voff_a[it] = gm < M ? (static_cast<uint32_t>(gm) * K + (e & 3) * 8) * 2u : kOutOfRange;
+  }
+  const bool b_ok = b_col < N;
+  const uint32_t voff_b = b_ok ? b_row * row_bytes + static_cast<uint32_t>(b_col) * 4u : kOutOfRange;
+  const uint32_t voff_s = b_ok ? static_cast<uint32_t>(b_col) * 2u : kOutOfRange;
+
+  // Loads of step `step`, clamped to the last step: a prefetch past the end
+  // re-reads it (an L2 hit) rather than being skipped, so the loads are the
+  // same on every path and the compiler's in-order wait counts stay exact.
+  auto load_step = [&](Stage& st, int step) {
+    const uint32_t k0 = static_cast<uint32_t>((step0 + min(step, ntiles - 1)) * BK);
+#pragma unroll
+    for (int it = 0; it < C::A_ITERS; ++it)
+      st.a[it] = __builtin_bit_cast(h8_t, __builtin_amdgcn_raw_buffer_load_b128(rx, voff_a[it], k0 * 2u, 0));
+    st.b = BWords<VB>::load_w(rw, voff_b, (k0 / 8) * row_bytes);
+    st.s = BWords<VB>::load_s(rsc, voff_s, (k0 / GROUP) * static_cast<uint32_t>(N) * 2u);
   };
-  auto load_a = [&](int k0) {
+  auto store_step = [&](const Stage& st, int buf) {
 #pragma unroll
     for (int it = 0; it < C::A_ITERS; ++it) {
       const int e = tid + it * kGemmThreads;
-      const int row = e / (BK / 8), col = (e % (BK / 8)) * 8;
-      const int gm = m0 + row;
-      h8_t v = {0, 0, 0, 0, 0, 0, 0, 0};
-      if (gm < M) v = *reinterpret_cast<const h8_t*>(X + static_cast<size_t>(gm) * K + k0 + col);
-      *reinterpret_cast<h8_t*>(&As[row * LDK + col]) = v;
+      const int row = e >> 2, ch = (e & 3) * 8;
+      *reinterpret_cast<h8_t*>(&As[buf][row * LDK + ch]) = st.a[it];
+    }
+    const int cl = VB * (tid & 63);
+#pragma unroll
+    for (int j = 0; j < VB; ++j) {
+      h2_t w[4];
+      const _Float16 sj = BWords<VB>::scale(st.s, j);
+      const h2_t s2 = {sj, sj};
+      decode8_scaled(BWords<VB>::word(st.b, j), s2, w);
+      const h8_t v = {w[0][0], w[0][1], w[1][0], w[1][1], w[2][0], w[2][1], w[3][0], w[3][1]};
+      *reinterpret_cast<h8_t*>(&Bs[buf][(cl + j) * LDK + b_row * 8]) = v;
+    }
+  };
+  const int r32 = lane & 31;
+  const int kq = (lane >> 5) * 8;
+  auto compute = [&](int buf) {
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      h8_t a[C::TM], b[C::TN];
+#pragma unroll
+      for (int i = 0; i < C::TM; ++i)
+        a[i] = *reinterpret_cast<const h8_t*>(&As[buf][(wm + 32 * i + r32) * LDK + 16 * ks + kq]);
+#pragma unroll
+      for (int j = 0; j < C::TN; ++j)
+        b[j] = *reinterpret_cast<const h8_t*>(&Bs[buf][(wn + 32 * j + r32) * LDK + 16 * ks + kq]);
+#pragma unroll
+      for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+        for (int j = 0; j < C::TN; ++j) acc[i][j] = mfma32(a[i], b[j], acc[i][j]);
     }
   };
 
-  const int ntiles = K / BK;
-  prefetch_b(0);
-  for (int t = 0; t < ntiles; ++t) {
-    load_a(t * BK);
-    commit_b();
-    if (t + 1 < ntiles) prefetch_b((t + 1) * BK);
+  Stage R[kStages];
+#pragma unroll
+  for (int i = 0; i < kStages; ++i) load_step(R[i], i);
+  store_step(R[0], 0);
+  __syncthreads();
+  // Step t: refill the register set that held step t (already in LDS) with
+  // step t + kStages, multiply step t from LDS, then move step t + 1 from its
+  // registers into the other LDS buffer.
+  auto iter = [&](auto u_const, int t) {
+    constexpr int u = decltype(u_const)::value;
+    load_step(R[u], t + kStages);
+    __builtin_amdgcn_sched_barrier(0);  // keep the refill ahead of the MFMAs
+    compute(t & 1);
+    __builtin_amdgcn_sched_barrier(0);
+    store_step(R[(u + 1) % kStages], (t + 1) & 1);
     __syncthreads();
-
-    const int kb = (lane >> 4) * 8;
-    const int r = lane & 15;
-    h8_t a[C::FM], b[C::FN];
-#pragma unroll
-    for (int i = 0; i < C::FM; ++i)
-      a[i] = *reinterpret_cast<const h8_t*>(&As[(wm + i * 16 + r) * LDK + kb]);
-#pragma unroll
-    for (int j = 0; j < C::FN; ++j)
-      b[j] = *reinterpret_cast<const h8_t*>(&Bs[(wn + j * 16 + r) * LDK + kb]);
-#pragma unroll
-    for (int i = 0; i < C::FM; ++i)
-#pragma unroll
-      for (int j = 0; j < C::FN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], acc[i][j], 0, 0, 0);
-    __syncthreads();
+  };
+  // Whole rounds of kStages steps with no exit in the middle (an exit after
+  // each step makes the compiler keep a copy of the accumulators per exit),
+  // then the remaining 0..kStages-1 steps once.
+  int t = 0;
+  for (; t + kStages <= ntiles; t += kStages) {
+    iter(std::integral_constant<int, 0>{}, t);
+    iter(std::integral_constant<int, 1>{}, t + 1);
+    iter(std::integral_constant<int, 2>{}, t + 2);
+    iter(std::integral_constant<int, 3>{}, t + 3);
   }
+  const int rem = ntiles - t;
+  if (rem > 0) iter(std::integral_constant<int, 0>{}, t);
+  if (rem > 1) iter(std::integral_constant<int, 1>{}, t + 1);
+  if (rem > 2) iter(std::integral_constant<int, 2>{}, t + 2);
 
-  // Epilogue: lane l holds column l % 16, rows 4 * (l / 16) + q.
-  const int col_in = lane & 15;
-  const int row_in = (lane >> 4) * 4;
+  // Epilogue: register r of lane l holds row 8*(r/4) + 4*(l/32) + r%4,
+  // column l % 32 of each 32 x 32 tile.
+  const int rq = (lane >> 5) * 4;
+  if (args.splits == 1) {
 #pragma unroll
-  for (int i = 0; i < C::FM; ++i) {
+    for (int i = 0; i < C::TM; ++i) {
 #pragma unroll
-    for (int j = 0; j < C::FN; ++j) {
-      const int gn = n0 + wn + j * 16 + col_in;
-      if (gn >= N) continue;
+      for (int j = 0; j < C::TN; ++j) {
+        const int gn = n0 + wn + 32 * j + r32;
+        if (gn >= N) continue;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int gm = m0 + wm + i * 16 + row_in + q;
-        if (gm < M) Y[static_cast<size_t>(gm) * N + gn] = (_Float16)acc[i][j][q];
+        for (int r = 0; r < 16; ++r) {
+          const int gm = m0 + wm + 32 * i + 8 * (r >> 2) + rq + (r & 3);
+          if (gm < M) Y[static_cast<size_t>(gm) * N + gn] = (_Float16)acc[i][j][r];
+        }
       }
     }
+    return;
   }
+
+  // K split: publish this split's fp32 tile with device-coherent stores; the
+  // last workgroup of the tile (agent-scope counter) sums the splits in
+  // split order and writes Y -- deterministic, one launch.
+  float* part = args.partial + static_cast<size_t>(blockIdx.z) * M * N;
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j) {
+      const int gn = n0 + wn + 32 * j + r32;
+      if (gn >= N) continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int gm = m0 + wm + 32 * i + 8 * (r >> 2) + rq + (r & 3);
+        if (gm < M) store_coherent(part + static_cast<size_t>(gm) * N + gn, acc[i][j][r]);
+      }
+    }
+  wait_vm_stores();
+  __syncthreads();
+  const int tile = blockIdx.y * gridDim.x + blockIdx.x;
+  if (tid == 0) {
+    const uint32_t prev =
+        __hip_atomic_fetch_add(args.counters + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = (prev == static_cast<uint32_t>(args.splits - 1));
+  }
+  __syncthreads();
+  if (!s_last) return;
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j) {
+      const int gn = n0 + wn + 32 * j + r32;
+      if (gn >= N) continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int gm = m0 + wm + 32 * i + 8 * (r >> 2) + rq + (r & 3);
+        if (gm >= M) continue;
+        const size_t off = static_cast<size_t>(gm) * N + gn;
+        float sum = 0.0f;
+        for (int sp = 0; sp < args.splits; ++sp)
+          sum += load_coherent(args.partial + static_cast<size_t>(sp) * M * N + off);
+        Y[off] = (_Float16)sum;
+      }
+    }
+  if (tid == 0)
+    __hip_atomic_store(args.counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int BM, int BN>
-hipError_t launch_tile(const _Float16* x, const uint32_t* w, const _Float16* s, _Float16* y,
-                       int64_t M, int64_t K, int64_t N, int64_t G, hipStream_t stream) {
-  dim3 grid(static_cast<unsigned>(ceil_div(N, BN)), static_cast<unsigned>(ceil_div(M, BM)));
+hipError_t launch_tile(const TileArgs& a, int64_t G, hipStream_t stream) {
+  dim3 grid(static_cast<unsigned>(ceil_div(a.N, BN)), static_cast<unsigned>(ceil_div(a.M, BM)),
+            static_cast<unsigned>(a.splits));
   if (G == 128)
-    gemm_mfma_kernel<BM, BN, 128><<<grid, kGemmThreads, 0, stream>>>(x, w, s, y, (int)M, (int)K, (int)N);
+    gemm_tile_kernel<BM, BN, 128><<<grid, kGemmThreads, 0, stream>>>(a);
   else
-    gemm_mfma_kernel<BM, BN, 64><<<grid, kGemmThreads, 0, stream>>>(x, w, s, y, (int)M, (int)K, (int)N);
+    gemm_tile_kernel<BM, BN, 64><<<grid, kGemmThreads, 0, stream>>>(a);
   return hipGetLastError();
+}
+
+struct TileChoice {
+  int bm, bn;
+};
+
+// Widest B vector (BN / 64 packed words per thread) the operands allow.
+int max_bn(int64_t N, const void* w, const void* s) {
+  if (N % 4 == 0 && aligned(w, 16) && aligned(s, 8)) return 256;
+  if (N % 2 == 0 && aligned(w, 8) && aligned(s, 4)) return 128;
+  return 64;
+}
+
+// The device the plans are made for: MI355X, 256 CUs.  Planning with a fixed
+// count keeps the workspace query pure host code and equal to the launch.
+constexpr int kPlanCUs = 256;
+
+// Tile choice, measured on MI355X over M = 64..2048 at 4096 x 14336 and
+// 14336 x 4096: 128 x 128 (2 waves per SIMD, so one workgroup's barrier
+// wait overlaps another's MFMAs) is fastest whenever its grid gives every CU
+// a workgroup; otherwise 64 x 128, whose doubled grid wins (e.g. 126 us vs
+// 165 us at M = 512, 14336 x 4096).  256-wide tiles, one workgroup per CU,
+// were slower at every shape.  Narrower B vectors serve N not a multiple of
+// 2 or operands without 8-byte alignment.
+TileChoice choose_tile(int64_t M, int64_t N, int bn_max) {
+  const int bn = std::min(128, bn_max);
+  if (ceil_div(M, 128) * ceil_div(N, bn) >= kPlanCUs) return {128, bn};
+  return {64, bn};
+}
+
+// Launch plan of the tile kernel.  Long reductions (K >= 8192) with few
+// output tiles split K so the grid reaches two workgroups per CU, at most 4
+// ways.  Measured at 14336 x 4096 (64 x 128 tiles): M = 128 from 126 us to
+// 70 us (4 splits), M = 512 from 129 us to 117 us (2 splits).  At K = 4096
+// every split measured slower: the partial round trip outweighs the extra
+// parallelism.
+struct TilePlan {
+  TileChoice t;
+  int splits = 1;
+  int steps_per_split = 0;
+  size_t counter_bytes = 0;
+  size_t workspace_bytes = 0;
+};
+
+TilePlan plan_tile(int64_t M, int64_t K, int64_t N, int64_t version, int bn_max) {
+  TilePlan p;
+  p.t = version == 7 ? TileChoice{128, std::min(128, bn_max)} : choose_tile(M, N, bn_max);
+  const int64_t tiles = ceil_div(M, p.t.bm) * ceil_div(N, p.t.bn);
+  const int steps = static_cast<int>(K / BK);
+  int splits = 1;
+  if (steps >= 256 && tiles < 2 * kPlanCUs)
+    splits = static_cast<int>(std::min<int64_t>(ceil_div(2 * kPlanCUs, tiles), 4));
+  p.steps_per_split = static_cast<int>(ceil_div(steps, splits));
+  p.splits = static_cast<int>(ceil_div(steps, p.steps_per_split));
+  if (p.splits > 1) {
+    p.counter_bytes = align_up(static_cast<size_t>(tiles) * 4, 256);
+    p.workspace_bytes = p.counter_bytes + static_cast<size_t>(p.splits) * M * N * 4;
+  }
+  return p;
+}
+
+hipError_t launch_choice(TileChoice t, const TileArgs& a, int64_t G, hipStream_t stream) {
+  if (t.bm == 128 && t.bn == 128) return launch_tile<128, 128>(a, G, stream);
+  if (t.bm == 64 && t.bn == 128) return launch_tile<64, 128>(a, G, stream);
+  if (t.bm == 128 && t.bn == 64) return launch_tile<128, 64>(a, G, stream);
+  return launch_tile<64, 64>(a, G, stream);
 }
 
 }  // namespace
@@ -215,24 +457,43 @@ bool gemm_streams(int64_t M, int64_t K, int64_t N, int64_t G) {
 }
 }  // namespace
 
+namespace {
+// The plan a call with these arguments runs (streaming for small batches,
+// tiles otherwise), assuming operands aligned for the widest loads.
+void gemm_plan_bytes(int64_t M, int64_t K, int64_t N, int64_t G, int64_t version, size_t* ws,
+                     size_t* counters) {
+  *ws = 0;
+  *counters = 0;
+  if ((version != 6 && version != 7) || (G != 64 && G != 128) || M <= 0 || N <= 0 || K <= 0 ||
+      K % BK != 0 || K % G != 0)
+    return;
+  if (gemm_streams(M, K, N, G)) {
+    StreamPlan p;
+    if (plan_stream(M, K, N, G, true, 0, 0, &p) != NIBBLE_OK) return;
+    *ws = p.workspace_bytes;
+    *counters = p.counter_bytes;
+    return;
+  }
+  const TilePlan p = plan_tile(M, K, N, version, N % 2 == 0 ? 128 : 64);
+  *ws = p.workspace_bytes;
+  *counters = p.counter_bytes;
+}
+}  // namespace
+
 extern "C" size_t nibble_gemm_workspace_bytes(int64_t M, int64_t K, int64_t N, int64_t group_size,
                                               int64_t version, void* stream) {
   (void)stream;
-  if ((version != 6 && version != 7) || (group_size != 64 && group_size != 128)) return 0;
-  if (!gemm_streams(M, K, N, group_size)) return 0;
-  StreamPlan p;
-  if (plan_stream(M, K, N, group_size, true, 0, 0, &p) != NIBBLE_OK) return 0;
-  return p.workspace_bytes;
+  size_t ws, counters;
+  gemm_plan_bytes(M, K, N, group_size, version, &ws, &counters);
+  return ws;
 }
 
 extern "C" size_t nibble_gemm_counter_bytes(int64_t M, int64_t K, int64_t N, int64_t group_size,
                                             int64_t version, void* stream) {
   (void)stream;
-  if ((version != 6 && version != 7) || (group_size != 64 && group_size != 128)) return 0;
-  if (!gemm_streams(M, K, N, group_size)) return 0;
-  StreamPlan p;
-  if (plan_stream(M, K, N, group_size, true, 0, 0, &p) != NIBBLE_OK) return 0;
-  return p.counter_bytes;
+  size_t ws, counters;
+  gemm_plan_bytes(M, K, N, group_size, version, &ws, &counters);
+  return counters;
 }
 
 extern "C" int nibble_gemm_w4a16(const void* X, int64_t x_rows, int64_t x_cols, const void* Wq,
@@ -261,14 +522,46 @@ extern "C" int nibble_gemm_w4a16(const void* X, int64_t x_rows, int64_t x_cols, 
     return rc == NIBBLE_OK ? ok() : rc;
   }
   const auto* x = static_cast<const _Float16*>(X);
-  const auto* w = static_cast<const uint32_t*>(Wq);
-  const auto* s = static_cast<const _Float16*>(S);
   auto* y = static_cast<_Float16*>(Y);
-  hipError_t e;
-  if (version == 7)
-    e = launch_tile<64, 128>(x, w, s, y, M, K, N, group_size, stream);
-  else
-    e = launch_tile<128, 128>(x, w, s, y, M, K, N, group_size, stream);
+  // Version 6 picks the tile for the shape; version 7 runs 128-row tiles.
+  // Every tile accumulates each output over k in the same order, so without
+  // a K split the two give identical bits (as the reference's v6 and v7 do).
+  const int bn_max = max_bn(N, Wq, S);
+  TilePlan p = plan_tile(M, K, N, version, bn_max);
+  // The kernel addresses X through a buffer resource with 32-bit offsets:
+  // tall activations are run in row blocks that stay below 2^31 bytes (such
+  // grids are far too large to need a K split).
+  const int64_t rows_max = std::max<int64_t>(256, ((int64_t(1) << 31) - 1) / (K * 2) / 256 * 256);
+  // The workspace query plans with the nominal 128-column B tiles; operands
+  // that only allow narrower ones (misaligned pointers) run without a split,
+  // as do row-blocked tall launches.
+  if (M > rows_max || bn_max < 128) p.splits = 1;
+  if (p.splits > 1) {
+    if (workspace == nullptr || workspace_bytes < p.workspace_bytes)
+      return fail(NIBBLE_ERR_WORKSPACE, "gemm needs %zu bytes of workspace, got %zu",
+                  p.workspace_bytes, workspace == nullptr ? size_t(0) : workspace_bytes);
+    if (!aligned(workspace, 256)) return fail(NIBBLE_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  } else {
+    p.steps_per_split = static_cast<int>(K / BK);
+  }
+  TileArgs a;
+  a.Wq = static_cast<const uint32_t*>(Wq);
+  a.S = static_cast<const _Float16*>(S);
+  a.K = static_cast<int>(K);
+  a.N = static_cast<int>(N);
+  a.steps_per_split = p.steps_per_split;
+  a.splits = p.splits;
+  a.counters = p.splits > 1 ? static_cast<uint32_t*>(workspace) : nullptr;
+  a.partial = p.splits > 1
+                  ? reinterpret_cast<float*>(static_cast<char*>(workspace) + p.counter_bytes)
+                  : nullptr;
+  hipError_t e = hipSuccess;
+  for (int64_t m0 = 0; m0 < M && e == hipSuccess; m0 += rows_max) {
+    a.X = x + m0 * K;
+    a.Y = y + m0 * N;
+    a.M = static_cast<int>(std::min(rows_max, M - m0));
+    e = launch_choice(p.t, a, group_size, stream);
+  }
   if (e != hipSuccess) return hip_fail(e, "gemm kernel launch");
   return ok();
 }

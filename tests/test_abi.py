@@ -93,12 +93,20 @@ def test_gemv_threads_override_validated():
 
 def test_gemm_workspace_formula():
     """Batches of M <= 32 run the streaming kernel (split-K workspace as for
-    gemv); larger M needs none."""
+    gemv); larger M runs tiles, split over K only when the tiles are few."""
     ext = ng.extension()
     assert ext.gemm_workspace_bytes(16, 14336, 4096, 128, 6, None) == (256 + 4 * 16 * 4096 * 4, 256)
     assert ext.gemm_workspace_bytes(32, 4096, 14336, 128, 7, None) == (0, 0)
-    assert ext.gemm_workspace_bytes(33, 14336, 4096, 128, 6, None) == (0, 0)
-    assert ext.gemm_workspace_bytes(16, 14336, 4098, 128, 6, None) == (0, 0)  # N % 4: tile kernel
+    # M > 32 runs 64 x 128 tiles here: 32 tiles and a long K (448 steps of
+    # 32) split 4 ways; counters padded to 256 bytes
+    assert ext.gemm_workspace_bytes(33, 14336, 4096, 128, 6, None) == (256 + 4 * 33 * 4096 * 4, 256)
+    # N % 4 != 0 cannot stream: 33 tiles of 64 x 128, split 4 ways
+    assert ext.gemm_workspace_bytes(16, 14336, 4098, 128, 6, None) == (256 + 4 * 16 * 4098 * 4, 256)
+    # M = 512 (256 tiles of 64 x 128) splits 2 ways; a short K never splits
+    assert ext.gemm_workspace_bytes(512, 14336, 4096, 128, 6, None) == (1024 + 2 * 512 * 4096 * 4, 1024)
+    assert ext.gemm_workspace_bytes(64, 4096, 14336, 128, 6, None) == (0, 0)
+    # enough tiles (M = 2048 gives 16 x 32 of 128 x 128): no split
+    assert ext.gemm_workspace_bytes(2048, 14336, 4096, 128, 6, None) == (0, 0)
     assert ext.gemm_workspace_bytes(16, 14336, 4096, 128, 5, None) == (0, 0)
 
 

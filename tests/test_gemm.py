@@ -137,3 +137,17 @@ def test_small_batch_split_k_is_deterministic():
     ys = [ng.gemm(Xd, qw) for _ in range(4)]
     for y in ys[1:]:
         assert torch.equal(y, ys[0])
+
+
+@pytest.mark.parametrize("M,K_,N", [(40, 8192, 640), (100, 14336, 256), (300, 8192, 1024),
+                                    (65, 8192, 130)])
+def test_tile_kernel_split_k(M, K_, N):
+    """Few output tiles over a long K split the reduction across workgroups
+    (deterministic last-arriver sum); both versions against the oracle."""
+    X, packed, scales, Xd, qw = synthetic(M, K_, N, 128, seed=M + K_ + N)
+    ref = oracle_y(X, packed, scales, K_, 128)
+    for version in (6, 7):
+        ys = [ng.gemm(Xd, qw, version=version) for _ in range(3)]
+        for y in ys[1:]:
+            assert torch.equal(y, ys[0]), version
+        assert rms_err(host(ys[0]), ref) <= RMS_TOL, version
