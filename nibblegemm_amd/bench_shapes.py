@@ -1,0 +1,175 @@
+"""Shape sweeps of the W4A16 kernels against their baselines on one GPU (the
+roles of the reference's bench/bench_decode.py, bench/bench_prefill.py and
+bench/autotune.py, for the BASELINE configs).
+
+    python3 -m nibblegemm_amd.bench_shapes decode      # configs 1-3: M <= 8 GEMV
+    python3 -m nibblegemm_amd.bench_shapes prefill     # configs 3-4: M = 16 .. 2048
+    python3 -m nibblegemm_amd.bench_shapes dequant     # standalone dequant
+    python3 -m nibblegemm_amd.bench_shapes crossover   # gemv vs gemm over M
+
+Every timing is a HIP-graph replay of many calls.  Each call streams its
+weights from HBM: copies of the weights rotate through at least 1 GiB, more
+than the 256 MiB Infinity Cache.  Inputs follow BASELINE's synthetic
+distributions: nibbles U{0..15}, scales U(0.002, 0.02), activations N(0, 1).
+Every measured configuration is first checked against a torch fp32
+reference, on the GPU, of the same weights (the bit-exact dequant kernel's
+output, multiplied in fp32): max |y - ref| <= 1e-2 * rms(ref), or the sweep
+stops.
+
+One JSON object per line on stdout; ``--markdown`` adds a table on stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import sys
+
+import torch
+
+from . import harness as H
+from . import ops
+from .quant import QuantizedWeight, pack_nibbles
+
+DECODE_SHAPES = [(4096, 4096), (4096, 14336), (14336, 4096), (8192, 8192), (4096, 1024)]
+PREFILL_SHAPES = [(4096, 14336), (14336, 4096)]
+TOL = 1e-2
+
+
+def _weights(K: int, N: int, G: int, seed: int):
+    gen = torch.Generator().manual_seed(seed)
+    qu = torch.randint(0, 16, (K, N), generator=gen, dtype=torch.uint8).numpy()
+    qweight = torch.from_numpy(pack_nibbles(qu)).cuda()
+    scales = (torch.rand((K // G, N), generator=gen) * 0.018 + 0.002).to(torch.float16).cuda()
+    rot = H.Rotation(qweight)
+    srot = [scales] + [scales.clone() for _ in range(rot.count - 1)]
+    qws = H.Cycle(QuantizedWeight(rot[i], srot[i], G, K, N) for i in range(rot.count))
+    return qws, gen
+
+
+def _fp16_baseline(qw: QuantizedWeight):
+    """fp16 copies of the same (dequantized) weight, rotated through >= 1 GiB."""
+    return H.Rotation(ops.dequant(qw))
+
+
+def _check(y: torch.Tensor, X: torch.Tensor, qw: QuantizedWeight, what: str) -> float:
+    ref = X.float() @ ops.dequant(qw).float()
+    err = float((y.float() - ref).abs().max() / ref.pow(2).mean().sqrt())
+    if not err <= TOL:
+        raise RuntimeError(f"{what}: max|y - ref| = {err:.3e} * rms(ref) exceeds {TOL}")
+    return err
+
+
+def _emit(rows, row):
+    rows.append(row)
+    print(json.dumps(row), flush=True)
+
+
+def decode(args, rows):
+    copy = H.measured_copy_gbps()
+    for K, N in DECODE_SHAPES:
+        qws, gen = _weights(K, N, args.group_size, seed=K + N)
+        w16 = _fp16_baseline(qws[0])
+        for M in args.M or [1, 2, 4, 8]:
+            X = torch.randn((M, K), generator=gen).to(torch.float16).cuda()
+            err = _check(ops.gemv(X, qws[0]), X, qws[0], f"gemv {M}x{K}x{N}")
+            t = H.bench_graph(lambda i: ops.gemv(X, qws[i]), reps=64, trials=args.trials)
+            f = H.bench_graph(lambda i: torch.mm(X, w16[i]), reps=64, trials=args.trials)
+            d = H.bench_graph(lambda i: torch.mm(X, ops.dequant(qws[i])), reps=8, trials=args.trials)
+            nb = H.total_bytes(M, K, N, args.group_size, 4)
+            gbps = H.achieved_gbps(nb, t.median_ms)
+            _emit(rows, {"bench": "decode", "M": M, "K": K, "N": N, "impl": "gemv v4",
+                         "us": round(t.median_ms * 1e3, 2), "GB/s": round(gbps),
+                         "%8TB/s": round(100 * gbps / H.HBM_PEAK_GBPS, 1),
+                         "%copy": round(100 * gbps / copy, 1),
+                         "hipblaslt_fp16_us": round(f.median_ms * 1e3, 2),
+                         "vs_fp16": round(f.median_ms / t.median_ms, 2),
+                         "dequant+fp16_us": round(d.median_ms * 1e3, 2),
+                         "max_err_rms": float(f"{err:.2e}")})
+        del qws, w16
+        torch.cuda.empty_cache()
+
+
+def prefill(args, rows):
+    for K, N in PREFILL_SHAPES:
+        qws, gen = _weights(K, N, args.group_size, seed=K + N)
+        w16 = _fp16_baseline(qws[0])
+        for M in args.M or [16, 32, 128, 512, 2048]:
+            X = torch.randn((M, K), generator=gen).to(torch.float16).cuda()
+            reps = 8 if M >= 512 else 32
+            f = H.bench_graph(lambda i: torch.mm(X, w16[i]), reps=reps, trials=args.trials)
+            for v in (6, 7):
+                err = _check(ops.gemm(X, qws[0], version=v), X, qws[0], f"gemm v{v} {M}x{K}x{N}")
+                t = H.bench_graph(lambda i: ops.gemm(X, qws[i], version=v), reps=reps,
+                                  trials=args.trials)
+                tf = H.tflops(M, K, N, t.median_ms)
+                _emit(rows, {"bench": "prefill", "M": M, "K": K, "N": N, "impl": f"gemm v{v}",
+                             "us": round(t.median_ms * 1e3, 2), "TFLOP/s": round(tf, 1),
+                             "%2.5PF": round(100 * tf / H.FP16_MFMA_PEAK_TFLOPS, 1),
+                             "hipblaslt_fp16_us": round(f.median_ms * 1e3, 2),
+                             "vs_fp16": round(f.median_ms / t.median_ms, 2),
+                             "max_err_rms": float(f"{err:.2e}")})
+        del qws, w16
+        torch.cuda.empty_cache()
+
+
+def dequant(args, rows):
+    copy = H.measured_copy_gbps()
+    for K, N in DECODE_SHAPES:
+        qws, _ = _weights(K, N, args.group_size, seed=K + N)
+        t = H.bench_graph(lambda i: ops.dequant(qws[i]), reps=16, trials=args.trials)
+        nb = H.dequant_bytes(K, N, args.group_size)
+        gbps = H.achieved_gbps(nb, t.median_ms)
+        _emit(rows, {"bench": "dequant", "K": K, "N": N, "impl": "dequant fast",
+                     "us": round(t.median_ms * 1e3, 2), "GB/s": round(gbps),
+                     "%8TB/s": round(100 * gbps / H.HBM_PEAK_GBPS, 1),
+                     "%copy": round(100 * gbps / copy, 1)})
+        del qws
+        torch.cuda.empty_cache()
+
+
+def crossover(args, rows):
+    K, N = 4096, 14336
+    qws, gen = _weights(K, N, args.group_size, seed=7)
+    w16 = _fp16_baseline(qws[0])
+    for M in args.M or [1, 2, 4, 8, 9, 16, 24, 32, 33, 48, 64, 96, 128]:
+        X = torch.randn((M, K), generator=gen).to(torch.float16).cuda()
+        f = H.bench_graph(lambda i: torch.mm(X, w16[i]), reps=32, trials=args.trials)
+        row = {"bench": "crossover", "M": M, "K": K, "N": N,
+               "hipblaslt_fp16_us": round(f.median_ms * 1e3, 2)}
+        if M <= ops.DECODE_MAX_M:
+            _check(ops.gemv(X, qws[0]), X, qws[0], f"gemv M={M}")
+            row["gemv_us"] = round(H.bench_graph(lambda i: ops.gemv(X, qws[i]), reps=32,
+                                                 trials=args.trials).median_ms * 1e3, 2)
+        _check(ops.gemm(X, qws[0]), X, qws[0], f"gemm M={M}")
+        row["gemm_us"] = round(H.bench_graph(lambda i: ops.gemm(X, qws[i]), reps=32,
+                                             trials=args.trials).median_ms * 1e3, 2)
+        row["matmul_us"] = min(v for k, v in row.items() if k in ("gemv_us", "gemm_us"))
+        row["vs_fp16"] = round(row["hipblaslt_fp16_us"] / row["matmul_us"], 2)
+        _emit(rows, row)
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("what", choices=["decode", "prefill", "dequant", "crossover"])
+    ap.add_argument("--M", type=int, nargs="*", help="batch sizes (default: the BASELINE configs)")
+    ap.add_argument("--group-size", type=int, default=128)
+    ap.add_argument("--trials", type=int, default=10)
+    ap.add_argument("--markdown", action="store_true")
+    args = ap.parse_args(argv)
+    if not torch.cuda.is_available():
+        print("bench_shapes needs a GPU", file=sys.stderr)
+        return 1
+    ops.extension()
+    torch.backends.cuda.matmul.allow_tf32 = False
+    print(f"# {H.device_summary()}", file=sys.stderr, flush=True)
+    rows = []
+    {"decode": decode, "prefill": prefill, "dequant": dequant, "crossover": crossover}[args.what](
+        args, rows)
+    if args.markdown and rows:
+        cols = [k for k in rows[0] if k != "bench"]
+        print(H.markdown_table(rows, cols), file=sys.stderr)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
