@@ -111,10 +111,10 @@ NIBBLE_API size_t nibble_gemv_counter_bytes(int64_t M, int64_t K, int64_t N, int
  * Prefill-regime matmul on CDNA4 MFMA (any M >= 1).  version 6 (default) or 7
  * (alternate tile shape; same numerics).  Requires K % 32 == 0, N even,
  * group_size in {64, 128} and M*N, M*K, K*N < 2^31 (the reference's checks).
- * Batches of M <= 32 (with N % 4 == 0) run the weight-streaming kernel of
- * the GEMV, which may split K: `workspace` follows the same rules as for
- * nibble_gemv_w4a16, sized by nibble_gemm_workspace_bytes(...) (0 for M > 32,
- * where it may be NULL).
+ * Batches of M <= 128 (with N % 4 == 0) run the weight-streaming kernel of
+ * the GEMV, larger ones the tile kernel; either may split K across
+ * workgroups.  `workspace` follows the same rules as for nibble_gemv_w4a16,
+ * sized by nibble_gemm_workspace_bytes(...) (NULL allowed when that is 0).
  */
 NIBBLE_API int nibble_gemm_w4a16(const void* X, int64_t x_rows, int64_t x_cols,
                       const void* Wq, int64_t wq_rows, int64_t wq_cols,

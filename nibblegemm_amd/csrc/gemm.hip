@@ -447,11 +447,12 @@ int validate_gemm(const void* X, int64_t x_rows, int64_t x_cols, const void* Wq,
 using namespace nibble;
 
 namespace {
-// Small batches go to the weight-streaming kernel: each weight byte is read
-// once and multiplied against all M rows (one or two 16-row MFMA tiles),
-// where a 64/128-row tile would leave most of the device idle and re-decode
-// the weights per row tile.  Measured on MI355X at K=4096, N=14336: M=16
-// takes 82 us through the tile kernel, ~9 us streaming.
+// Small batches go to the weight-streaming kernel: each pass reads every
+// weight byte once and multiplies it against up to 32 rows (one or two
+// 16-row MFMA tiles), where a 64/128-row tile would leave most of the device
+// idle.  Measured on MI355X at K=4096, N=14336: M=16 takes 82 us through the
+// tile kernel and 11 us streaming; M=33 38.4 us tiled; the streaming cost
+// grows ~0.2 us per row, so it stays ahead up to M=128 (39 us tiled).
 bool gemm_streams(int64_t M, int64_t K, int64_t N, int64_t G) {
   return M >= 1 && M <= kStreamMaxM && K > 0 && N > 0 && N % 4 == 0 && K % G == 0;
 }

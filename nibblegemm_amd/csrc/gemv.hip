@@ -74,6 +74,11 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int strip = blockIdx.x;
   const int split = blockIdx.y;
+  // Rows [m_base, m_base + mrows) of X and Y belong to this workgroup: one
+  // block of MT rows per grid z (batches above 32 rows run several blocks,
+  // each streaming the weights; repeats hit the Infinity Cache).
+  const int m_base = blockIdx.z * MT;
+  const int mrows = min(MT, a.M - m_base);
   const int q = lane & 15;   // B column slot (column quad) and A row within a tile
   const int kb = lane >> 4;  // 8-k block within a 32-k chunk
   const int col = strip * kStripCols + 4 * q;
@@ -91,7 +96,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs a) {
 #pragma unroll
   for (int t = 0; t < TILES; ++t) {
     const int m = 16 * t + q;
-    voff_x[t] = m < a.M ? (static_cast<uint32_t>(m) * a.K + 8u * kb) * 2u : kOutOfRange;
+    voff_x[t] = m < mrows ? (static_cast<uint32_t>(m_base + m) * a.K + 8u * kb) * 2u : kOutOfRange;
   }
 
   struct Stage {
@@ -209,7 +214,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs a) {
   for (int e = threadIdx.x; e < MT * 16; e += THREADS) {
     const int r = e >> 4, qq = e & 15;
     const int ocol = strip * kStripCols + 4 * qq;
-    if (r >= a.M || ocol >= a.N) continue;
+    if (r >= mrows || ocol >= a.N) continue;
+    const int gr = m_base + r;
     f4_t sum = red[0][r][qq];
 #pragma unroll
     for (int w = 1; w < WAVES; ++w) {
@@ -221,9 +227,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs a) {
     }
     if (direct) {
       const h4_t y = {(_Float16)sum[0], (_Float16)sum[1], (_Float16)sum[2], (_Float16)sum[3]};
-      *reinterpret_cast<h4_t*>(a.Y + static_cast<size_t>(r) * a.N + ocol) = y;
+      *reinterpret_cast<h4_t*>(a.Y + static_cast<size_t>(gr) * a.N + ocol) = y;
     } else {
-      float* dst = a.partial + (static_cast<size_t>(split) * a.M + r) * a.N + ocol;
+      float* dst = a.partial + (static_cast<size_t>(split) * a.M + gr) * a.N + ocol;
 #pragma unroll
       for (int c = 0; c < 4; ++c) store_coherent(dst + c, sum[c]);
     }
@@ -236,9 +242,10 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs a) {
   // write-back / invalidate an agent-scope fence costs on a multi-XCD device.
   wait_vm_stores();
   __syncthreads();
+  uint32_t* counter = a.counters + blockIdx.z * gridDim.x + strip;
   if (threadIdx.x == 0) {
     const uint32_t prev =
-        __hip_atomic_fetch_add(a.counters + strip, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_last = (prev == static_cast<uint32_t>(a.splits - 1));
   }
   __syncthreads();
@@ -247,18 +254,19 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs a) {
   for (int e = threadIdx.x; e < MT * 16; e += THREADS) {
     const int r = e >> 4, qq = e & 15;
     const int ocol = strip * kStripCols + 4 * qq;
-    if (r >= a.M || ocol >= a.N) continue;
+    if (r >= mrows || ocol >= a.N) continue;
+    const int gr = m_base + r;
     f4_t sum = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int sp = 0; sp < a.splits; ++sp) {
-      const float* src = a.partial + (static_cast<size_t>(sp) * a.M + r) * a.N + ocol;
+      const float* src = a.partial + (static_cast<size_t>(sp) * a.M + gr) * a.N + ocol;
 #pragma unroll
       for (int c = 0; c < 4; ++c) sum[c] += load_coherent(src + c);
     }
     const h4_t y = {(_Float16)sum[0], (_Float16)sum[1], (_Float16)sum[2], (_Float16)sum[3]};
-    *reinterpret_cast<h4_t*>(a.Y + static_cast<size_t>(r) * a.N + ocol) = y;
+    *reinterpret_cast<h4_t*>(a.Y + static_cast<size_t>(gr) * a.N + ocol) = y;
   }
   if (threadIdx.x == 0)
-    __hip_atomic_store(a.counters + strip, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Versions 0 and 1: one thread per (m, n), scalar decode, fp32 weights
@@ -309,7 +317,7 @@ constexpr int kGroupsPerWave = 8;
 
 template <int MT, int GROUP>
 hipError_t launch_mt(const GemvArgs& a, const StreamPlan& p, hipStream_t stream) {
-  dim3 grid(p.strips, p.splits);
+  dim3 grid(p.strips, p.splits, p.mblocks);
   switch (p.waves) {
     case 1: gemv_mfma_kernel<MT, GROUP, 1><<<grid, 64, 0, stream>>>(a); break;
     case 2: gemv_mfma_kernel<MT, GROUP, 2><<<grid, 128, 0, stream>>>(a); break;
@@ -350,7 +358,8 @@ int plan_stream(int64_t M, int64_t K, int64_t N, int64_t G, bool split_k, int64_
   if (M < 1 || M > kStreamMaxM || K <= 0 || N <= 0 || (G != 64 && G != 128) || K % G != 0)
     return fail(NIBBLE_ERR_INVALID_ARGUMENT, "no streaming plan for M=%lld K=%lld N=%lld G=%lld",
                 (long long)M, (long long)K, (long long)N, (long long)G);
-  p->mt = mt_for(M);
+  p->mt = mt_for(std::min<int64_t>(M, 32));
+  p->mblocks = static_cast<int>(ceil_div(M, p->mt));
   p->waves = threads_override > 0 ? static_cast<int>(threads_override / 64) : kDefaultWaves;
   if (p->waves > max_waves_for(p->mt))
     return fail(NIBBLE_ERR_UNSUPPORTED, "block_threads=%lld too large for M=%lld (max %d)",
@@ -369,7 +378,7 @@ int plan_stream(int64_t M, int64_t K, int64_t N, int64_t G, bool split_k, int64_
   p->splits = splits;
   p->groups_per_split = gps;
   if (splits > 1) {
-    p->counter_bytes = align_up(static_cast<size_t>(p->strips) * 4, 256);
+    p->counter_bytes = align_up(static_cast<size_t>(p->strips) * p->mblocks * 4, 256);
     p->workspace_bytes = p->counter_bytes + static_cast<size_t>(splits) * M * N * 4;
   } else {
     p->counter_bytes = 0;

@@ -1,19 +1,21 @@
 // The weight-streaming MFMA matmul (gemv.hip) as used by both entry points:
 // nibble_gemv_w4a16 (M <= 8) and nibble_gemm_w4a16 for small batches
-// (M <= kStreamMaxM), where streaming each weight once beats tiling.
+// (M <= kStreamMaxM), where streaming the weights beats tiling: up to 32 rows
+// share one pass over the weights, larger batches take one pass per 32 rows.
 #pragma once
 
 #include "nibble_common.h"
 
 namespace nibble {
 
-constexpr int kStreamMaxM = 32;
+constexpr int kStreamMaxM = 128;
 
 // Launch geometry.  The split-K workspace (splits > 1) is `counter_bytes` of
-// uint32 counters (zero on entry, left zero) followed by fp32 partials
-// [splits, M, N]; `workspace_bytes` is the total.
+// uint32 counters, one per (row block, strip), zero on entry and left zero,
+// followed by fp32 partials [splits, M, N]; `workspace_bytes` is the total.
 struct StreamPlan {
   int mt = 1;      // compiled row count: 1, 2, 4, 8, 16 or 32
+  int mblocks = 1; // blocks of mt rows (grid.z); more than one only above 32 rows
   int waves = 4;   // wave64s per workgroup
   int strips = 0;  // 64-column strips (grid.x)
   int splits = 1;  // K splits (grid.y)

@@ -235,7 +235,7 @@ def gemv(X: torch.Tensor, qw: QuantizedWeight, version: int = 4, splits: int = 0
 def gemm(X: torch.Tensor, qw: QuantizedWeight, version: int = 6) -> torch.Tensor:
     """Prefill-regime matmul on MFMA (reference ops.py:77-86).  ``version`` 6
     (default) or 7 select two tile shapes with identical numerics; batches of
-    M <= 32 run the GEMV's weight-streaming kernel whatever the version."""
+    M <= 128 run the GEMV's weight-streaming kernel whatever the version."""
     ext = _bind()
     Wq, S = qw.qweight, qw.scales
     _check_matmul_inputs(X, Wq, S)

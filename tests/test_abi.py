@@ -97,9 +97,12 @@ def test_gemm_workspace_formula():
     ext = ng.extension()
     assert ext.gemm_workspace_bytes(16, 14336, 4096, 128, 6, None) == (256 + 4 * 16 * 4096 * 4, 256)
     assert ext.gemm_workspace_bytes(32, 4096, 14336, 128, 7, None) == (0, 0)
-    # M > 32 runs 64 x 128 tiles here: 32 tiles and a long K (448 steps of
-    # 32) split 4 ways; counters padded to 256 bytes
-    assert ext.gemm_workspace_bytes(33, 14336, 4096, 128, 6, None) == (256 + 4 * 33 * 4096 * 4, 256)
+    # M = 33 streams in two 32-row blocks: 112 groups split 4 ways, counters
+    # for 64 strips x 2 blocks
+    assert ext.gemm_workspace_bytes(33, 14336, 4096, 128, 6, None) == (512 + 4 * 33 * 4096 * 4, 512)
+    # M > 128 runs 64 x 128 tiles here: 3 x 32 tiles and a long K (448 steps
+    # of 32) split 4 ways; counters padded to 512 bytes
+    assert ext.gemm_workspace_bytes(129, 14336, 4096, 128, 6, None) == (512 + 4 * 129 * 4096 * 4, 512)
     # N % 4 != 0 cannot stream: 33 tiles of 64 x 128, split 4 ways
     assert ext.gemm_workspace_bytes(16, 14336, 4098, 128, 6, None) == (256 + 4 * 16 * 4098 * 4, 256)
     # M = 512 (256 tiles of 64 x 128) splits 2 ways; a short K never splits

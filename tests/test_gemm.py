@@ -119,11 +119,11 @@ def test_gemm_rejects_bad_version():
         ng.gemm(Xd, qw, version=5)
 
 
-@pytest.mark.parametrize("M", [9, 16, 24, 32, 33])
+@pytest.mark.parametrize("M", [9, 16, 24, 32, 33, 64, 100, 128, 129])
 @pytest.mark.parametrize("K_,N,g", [(4096, 1024, 128), (14336, 512, 128), (1024, 260, 64)])
 def test_small_batch_handover(M, K_, N, g):
-    """M <= 32 runs the weight-streaming kernel (split over K when K is
-    long), M = 33 the tile kernel; both against the oracle."""
+    """M <= 128 runs the weight-streaming kernel (32-row blocks, split over K
+    when K is long), M = 129 the tile kernel; both against the oracle."""
     X, packed, scales, Xd, qw = synthetic(M, K_, N, g, seed=M * 3 + N)
     ref = oracle_y(X, packed, scales, K_, g)
     for version in (6, 7):
@@ -139,8 +139,8 @@ def test_small_batch_split_k_is_deterministic():
         assert torch.equal(y, ys[0])
 
 
-@pytest.mark.parametrize("M,K_,N", [(40, 8192, 640), (100, 14336, 256), (300, 8192, 1024),
-                                    (65, 8192, 130)])
+@pytest.mark.parametrize("M,K_,N", [(140, 8192, 640), (200, 14336, 256), (300, 8192, 1024),
+                                    (133, 8192, 130)])
 def test_tile_kernel_split_k(M, K_, N):
     """Few output tiles over a long K split the reduction across workgroups
     (deterministic last-arriver sum); both versions against the oracle."""
