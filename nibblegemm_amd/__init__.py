@@ -8,9 +8,11 @@ are hand-written HIP behind the C ABI in ``include/nibblegemm_amd.h``.
 
 GPTQ (``gptq_quantize``, ``quantize_model_gptq``, ``HessianAccumulator``,
 ``find_decoder_blocks``) and the Triton baseline of the reference are not part
-of this package.
+of this package.  Symmetric GPTQ / AWQ 4-bit checkpoints are ingested by
+:mod:`nibblegemm_amd.convert`.
 """
 
+from . import convert
 from .ops import DECODE_MAX_M, QuantLinear, dequant, extension, gemm, gemv, matmul
 from .quant import (
     QuantizedWeight,
@@ -28,6 +30,7 @@ __all__ = [
     "QuantLinear",
     "QuantizedWeight",
     "concat_columns",
+    "convert",
     "dequant",
     "dequantize",
     "extension",
