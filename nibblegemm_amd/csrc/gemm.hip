@@ -18,8 +18,8 @@
 //   * the next step's global loads are issued before the current step's
 //     MFMAs and written to the other LDS buffer after them: one barrier per
 //     step;
-//   * each wave reads its operands with ds_read_b128 (rows padded to 80 bytes,
-//     so the 8 lanes of a read phase hit distinct banks) and issues
+//   * each wave reads its operands with ds_read_b128 (the swizzled layout of
+//     lds_unit keeps reads and stores free of bank conflicts) and issues
 //     (BM/64) x (BN/64) MFMAs per 16 k with fp32 accumulation.
 //
 // MFMA operand layout (32x32x16 f16): lane l supplies row (A) / column (B)
@@ -39,8 +39,25 @@ namespace {
 typedef float f16_t __attribute__((ext_vector_type(16)));
 
 constexpr int BK = 32;
-constexpr int kPad = 8;            // fp16 elements of padding per LDS row
-constexpr int LDK = BK + kPad;     // LDS row pitch in fp16 elements (80 bytes)
+// LDS tile layout.  A tile row (an A row or a B column) holds BK = 32 fp16
+// as four 16-byte units, rows 64 bytes apart with no padding.  Rows are
+// permuted within aligned groups of four and the units of a row XOR-swizzled,
+// both by low row bits, so that every 16-lane phase of the three access
+// patterns touches 16 distinct units -- all 64 banks once -- (and every
+// 8-lane phase all of 32 banks once):
+//   * operand reads: 16 consecutive rows, one unit each;
+//   * A stores: 4 consecutive rows, all 4 units each;
+//   * B stores: 16 rows 1 or 2 apart (a lane's 1 or 2 adjacent columns), one
+//     unit each -- with a 64-byte pitch, rows of one parity alone cover only
+//     half the banks, hence the row permutation.
+// Found by exhaustive search over linear (XOR) maps of the row bits.
+__device__ __forceinline__ int lds_unit(int r, int c) {
+  const int p0 = (r ^ (r >> 3) ^ (r >> 4)) & 1;
+  const int p1 = ((r >> 1) ^ (r >> 3)) & 1;
+  const int f = ((r >> 1) & 1) | (((r >> 2) & 1) << 1);
+  return 4 * ((r & ~3) + p0 + 2 * p1) + (c ^ f);
+}
+constexpr int LDK = BK;  // fp16 elements per tile row
 constexpr int kGemmThreads = 256;  // 4 waves as 2 x 2
 constexpr int kStages = 4;         // 32-k steps of global loads in flight
 
@@ -193,14 +210,18 @@ gemm_tile_kernel(TileArgs args) {
     st.b = BWords<VB>::load_w(rw, voff_b, (k0 / 8) * row_bytes);
     st.s = BWords<VB>::load_s(rsc, voff_s, (k0 / GROUP) * static_cast<uint32_t>(N) * 2u);
   };
+  // LDS offsets (fp16 elements).  Rows 64 apart share the swizzle of their
+  // low 5 bits, so each offset is a per-thread constant plus a row multiple.
+  // A stores: thread tid writes row tid / 4 + 64 it, unit tid % 4.
+  const int a_st = lds_unit(tid >> 2, tid & 3) * 8;
+  // B stores: columns VB * (tid % 64) + j, unit b_row.
+  int b_st[VB];
+#pragma unroll
+  for (int j = 0; j < VB; ++j) b_st[j] = lds_unit(VB * (tid & 63) + j, b_row) * 8;
   auto store_step = [&](const Stage& st, int buf) {
 #pragma unroll
-    for (int it = 0; it < C::A_ITERS; ++it) {
-      const int e = tid + it * kGemmThreads;
-      const int row = e >> 2, ch = (e & 3) * 8;
-      *reinterpret_cast<h8_t*>(&As[buf][row * LDK + ch]) = st.a[it];
-    }
-    const int cl = VB * (tid & 63);
+    for (int it = 0; it < C::A_ITERS; ++it)
+      *reinterpret_cast<h8_t*>(&As[buf][a_st + it * 64 * LDK]) = st.a[it];
 #pragma unroll
     for (int j = 0; j < VB; ++j) {
       h2_t w[4];
@@ -208,21 +229,25 @@ gemm_tile_kernel(TileArgs args) {
       const h2_t s2 = {sj, sj};
       decode8_scaled(BWords<VB>::word(st.b, j), s2, w);
       const h8_t v = {w[0][0], w[0][1], w[1][0], w[1][1], w[2][0], w[2][1], w[3][0], w[3][1]};
-      *reinterpret_cast<h8_t*>(&Bs[buf][(cl + j) * LDK + b_row * 8]) = v;
+      *reinterpret_cast<h8_t*>(&Bs[buf][b_st[j]]) = v;
     }
   };
+  // Operand reads: row (32 i + lane % 32) of a wave's 32-row block, unit
+  // 2 ks + lane / 32 (the lane's 8 k of the 16-k MFMA step ks).
   const int r32 = lane & 31;
-  const int kq = (lane >> 5) * 8;
+  int rd[BK / 16];
+#pragma unroll
+  for (int ks = 0; ks < BK / 16; ++ks) rd[ks] = lds_unit(r32, 2 * ks + (lane >> 5)) * 8;
   auto compute = [&](int buf) {
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
       h8_t a[C::TM], b[C::TN];
 #pragma unroll
       for (int i = 0; i < C::TM; ++i)
-        a[i] = *reinterpret_cast<const h8_t*>(&As[buf][(wm + 32 * i + r32) * LDK + 16 * ks + kq]);
+        a[i] = *reinterpret_cast<const h8_t*>(&As[buf][(wm + 32 * i) * LDK + rd[ks]]);
 #pragma unroll
       for (int j = 0; j < C::TN; ++j)
-        b[j] = *reinterpret_cast<const h8_t*>(&Bs[buf][(wn + 32 * j + r32) * LDK + 16 * ks + kq]);
+        b[j] = *reinterpret_cast<const h8_t*>(&Bs[buf][(wn + 32 * j) * LDK + rd[ks]]);
 #pragma unroll
       for (int i = 0; i < C::TM; ++i)
 #pragma unroll
