@@ -354,6 +354,253 @@ gemm_tile_kernel(TileArgs args) {
     __hip_atomic_store(args.counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Epilogue of the producer/consumer kernels: the consumer waves hold the
+// results (wave block top-left (mw, nw), the tile kernel's register layout);
+// every wave passes the barriers of the K-split exchange.
+template <int TM, int TN>
+__device__ __forceinline__ void pc_epilogue(const f16_t (&acc)[TM][TN], const TileArgs& args,
+                                            bool producer, int mw, int nw, int& s_last) {
+  const int M = args.M, N = args.N;
+  const int lane = threadIdx.x & 63;
+  const int r32 = lane & 31;
+  const int rq = (lane >> 5) * 4;
+  _Float16* __restrict__ Y = args.Y;
+  if (args.splits == 1) {
+    if (producer) return;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int gn = nw + 32 * j + r32;
+        if (gn >= N) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int gm = mw + 32 * i + 8 * (r >> 2) + rq + (r & 3);
+          if (gm < M) Y[static_cast<size_t>(gm) * N + gn] = (_Float16)acc[i][j][r];
+        }
+      }
+    return;
+  }
+  float* part = args.partial + static_cast<size_t>(blockIdx.z) * M * N;
+  if (!producer) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int gn = nw + 32 * j + r32;
+        if (gn >= N) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int gm = mw + 32 * i + 8 * (r >> 2) + rq + (r & 3);
+          if (gm < M) store_coherent(part + static_cast<size_t>(gm) * N + gn, acc[i][j][r]);
+        }
+      }
+  }
+  wait_vm_stores();
+  __syncthreads();
+  const int tile = blockIdx.y * gridDim.x + blockIdx.x;
+  if (threadIdx.x == 0) {
+    const uint32_t prev =
+        __hip_atomic_fetch_add(args.counters + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = (prev == static_cast<uint32_t>(args.splits - 1));
+  }
+  __syncthreads();
+  if (!s_last || producer) return;
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int gn = nw + 32 * j + r32;
+      if (gn >= N) continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int gm = mw + 32 * i + 8 * (r >> 2) + rq + (r & 3);
+        if (gm >= M) continue;
+        const size_t off = static_cast<size_t>(gm) * N + gn;
+        float sum = 0.0f;
+        for (int sp = 0; sp < args.splits; ++sp)
+          sum += load_coherent(args.partial + static_cast<size_t>(sp) * M * N + off);
+        Y[off] = (_Float16)sum;
+      }
+    }
+  if (threadIdx.x == 0)
+    __hip_atomic_store(args.counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// LDS layout of the 64-k producer/consumer kernel: rows of 64 fp16 (eight
+// 16-byte units, 128 bytes, no padding), rows paired and XOR-swizzled by row
+// bits 0..5 so that the operand reads (16 consecutive rows, one unit),
+// A stores (2 rows x 8 units) and B stores (rows 4 apart, one unit) of every
+// 16-lane phase cover all 64 banks once (and every 8-lane phase all 32).
+__device__ __forceinline__ int lds_unit64(int r, int c) {
+  const int s0 = (r ^ (r >> 5)) & 1;
+  const int f = ((r ^ (r >> 3)) & 1) | (((r >> 1) ^ (r >> 4)) & 1) << 1 | ((r >> 2) & 1) << 2;
+  return 8 * ((r & ~1) | s0) + (c ^ f);
+}
+
+// Producer/consumer form of the tile kernel, with 64-k steps: eight waves,
+// four of each role.
+//
+// In the tile kernel above every wave loads, decodes and stores its share of
+// the next step, waits at the barrier and then multiplies, so its MFMA pipe
+// idles while it does the rest (busy about a quarter of a wave's lifetime at
+// M = 2048).  Here the four consumer waves only read operands from LDS and
+// issue MFMAs (the tile kernel's 2 x 2 arrangement and wave tiles, 16 MFMAs
+// per wave per step), while the four producer waves run the global-load
+// pipeline and the decode, storing step t + 1 into the other LDS buffer
+// while step t is multiplied.  One consumer and one producer share each
+// SIMD, so the decode VALU work and the memory waits overlap the MFMAs.  Both
+// roles pass the same barriers, ntiles + 1 of them, one per step.
+//
+// Producers: thread tid loads four 16-byte A chunks (rows tid / 8 + 32 it,
+// unit tid % 8) and one dwordx4 of B -- packed row tid / 32 of the step,
+// columns 4 (tid % 32) .. + 3 -- with its four scales.  BN = 128.
+template <int BM, int GROUP>
+__global__ __launch_bounds__(2 * kGemmThreads) void gemm_pc64_kernel(TileArgs args) {
+  constexpr int BN = 128;
+  constexpr int PBK = 64;
+  using C = TileCfg<BM, BN>;
+  constexpr int A_IT = BM * (PBK / 8) / kGemmThreads;
+  __shared__ __attribute__((aligned(16))) _Float16 As[2][BM * PBK];
+  __shared__ __attribute__((aligned(16))) _Float16 Bs[2][BN * PBK];
+  __shared__ int s_last;
+  const int M = args.M, K = args.K, N = args.N;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+  const bool producer = wave >= 4;
+  const int tid = static_cast<int>(threadIdx.x) & (kGemmThreads - 1);
+  const int lane = tid & 63;
+  const int m0 = blockIdx.y * BM;
+  const int n0 = blockIdx.x * BN;
+  const int step0 = blockIdx.z * args.steps_per_split;
+  const int ntiles = min(args.steps_per_split, K / PBK - step0);
+  const int wm = ((wave & 3) >> 1) * C::WM;
+  const int wn = (wave & 1) * C::WN;
+  const int r32 = lane & 31;
+
+  f16_t acc[C::TM][C::TN];
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  if (producer) {
+    struct Stage {
+      h8_t a[A_IT];
+      u4_t b;
+      h4_t s;
+    };
+    const int prow = tid >> 5;
+    const int b_col = n0 + 4 * (tid & 31);
+    const uint32_t row_bytes = static_cast<uint32_t>(N) * 4u;
+    const __amdgpu_buffer_rsrc_t rx =
+        make_rsrc(args.X, static_cast<uint32_t>(M) * static_cast<uint32_t>(K) * 2u);
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(args.Wq, static_cast<uint32_t>(K / 8) * row_bytes);
+    const __amdgpu_buffer_rsrc_t rsc =
+        make_rsrc(args.S, static_cast<uint32_t>(K / GROUP) * static_cast<uint32_t>(N) * 2u);
+    uint32_t voff_a[A_IT];
+    int a_st[A_IT];
+#pragma unroll
+    for (int it = 0; it < A_IT; ++it) {
+      const int row = (tid >> 3) + 32 * it;
+      const int gm = m0 + row;
+      voff_a[it] = gm < M ? (static_cast<uint32_t>(gm) * K + (tid & 7) * 8) * 2u : kOutOfRange;
+      a_st[it] = lds_unit64(row, tid & 7) * 8;
+    }
+    const bool b_ok = b_col < N;  // N % 4 == 0: the quad is wholly inside or outside
+    const uint32_t voff_b = b_ok ? prow * row_bytes + static_cast<uint32_t>(b_col) * 4u : kOutOfRange;
+    const uint32_t voff_s = b_ok ? static_cast<uint32_t>(b_col) * 2u : kOutOfRange;
+    int b_st[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) b_st[j] = lds_unit64(4 * (tid & 31) + j, prow) * 8;
+    auto load_step = [&](Stage& st, int step) {
+      const uint32_t k0 = static_cast<uint32_t>((step0 + min(step, ntiles - 1)) * PBK);
+#pragma unroll
+      for (int it = 0; it < A_IT; ++it)
+        st.a[it] = __builtin_bit_cast(
+            h8_t, __builtin_amdgcn_raw_buffer_load_b128(rx, voff_a[it], k0 * 2u, 0));
+      st.b = __builtin_bit_cast(
+          u4_t, __builtin_amdgcn_raw_buffer_load_b128(rw, voff_b, (k0 / 8) * row_bytes, 0));
+      st.s = __builtin_bit_cast(
+          h4_t, __builtin_amdgcn_raw_buffer_load_b64(
+                    rsc, voff_s, (k0 / GROUP) * static_cast<uint32_t>(N) * 2u, 0));
+    };
+    auto store_step = [&](const Stage& st, int buf) {
+#pragma unroll
+      for (int it = 0; it < A_IT; ++it) *reinterpret_cast<h8_t*>(&As[buf][a_st[it]]) = st.a[it];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        h2_t w[4];
+        const h2_t s2 = {st.s[j], st.s[j]};
+        decode8_scaled(st.b[j], s2, w);
+        const h8_t v = {w[0][0], w[0][1], w[1][0], w[1][1], w[2][0], w[2][1], w[3][0], w[3][1]};
+        *reinterpret_cast<h8_t*>(&Bs[buf][b_st[j]]) = v;
+      }
+    };
+    Stage R[kStages];
+#pragma unroll
+    for (int i = 0; i < kStages; ++i) load_step(R[i], i);
+    auto piter = [&](auto u_const, int i) {
+      constexpr int u = decltype(u_const)::value;
+      store_step(R[u], u & 1);
+      load_step(R[u], i + kStages);
+      __syncthreads();
+    };
+    int i = 0;
+    for (; i + kStages <= ntiles; i += kStages) {
+      piter(std::integral_constant<int, 0>{}, i);
+      piter(std::integral_constant<int, 1>{}, i + 1);
+      piter(std::integral_constant<int, 2>{}, i + 2);
+      piter(std::integral_constant<int, 3>{}, i + 3);
+    }
+    const int rem = ntiles - i;
+    if (rem > 0) piter(std::integral_constant<int, 0>{}, i);
+    if (rem > 1) piter(std::integral_constant<int, 1>{}, i + 1);
+    if (rem > 2) piter(std::integral_constant<int, 2>{}, i + 2);
+    __syncthreads();
+  } else {
+    int rda[C::TM][PBK / 16], rdb[C::TN][PBK / 16];
+#pragma unroll
+    for (int ks = 0; ks < PBK / 16; ++ks) {
+#pragma unroll
+      for (int i = 0; i < C::TM; ++i) rda[i][ks] = lds_unit64(wm + 32 * i + r32, 2 * ks + (lane >> 5)) * 8;
+#pragma unroll
+      for (int j = 0; j < C::TN; ++j) rdb[j][ks] = lds_unit64(wn + 32 * j + r32, 2 * ks + (lane >> 5)) * 8;
+    }
+    __syncthreads();
+    for (int t = 0; t < ntiles; ++t) {
+      const int buf = t & 1;
+#pragma unroll
+      for (int ks = 0; ks < PBK / 16; ++ks) {
+        h8_t a[C::TM], b[C::TN];
+#pragma unroll
+        for (int i = 0; i < C::TM; ++i) a[i] = *reinterpret_cast<const h8_t*>(&As[buf][rda[i][ks]]);
+#pragma unroll
+        for (int j = 0; j < C::TN; ++j) b[j] = *reinterpret_cast<const h8_t*>(&Bs[buf][rdb[j][ks]]);
+#pragma unroll
+        for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+          for (int j = 0; j < C::TN; ++j) acc[i][j] = mfma32(a[i], b[j], acc[i][j]);
+      }
+      __syncthreads();
+    }
+  }
+  pc_epilogue<C::TM, C::TN>(acc, args, producer, m0 + wm, n0 + wn, s_last);
+}
+
+template <int BM>
+hipError_t launch_pc64(const TileArgs& a, int64_t G, hipStream_t stream) {
+  dim3 grid(static_cast<unsigned>(ceil_div(a.N, 128)), static_cast<unsigned>(ceil_div(a.M, BM)),
+            static_cast<unsigned>(a.splits));
+  if (G == 128)
+    gemm_pc64_kernel<BM, 128><<<grid, 2 * kGemmThreads, 0, stream>>>(a);
+  else
+    gemm_pc64_kernel<BM, 64><<<grid, 2 * kGemmThreads, 0, stream>>>(a);
+  return hipGetLastError();
+}
+
+
 template <int BM, int BN>
 hipError_t launch_tile(const TileArgs& a, int64_t G, hipStream_t stream) {
   dim3 grid(static_cast<unsigned>(ceil_div(a.N, BN)), static_cast<unsigned>(ceil_div(a.M, BM)),
@@ -367,7 +614,15 @@ hipError_t launch_tile(const TileArgs& a, int64_t G, hipStream_t stream) {
 
 struct TileChoice {
   int bm, bn;
+  bool pc = false;  // the producer/consumer kernel (BN = 128, 64-k steps)
 };
+
+// The widest B vector aligned operands of this N allow (the plan the
+// workspace query assumes).
+int nominal_bn_max(int64_t N) { return N % 4 == 0 ? 256 : N % 2 == 0 ? 128 : 64; }
+
+// k per pipeline step of the kernel a choice runs.
+int step_k(TileChoice t) { return t.pc ? 64 : BK; }
 
 // Widest B vector (BN / 64 packed words per thread) the operands allow.
 int max_bn(int64_t N, const void* w, const void* s) {
@@ -410,10 +665,13 @@ struct TilePlan {
 TilePlan plan_tile(int64_t M, int64_t K, int64_t N, int64_t version, int bn_max) {
   TilePlan p;
   p.t = version == 7 ? TileChoice{128, std::min(128, bn_max)} : choose_tile(M, N, bn_max);
+  // The producer/consumer kernel wherever it applies: whole 64-k steps and
+  // 16-byte packed-word loads.
+  if (K % 64 == 0 && bn_max >= 256) p.t = TileChoice{p.t.bm, 128, true};
   const int64_t tiles = ceil_div(M, p.t.bm) * ceil_div(N, p.t.bn);
-  const int steps = static_cast<int>(K / BK);
+  const int steps = static_cast<int>(K / step_k(p.t));
   int splits = 1;
-  if (steps >= 256 && tiles < 2 * kPlanCUs)
+  if (K >= 8192 && tiles < 2 * kPlanCUs)
     splits = static_cast<int>(std::min<int64_t>(ceil_div(2 * kPlanCUs, tiles), 4));
   p.steps_per_split = static_cast<int>(ceil_div(steps, splits));
   p.splits = static_cast<int>(ceil_div(steps, p.steps_per_split));
@@ -425,6 +683,7 @@ TilePlan plan_tile(int64_t M, int64_t K, int64_t N, int64_t version, int bn_max)
 }
 
 hipError_t launch_choice(TileChoice t, const TileArgs& a, int64_t G, hipStream_t stream) {
+  if (t.pc) return t.bm == 128 ? launch_pc64<128>(a, G, stream) : launch_pc64<64>(a, G, stream);
   if (t.bm == 128 && t.bn == 128) return launch_tile<128, 128>(a, G, stream);
   if (t.bm == 64 && t.bn == 128) return launch_tile<64, 128>(a, G, stream);
   if (t.bm == 128 && t.bn == 64) return launch_tile<128, 64>(a, G, stream);
@@ -500,7 +759,7 @@ void gemm_plan_bytes(int64_t M, int64_t K, int64_t N, int64_t G, int64_t version
     *counters = p.counter_bytes;
     return;
   }
-  const TilePlan p = plan_tile(M, K, N, version, N % 2 == 0 ? 128 : 64);
+  const TilePlan p = plan_tile(M, K, N, version, nominal_bn_max(N));
   *ws = p.workspace_bytes;
   *counters = p.counter_bytes;
 }
@@ -558,17 +817,19 @@ extern "C" int nibble_gemm_w4a16(const void* X, int64_t x_rows, int64_t x_cols, 
   // tall activations are run in row blocks that stay below 2^31 bytes (such
   // grids are far too large to need a K split).
   const int64_t rows_max = std::max<int64_t>(256, ((int64_t(1) << 31) - 1) / (K * 2) / 256 * 256);
-  // The workspace query plans with the nominal 128-column B tiles; operands
-  // that only allow narrower ones (misaligned pointers) run without a split,
-  // as do row-blocked tall launches.
-  if (M > rows_max || bn_max < 128) p.splits = 1;
+  // The workspace query plans for aligned operands; when the pointers force
+  // another kernel than that plan's, the call runs without a split, as do
+  // row-blocked tall launches.
+  const TilePlan nominal = plan_tile(M, K, N, version, nominal_bn_max(N));
+  if (M > rows_max || p.t.pc != nominal.t.pc || p.t.bm != nominal.t.bm || p.t.bn != nominal.t.bn)
+    p.splits = 1;
   if (p.splits > 1) {
     if (workspace == nullptr || workspace_bytes < p.workspace_bytes)
       return fail(NIBBLE_ERR_WORKSPACE, "gemm needs %zu bytes of workspace, got %zu",
                   p.workspace_bytes, workspace == nullptr ? size_t(0) : workspace_bytes);
     if (!aligned(workspace, 256)) return fail(NIBBLE_ERR_WORKSPACE, "workspace must be 256-byte aligned");
   } else {
-    p.steps_per_split = static_cast<int>(K / BK);
+    p.steps_per_split = static_cast<int>(K / step_k(p.t));
   }
   TileArgs a;
   a.Wq = static_cast<const uint32_t*>(Wq);

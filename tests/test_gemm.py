@@ -151,3 +151,42 @@ def test_tile_kernel_split_k(M, K_, N):
         for y in ys[1:]:
             assert torch.equal(y, ys[0]), version
         assert rms_err(host(ys[0]), ref) <= RMS_TOL, version
+
+
+@pytest.mark.parametrize("M,K_,N,g", [(129, 320, 132, 64), (257, 576, 260, 64), (1000, 128, 4100, 128),
+                                      (300, 8256, 516, 64), (192, 4096, 640, 128)])
+def test_producer_consumer_kernel_edges(M, K_, N, g):
+    """Shapes for the 64-k producer/consumer kernel: row and column tails of
+    its 64/128-row, 128-column tiles, odd numbers of 64-k steps, group 64 and
+    a K split (K >= 8192)."""
+    X, packed, scales, Xd, qw = synthetic(M, K_, N, g, seed=M + K_ + N)
+    ref = oracle_y(X, packed, scales, K_, g)
+    for version in (6, 7):
+        ys = [ng.gemm(Xd, qw, version=version) for _ in range(2)]
+        assert torch.equal(ys[0], ys[1]), version
+        assert rms_err(host(ys[0]), ref) <= RMS_TOL, version
+        assert rel_err(host(ys[0]), ref) < REL_TOL, version
+
+
+def _offset_copy(t: torch.Tensor, elems: int) -> torch.Tensor:
+    """A contiguous copy of ``t`` starting ``elems`` elements into a larger buffer."""
+    buf = torch.empty(t.numel() + elems, dtype=t.dtype, device=t.device)
+    out = buf[elems:].view(t.shape)
+    out.copy_(t)
+    return out
+
+
+@pytest.mark.parametrize("M,K_,N", [(300, 512, 260), (600, 1024, 512)])
+def test_gemm_under_aligned_weights(M, K_, N):
+    """Weights only 8-byte (packed) / 4-byte (scales) aligned cannot take the
+    producer/consumer kernel's 16-byte loads and run the tile kernel; both
+    sum every output over k in the same order, so without a K split the bits
+    agree."""
+    X, packed, scales, Xd, qw = synthetic(M, K_, N, 128, seed=M + N)
+    qw_off = ng.QuantizedWeight(_offset_copy(qw.qweight, 2), _offset_copy(qw.scales, 2),
+                                qw.group_size, qw.K, qw.N)
+    assert qw_off.qweight.data_ptr() % 16 == 8
+    y = ng.gemm(Xd, qw)
+    y_off = ng.gemm(Xd, qw_off)
+    assert torch.equal(y, y_off)
+    assert rms_err(host(y_off), oracle_y(X, packed, scales, K_, 128)) <= RMS_TOL
