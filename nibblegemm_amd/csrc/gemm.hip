@@ -664,15 +664,28 @@ struct TilePlan {
 
 TilePlan plan_tile(int64_t M, int64_t K, int64_t N, int64_t version, int bn_max) {
   TilePlan p;
-  p.t = version == 7 ? TileChoice{128, std::min(128, bn_max)} : choose_tile(M, N, bn_max);
-  // The producer/consumer kernel wherever it applies: whole 64-k steps and
-  // 16-byte packed-word loads.
-  if (K % 64 == 0 && bn_max >= 256) p.t = TileChoice{p.t.bm, 128, true};
-  const int64_t tiles = ceil_div(M, p.t.bm) * ceil_div(N, p.t.bn);
-  const int steps = static_cast<int>(K / step_k(p.t));
+  int64_t tiles = 0;
   int splits = 1;
-  if (K >= 8192 && tiles < 2 * kPlanCUs)
-    splits = static_cast<int>(std::min<int64_t>(ceil_div(2 * kPlanCUs, tiles), 4));
+  if (K % 64 == 0 && bn_max >= 256) {
+    // The producer/consumer kernel wherever it applies (whole 64-k steps,
+    // 16-byte packed-word loads).  Measured on MI355X over M = 160..2048 at
+    // 4096 x 14336 and 14336 x 4096: 128-row tiles win once the launch has
+    // ~192 of them (4096 x 14336 from M = 160, 14336 x 4096 from M = 768),
+    // 64-row tiles below; a K split pays only for long K with at most 128
+    // tiles, two ways there (M = 160 at 14336 x 4096: 75 -> 64 us), while
+    // more splits, or splits of larger grids, lose to the partial exchange.
+    const int64_t t128 = ceil_div(M, 128) * ceil_div(N, 128);
+    p.t = TileChoice{version == 7 || t128 >= 192 ? 128 : 64, 128, true};
+    tiles = ceil_div(M, p.t.bm) * ceil_div(N, 128);
+    if (K >= 8192 && tiles <= 128)
+      splits = static_cast<int>(std::min<int64_t>(ceil_div(192, tiles), 4));
+  } else {
+    p.t = version == 7 ? TileChoice{128, std::min(128, bn_max)} : choose_tile(M, N, bn_max);
+    tiles = ceil_div(M, p.t.bm) * ceil_div(N, p.t.bn);
+    if (K >= 8192 && tiles < 2 * kPlanCUs)
+      splits = static_cast<int>(std::min<int64_t>(ceil_div(2 * kPlanCUs, tiles), 4));
+  }
+  const int steps = static_cast<int>(K / step_k(p.t));
   p.steps_per_split = static_cast<int>(ceil_div(steps, splits));
   p.splits = static_cast<int>(ceil_div(steps, p.steps_per_split));
   if (p.splits > 1) {

@@ -92,7 +92,7 @@ def test_gemv_threads_override_validated():
 
 
 def test_gemm_workspace_formula():
-    """Batches of M <= 32 run the streaming kernel (split-K workspace as for
+    """Batches of M <= 128 run the streaming kernel (split-K workspace as for
     gemv); larger M runs tiles, split over K only when the tiles are few."""
     ext = ng.extension()
     assert ext.gemm_workspace_bytes(16, 14336, 4096, 128, 6, None) == (256 + 4 * 16 * 4096 * 4, 256)
@@ -100,13 +100,17 @@ def test_gemm_workspace_formula():
     # M = 33 streams in two 32-row blocks: 112 groups split 4 ways, counters
     # for 64 strips x 2 blocks
     assert ext.gemm_workspace_bytes(33, 14336, 4096, 128, 6, None) == (512 + 4 * 33 * 4096 * 4, 512)
-    # M > 128 runs 64 x 128 tiles here: 3 x 32 tiles and a long K (448 steps
-    # of 32) split 4 ways; counters padded to 512 bytes
-    assert ext.gemm_workspace_bytes(129, 14336, 4096, 128, 6, None) == (512 + 4 * 129 * 4096 * 4, 512)
-    # N % 4 != 0 cannot stream: 33 tiles of 64 x 128, split 4 ways
+    # M > 128 runs the producer/consumer kernel: 64 x 128 tiles here (2 x 32
+    # of 128 x 128 would be too few), 3 x 32 = 96 of them over a long K (224
+    # steps of 64) split 2 ways; counters padded to 512 bytes
+    assert ext.gemm_workspace_bytes(129, 14336, 4096, 128, 6, None) == (512 + 2 * 129 * 4096 * 4, 512)
+    # version 7 keeps 128 x 128 tiles: 2 x 32 = 64 of them, split 3 ways
+    assert ext.gemm_workspace_bytes(129, 14336, 4096, 128, 7, None) == (256 + 3 * 129 * 4096 * 4, 256)
+    # N % 4 != 0 cannot stream nor take 16-byte B loads: the tile kernel, 33
+    # tiles of 64 x 128, split 4 ways
     assert ext.gemm_workspace_bytes(16, 14336, 4098, 128, 6, None) == (256 + 4 * 16 * 4098 * 4, 256)
-    # M = 512 (256 tiles of 64 x 128) splits 2 ways; a short K never splits
-    assert ext.gemm_workspace_bytes(512, 14336, 4096, 128, 6, None) == (1024 + 2 * 512 * 4096 * 4, 1024)
+    # M = 512: 256 tiles of 64 x 128, enough not to split; a short K never splits
+    assert ext.gemm_workspace_bytes(512, 14336, 4096, 128, 6, None) == (0, 0)
     assert ext.gemm_workspace_bytes(64, 4096, 14336, 128, 6, None) == (0, 0)
     # enough tiles (M = 2048 gives 16 x 32 of 128 x 128): no split
     assert ext.gemm_workspace_bytes(2048, 14336, 4096, 128, 6, None) == (0, 0)
