@@ -4,6 +4,11 @@
 // checks :379-429).  The reference decodes B into shared memory and feeds
 // wmma / mma.sync; here the tile feeds v_mfma_f32_32x32x16_f16.
 //
+// Two kernels share the tile arithmetic.  gemm_pc64_kernel (further down)
+// runs wherever its 16-byte B loads apply: four waves multiply while four
+// others load and decode the next 64-k step.  gemm_tile_kernel, described
+// here, serves the remaining operands (N % 4 != 0, under-aligned weights).
+//
 // Tile: BM x BN x 32 per workgroup of 4 wave64s (2 x 2), each wave owning a
 // (BM/2) x (BN/2) block of 32 x 32 MFMA tiles.  Per 32-k step:
 //   * A (X, fp16): 16-byte global loads into registers, rows past M read as
