@@ -50,7 +50,7 @@
 extern "C" {
 #endif
 
-#define NIBBLE_ABI_VERSION 2
+#define NIBBLE_ABI_VERSION 3
 
 #if defined(__GNUC__) || defined(__clang__)
 #define NIBBLE_API __attribute__((visibility("default")))
@@ -128,6 +128,34 @@ NIBBLE_API size_t nibble_gemm_workspace_bytes(int64_t M, int64_t K, int64_t N, i
                                    int64_t version, void* stream);
 NIBBLE_API size_t nibble_gemm_counter_bytes(int64_t M, int64_t K, int64_t N, int64_t group_size,
                                  int64_t version, void* stream);
+
+/*
+ * Streaming matmul (1 <= M <= 128) with a fused output epilogue.  No
+ * counterpart in the reference: its QuantLinear adds the bias as a separate
+ * fp16 op (python/nibblegemm/ops.py:131-135), and gate/up activations run as
+ * separate ops after the matmul.  For callers that want one launch per
+ * layer projection (decode steps, HIP graphs):
+ *   epilogue 0  Y [M, N] = X @ W, as nibble_gemm_w4a16 writes it;
+ *   epilogue 1  Y [M, N] = fp16(fp16(X @ W) + bias), bias fp16 [N] -- the
+ *               same bits as the separate fp16 add;
+ *   epilogue 2  W is [gate | up] interleaved in 32-column blocks (N a
+ *               multiple of 64, nibblegemm_amd.quant.interleave_swiglu);
+ *               Y [M, N/2] = silu(G) * U with G, U and silu(G) rounded to
+ *               fp16 as the unfused fp16 ops would.
+ * Requires N % 4 == 0, group_size in {64, 128}, X and Wq 16-byte and S, Y
+ * 8-byte aligned (NIBBLE_ERR_INVALID_ARGUMENT otherwise; there is no other
+ * kernel to fall back to).  `workspace` as for nibble_gemv_w4a16, sized by
+ * nibble_matmul_fused_workspace_bytes(...).
+ */
+NIBBLE_API int nibble_matmul_w4a16_fused(const void* X, int64_t x_rows, int64_t x_cols,
+                      const void* Wq, int64_t wq_rows, int64_t wq_cols,
+                      const void* S, int64_t s_rows, int64_t s_cols,
+                      int64_t group_size, int64_t epilogue, const void* bias, void* Y,
+                      void* workspace, size_t workspace_bytes, void* stream);
+NIBBLE_API size_t nibble_matmul_fused_workspace_bytes(int64_t M, int64_t K, int64_t N,
+                                           int64_t group_size, void* stream);
+NIBBLE_API size_t nibble_matmul_fused_counter_bytes(int64_t M, int64_t K, int64_t N,
+                                         int64_t group_size, void* stream);
 
 /*
  * Dense fp16 W [K, N] from packed weights, bit-exact with the reference's

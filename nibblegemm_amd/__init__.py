@@ -13,11 +13,13 @@ of this package.  Symmetric GPTQ / AWQ 4-bit checkpoints are ingested by
 """
 
 from . import convert
-from .ops import DECODE_MAX_M, QuantLinear, dequant, extension, gemm, gemv, matmul
+from .ops import (DECODE_MAX_M, QuantLinear, dequant, extension, gemm, gemv, matmul, matmul_bias,
+                  matmul_swiglu)
 from .quant import (
     QuantizedWeight,
     concat_columns,
     dequantize,
+    interleave_swiglu,
     pack_nibbles,
     quantize,
     quantize_device,
@@ -36,7 +38,10 @@ __all__ = [
     "extension",
     "gemm",
     "gemv",
+    "interleave_swiglu",
     "matmul",
+    "matmul_bias",
+    "matmul_swiglu",
     "pack_nibbles",
     "quantize",
     "quantize_device",

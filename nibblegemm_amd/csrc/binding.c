@@ -99,6 +99,38 @@ static PyObject* py_gemm_ws(PyObject* self, PyObject* const* a, Py_ssize_t n) {
   return Py_BuildValue("(nn)", (Py_ssize_t)ws, (Py_ssize_t)cb);
 }
 
+/* matmul_fused(X, xr, xc, Wq, wr, wc, S, sr, sc, g, epilogue, bias, Y, ws, ws_bytes, stream) */
+static PyObject* py_fused(PyObject* self, PyObject* const* a, Py_ssize_t n) {
+  (void)self;
+  if (!nargs_is(n, 16, "matmul_fused")) return NULL;
+  void *X, *Wq, *S, *bias, *Y, *ws, *stream;
+  long long xr, xc, wr, wc, sr, sc, g, ep, wsb;
+  if (!take_ptr(a[0], &X) || !take_i64(a[1], &xr) || !take_i64(a[2], &xc) ||
+      !take_ptr(a[3], &Wq) || !take_i64(a[4], &wr) || !take_i64(a[5], &wc) ||
+      !take_ptr(a[6], &S) || !take_i64(a[7], &sr) || !take_i64(a[8], &sc) ||
+      !take_i64(a[9], &g) || !take_i64(a[10], &ep) || !take_ptr(a[11], &bias) ||
+      !take_ptr(a[12], &Y) || !take_ptr(a[13], &ws) || !take_i64(a[14], &wsb) ||
+      !take_ptr(a[15], &stream))
+    return NULL;
+  int rc = nibble_matmul_w4a16_fused(X, xr, xc, Wq, wr, wc, S, sr, sc, g, ep, bias, Y, ws,
+                                     (size_t)(wsb < 0 ? 0 : wsb), stream);
+  return PyLong_FromLong(rc);
+}
+
+/* matmul_fused_workspace_bytes(M, K, N, g, stream) */
+static PyObject* py_fused_ws(PyObject* self, PyObject* const* a, Py_ssize_t n) {
+  (void)self;
+  if (!nargs_is(n, 5, "matmul_fused_workspace_bytes")) return NULL;
+  long long M, K, N, g;
+  void* stream;
+  if (!take_i64(a[0], &M) || !take_i64(a[1], &K) || !take_i64(a[2], &N) || !take_i64(a[3], &g) ||
+      !take_ptr(a[4], &stream))
+    return NULL;
+  size_t ws = nibble_matmul_fused_workspace_bytes(M, K, N, g, stream);
+  size_t cb = nibble_matmul_fused_counter_bytes(M, K, N, g, stream);
+  return Py_BuildValue("(nn)", (Py_ssize_t)ws, (Py_ssize_t)cb);
+}
+
 /* dequant(Wq, wr, wc, S, sr, sc, g, fast, W, stream) */
 static PyObject* py_dequant(PyObject* self, PyObject* const* a, Py_ssize_t n) {
   (void)self;
@@ -134,6 +166,10 @@ static PyMethodDef kMethods[] = {
     {"gemm_workspace_bytes", (PyCFunction)(void (*)(void))py_gemm_ws, METH_FASTCALL,
      "(nibble_gemm_workspace_bytes, nibble_gemm_counter_bytes)"},
     {"dequant", (PyCFunction)(void (*)(void))py_dequant, METH_FASTCALL, "nibble_dequant_w4"},
+    {"matmul_fused", (PyCFunction)(void (*)(void))py_fused, METH_FASTCALL,
+     "nibble_matmul_w4a16_fused"},
+    {"matmul_fused_workspace_bytes", (PyCFunction)(void (*)(void))py_fused_ws, METH_FASTCALL,
+     "nibble_matmul_fused_workspace_bytes / nibble_matmul_fused_counter_bytes"},
     {"last_error", py_last_error, METH_NOARGS, "nibble_last_error"},
     {"abi_version", py_abi_version, METH_NOARGS, "nibble_abi_version"},
     {NULL, NULL, 0, NULL}};

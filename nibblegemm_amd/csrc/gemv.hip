@@ -55,10 +55,62 @@ struct GemvArgs {
   int M, K, N;
   int groups_per_split;
   int splits;
+  int epilogue;           // kEpilogueNone / kEpilogueBias / kEpilogueSwiglu
+  const _Float16* bias;   // [N] for kEpilogueBias
 };
+
+// Output epilogues of the streaming kernel (fused forms of what a caller
+// would otherwise run as separate elementwise kernels on the fp16 result).
+constexpr int kEpilogueNone = 0;
+constexpr int kEpilogueBias = 1;    // Y = fp16(fp16(X W) + bias)
+constexpr int kEpilogueSwiglu = 2;  // W = [gate | up] in 32-column blocks; Y = silu(G) * U
+
+// The fp16 arithmetic of the unfused composition, step by step: the two
+// products rounded to fp16, silu(g) = g / (1 + e^-g) evaluated in fp32 and
+// rounded, then the fp32 product of the two fp16 values (rounded at the
+// store).
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  const float g16 = static_cast<float>(static_cast<_Float16>(g));
+  const float u16 = static_cast<float>(static_cast<_Float16>(u));
+  const float s16 = static_cast<float>(static_cast<_Float16>(g16 / (1.0f + expf(-g16))));
+  return s16 * u16;
+}
 
 __device__ __forceinline__ f4_t mfma16(h8_t a, h8_t b, f4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// Writes a strip's outputs from `total(r, qq)`, the fp32 sums of column quad
+// qq of row r, through the launch's epilogue.
+template <int MT, int THREADS, typename Total>
+__device__ __forceinline__ void emit_outputs(const GemvArgs& a, int strip, int m_base, int mrows,
+                                             Total total) {
+  if (a.epilogue == kEpilogueSwiglu) {
+    const int nout = a.N / 2;
+    for (int e = threadIdx.x; e < MT * 8; e += THREADS) {
+      const int r = e >> 3, qq = e & 7;
+      const int ocol = strip * (kStripCols / 2) + 4 * qq;
+      if (r >= mrows || ocol >= nout) continue;
+      const f4_t g = total(r, qq), u = total(r, qq + 8);
+      const h4_t y = {(_Float16)silu_mul(g[0], u[0]), (_Float16)silu_mul(g[1], u[1]),
+                      (_Float16)silu_mul(g[2], u[2]), (_Float16)silu_mul(g[3], u[3])};
+      *reinterpret_cast<h4_t*>(a.Y + static_cast<size_t>(m_base + r) * nout + ocol) = y;
+    }
+    return;
+  }
+  for (int e = threadIdx.x; e < MT * 16; e += THREADS) {
+    const int r = e >> 4, qq = e & 15;
+    const int ocol = strip * kStripCols + 4 * qq;
+    if (r >= mrows || ocol >= a.N) continue;
+    const f4_t sum = total(r, qq);
+    h4_t y = {(_Float16)sum[0], (_Float16)sum[1], (_Float16)sum[2], (_Float16)sum[3]};
+    if (a.epilogue == kEpilogueBias) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        y[c] = (_Float16)(static_cast<float>(y[c]) + static_cast<float>(a.bias[ocol + c]));
+    }
+    *reinterpret_cast<h4_t*>(a.Y + static_cast<size_t>(m_base + r) * a.N + ocol) = y;
+  }
 }
 
 template <int MT, int GROUP, int WAVES>
@@ -209,13 +261,11 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs a) {
     }
   __syncthreads();
 
-  // Thread e of the workgroup owns (row e / 16, column quad e % 16).
+  // Thread e of the workgroup owns (row e / 16, column quad e % 16) -- or,
+  // with the SwiGLU epilogue, (row e / 8, output quad e % 8), reading gate
+  // quad e % 8 and up quad e % 8 + 8 of the strip.
   const bool direct = a.splits == 1;
-  for (int e = threadIdx.x; e < MT * 16; e += THREADS) {
-    const int r = e >> 4, qq = e & 15;
-    const int ocol = strip * kStripCols + 4 * qq;
-    if (r >= mrows || ocol >= a.N) continue;
-    const int gr = m_base + r;
+  auto wave_sum = [&](int r, int qq) {
     f4_t sum = red[0][r][qq];
 #pragma unroll
     for (int w = 1; w < WAVES; ++w) {
@@ -225,16 +275,22 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs a) {
       sum[2] += v[2];
       sum[3] += v[3];
     }
-    if (direct) {
-      const h4_t y = {(_Float16)sum[0], (_Float16)sum[1], (_Float16)sum[2], (_Float16)sum[3]};
-      *reinterpret_cast<h4_t*>(a.Y + static_cast<size_t>(gr) * a.N + ocol) = y;
-    } else {
-      float* dst = a.partial + (static_cast<size_t>(split) * a.M + gr) * a.N + ocol;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) store_coherent(dst + c, sum[c]);
-    }
+    return sum;
+  };
+  if (direct) {
+    emit_outputs<MT, THREADS>(a, strip, m_base, mrows, wave_sum);
+    return;
   }
-  if (direct) return;
+  for (int e = threadIdx.x; e < MT * 16; e += THREADS) {
+    const int r = e >> 4, qq = e & 15;
+    const int ocol = strip * kStripCols + 4 * qq;
+    if (r >= mrows || ocol >= a.N) continue;
+    const int gr = m_base + r;
+    const f4_t sum = wave_sum(r, qq);
+    float* dst = a.partial + (static_cast<size_t>(split) * a.M + gr) * a.N + ocol;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) store_coherent(dst + c, sum[c]);
+  }
 
   // Publish this split's partial; the last workgroup of the strip reduces.
   // The partials were written with device-coherent stores; waiting for them
@@ -251,20 +307,17 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs a) {
   __syncthreads();
   if (!s_last) return;
 
-  for (int e = threadIdx.x; e < MT * 16; e += THREADS) {
-    const int r = e >> 4, qq = e & 15;
+  auto split_sum = [&](int r, int qq) {
     const int ocol = strip * kStripCols + 4 * qq;
-    if (r >= mrows || ocol >= a.N) continue;
-    const int gr = m_base + r;
     f4_t sum = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int sp = 0; sp < a.splits; ++sp) {
-      const float* src = a.partial + (static_cast<size_t>(sp) * a.M + gr) * a.N + ocol;
+      const float* src = a.partial + (static_cast<size_t>(sp) * a.M + m_base + r) * a.N + ocol;
 #pragma unroll
       for (int c = 0; c < 4; ++c) sum[c] += load_coherent(src + c);
     }
-    const h4_t y = {(_Float16)sum[0], (_Float16)sum[1], (_Float16)sum[2], (_Float16)sum[3]};
-    *reinterpret_cast<h4_t*>(a.Y + static_cast<size_t>(gr) * a.N + ocol) = y;
-  }
+    return sum;
+  };
+  emit_outputs<MT, THREADS>(a, strip, m_base, mrows, split_sum);
   if (threadIdx.x == 0)
     __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -396,7 +449,8 @@ bool stream_supported(const void* X, const void* Wq, const void* S, const void* 
 
 int launch_stream(const void* X, const void* Wq, const void* S, void* Y, int64_t M, int64_t K,
                   int64_t N, int64_t G, const StreamPlan& p, void* workspace,
-                  size_t workspace_bytes, hipStream_t stream, const char* who) {
+                  size_t workspace_bytes, hipStream_t stream, const char* who, int epilogue,
+                  const void* bias) {
   if (p.workspace_bytes > 0) {
     if (workspace == nullptr || workspace_bytes < p.workspace_bytes)
       return fail(NIBBLE_ERR_WORKSPACE, "%s needs %zu bytes of workspace, got %zu", who,
@@ -418,6 +472,8 @@ int launch_stream(const void* X, const void* Wq, const void* S, void* Y, int64_t
   a.N = static_cast<int>(N);
   a.groups_per_split = p.groups_per_split;
   a.splits = p.splits;
+  a.epilogue = epilogue;
+  a.bias = static_cast<const _Float16*>(bias);
   hipError_t e = G == 128 ? launch_group<128>(a, p, stream) : launch_group<64>(a, p, stream);
   if (e != hipSuccess) return hip_fail(e, who);
   return NIBBLE_OK;
@@ -575,5 +631,82 @@ extern "C" int nibble_gemv_w4a16(const void* X, int64_t x_rows, int64_t x_cols, 
   NIBBLE_HIP(guard.enter(stream, &dev));
   rc = launch_stream(X, Wq, S, Y, M, K, N, group_size, p, workspace, workspace_bytes, stream,
                      "gemv kernel launch");
+  return rc == NIBBLE_OK ? ok() : rc;
+}
+
+// ---------------------------------------------------------------------------
+// Streaming matmul with a fused output epilogue (no counterpart in the
+// reference, whose QuantLinear adds the bias as a separate fp16 op,
+// python/nibblegemm/ops.py:131-135).
+
+namespace {
+int validate_fused(const void* X, int64_t x_rows, int64_t x_cols, const void* Wq, int64_t wq_rows,
+                   int64_t wq_cols, const void* S, int64_t s_rows, int64_t s_cols,
+                   int64_t group_size, int64_t epilogue, const void* bias, const void* Y) {
+  NIBBLE_CHECK(x_rows >= 0 && x_cols > 0 && wq_rows >= 0 && wq_cols > 0 && s_rows >= 0 && s_cols >= 0,
+               "bad dimension (K and N must be positive)");
+  const int64_t M = x_rows, K = x_cols, N = wq_cols;
+  NIBBLE_CHECK(M <= kStreamMaxM, "fused matmul supports M <= %d, got %lld", kStreamMaxM,
+               (long long)M);
+  NIBBLE_CHECK(wq_rows * 8 == K, "packed weight rows disagree with K");
+  NIBBLE_CHECK(group_size == 64 || group_size == 128, "group_size must be 64 or 128");
+  NIBBLE_CHECK(s_rows * group_size == K, "scale rows disagree with K/group_size");
+  NIBBLE_CHECK(s_cols == N, "scale columns disagree with N");
+  NIBBLE_CHECK(N % 4 == 0, "N must be a multiple of 4");
+  NIBBLE_CHECK(epilogue == kEpilogueNone || epilogue == kEpilogueBias ||
+                   epilogue == kEpilogueSwiglu,
+               "epilogue must be 0 (none), 1 (bias) or 2 (swiglu), got %lld", (long long)epilogue);
+  NIBBLE_CHECK(epilogue != kEpilogueSwiglu || N % kStripCols == 0,
+               "swiglu needs N (gate|up interleaved in 32-column blocks) to be a multiple of 64");
+  NIBBLE_CHECK(epilogue != kEpilogueBias || M == 0 || bias != nullptr, "null bias");
+  NIBBLE_CHECK(epilogue != kEpilogueBias || aligned(bias, 2), "misaligned bias");
+  if (M == 0) return NIBBLE_OK;
+  NIBBLE_CHECK(X != nullptr && Wq != nullptr && S != nullptr && Y != nullptr, "null pointer");
+  NIBBLE_CHECK(stream_supported(X, Wq, S, Y, M, K, N, group_size),
+               "operands must be aligned (X, Wq 16-byte; S, Y 8-byte) and within 32-bit offsets");
+  return NIBBLE_OK;
+}
+}  // namespace
+
+extern "C" size_t nibble_matmul_fused_workspace_bytes(int64_t M, int64_t K, int64_t N,
+                                                      int64_t group_size, void* stream) {
+  (void)stream;
+  StreamPlan p;
+  if (M < 1 || M > kStreamMaxM || K <= 0 || N <= 0 || (group_size != 64 && group_size != 128) ||
+      K % group_size != 0 || plan_stream(M, K, N, group_size, true, 0, 0, &p) != NIBBLE_OK)
+    return 0;
+  return p.workspace_bytes;
+}
+
+extern "C" size_t nibble_matmul_fused_counter_bytes(int64_t M, int64_t K, int64_t N,
+                                                    int64_t group_size, void* stream) {
+  (void)stream;
+  StreamPlan p;
+  if (M < 1 || M > kStreamMaxM || K <= 0 || N <= 0 || (group_size != 64 && group_size != 128) ||
+      K % group_size != 0 || plan_stream(M, K, N, group_size, true, 0, 0, &p) != NIBBLE_OK)
+    return 0;
+  return p.counter_bytes;
+}
+
+extern "C" int nibble_matmul_w4a16_fused(const void* X, int64_t x_rows, int64_t x_cols,
+                                         const void* Wq, int64_t wq_rows, int64_t wq_cols,
+                                         const void* S, int64_t s_rows, int64_t s_cols,
+                                         int64_t group_size, int64_t epilogue, const void* bias,
+                                         void* Y, void* workspace, size_t workspace_bytes,
+                                         void* stream_) {
+  int rc = validate_fused(X, x_rows, x_cols, Wq, wq_rows, wq_cols, S, s_rows, s_cols, group_size,
+                          epilogue, bias, Y);
+  if (rc != NIBBLE_OK) return rc;
+  const int64_t M = x_rows, K = x_cols, N = wq_cols;
+  if (M == 0) return ok();
+  StreamPlan p;
+  rc = plan_stream(M, K, N, group_size, true, 0, 0, &p);
+  if (rc != NIBBLE_OK) return rc;
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  DeviceGuard guard;
+  int dev = 0;
+  NIBBLE_HIP(guard.enter(stream, &dev));
+  rc = launch_stream(X, Wq, S, Y, M, K, N, group_size, p, workspace, workspace_bytes, stream,
+                     "fused matmul kernel launch", static_cast<int>(epilogue), bias);
   return rc == NIBBLE_OK ? ok() : rc;
 }

@@ -35,9 +35,12 @@ bool stream_supported(const void* X, const void* Wq, const void* S, const void* 
                       int64_t K, int64_t N, int64_t G);
 
 // Checks the workspace against the plan and launches on `stream` (whose
-// device must be current).  Returns a NIBBLE_* status.
+// device must be current).  `epilogue` 0 writes X W; 1 adds `bias` ([N]
+// fp16) in fp16; 2 reads W as gate|up interleaved in 32-column blocks and
+// writes silu(gate) * up ([M, N/2]).  Returns a NIBBLE_* status.
 int launch_stream(const void* X, const void* Wq, const void* S, void* Y, int64_t M, int64_t K,
                   int64_t N, int64_t G, const StreamPlan& p, void* workspace,
-                  size_t workspace_bytes, hipStream_t stream, const char* who);
+                  size_t workspace_bytes, hipStream_t stream, const char* who, int epilogue = 0,
+                  const void* bias = nullptr);
 
 }  // namespace nibble

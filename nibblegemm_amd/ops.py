@@ -27,7 +27,7 @@ from typing import Dict, Optional, Tuple
 import torch
 
 from . import _native
-from .quant import QuantizedWeight, quantize  # noqa: F401  (re-exported)
+from .quant import SWIGLU_BLOCK, QuantizedWeight, quantize, split_swiglu  # noqa: F401
 
 #: Batch sizes at or below this go to the bandwidth-bound decode kernel
 #: (reference ops.py:30).
@@ -266,6 +266,81 @@ def matmul(X: torch.Tensor, qw: QuantizedWeight, splits: int = 0,
     return gemm(X, qw)
 
 
+#: Largest batch the fused-epilogue entry point takes (the streaming kernel's).
+FUSED_MAX_M = 128
+
+
+def _fused_workspace(ext, device: torch.device, stream: int, M: int, K: int, N: int,
+                     g: int) -> Tuple[Optional[torch.Tensor], int]:
+    key = ("fused", M, K, N, g)
+    plan = _ws_plan.get(key)
+    if plan is None:
+        plan = ext.matmul_fused_workspace_bytes(M, K, N, g, stream)
+        _ws_plan[key] = plan
+    return _workspace(plan, device, stream)
+
+
+def _fusable(X: torch.Tensor, qw: QuantizedWeight) -> bool:
+    """Whether the fused-epilogue launch takes these operands (else the
+    caller composes the same arithmetic from separate ops)."""
+    return (X.dim() == 2 and X.is_cuda and 1 <= X.size(0) <= FUSED_MAX_M and qw.N % 4 == 0
+            and X.is_contiguous() and X.data_ptr() % 16 == 0
+            and qw.qweight.data_ptr() % 16 == 0 and qw.scales.data_ptr() % 8 == 0)
+
+
+def _fused(X: torch.Tensor, qw: QuantizedWeight, epilogue: int, bias: Optional[torch.Tensor],
+           n_out: int) -> torch.Tensor:
+    ext = _bind()
+    Wq, S = qw.qweight, qw.scales
+    _check_matmul_inputs(X, Wq, S)
+    M, K = X.shape
+    N = Wq.shape[1]
+    dev = X.device
+    stream = _stream(dev)
+    Y = torch.empty((M, n_out), dtype=torch.float16, device=dev)
+    ws, ws_bytes = _fused_workspace(ext, dev, stream, M, K, N, qw.group_size)
+    rc = ext.matmul_fused(X.data_ptr(), M, K, Wq.data_ptr(), Wq.shape[0], N, S.data_ptr(),
+                          S.shape[0], S.shape[1], qw.group_size, epilogue,
+                          bias.data_ptr() if bias is not None else None, Y.data_ptr(),
+                          ws.data_ptr() if ws is not None else None, ws_bytes, stream)
+    if rc:
+        _raise(rc, ext)
+    return Y
+
+
+def _check_2d(X: torch.Tensor, qw: QuantizedWeight) -> None:
+    if X.dim() != 2:
+        raise ValueError(f"expected a 2-D activation matrix, got {tuple(X.shape)}")
+    if X.size(1) != qw.K:
+        raise ValueError(f"K mismatch: activations have {X.size(1)}, weights have {qw.K}")
+
+
+def matmul_bias(X: torch.Tensor, qw: QuantizedWeight, bias: torch.Tensor) -> torch.Tensor:
+    """``matmul(X, qw) + bias`` -- the arithmetic of the reference's
+    ``QuantLinear`` with a bias (ops.py:131-135): the fp16 product, then the
+    bias added in fp16.  An fp16 bias with M <= 128 runs as one launch (the
+    bias added in the kernel's epilogue, same bits); other cases run the two
+    ops."""
+    _check_2d(X, qw)
+    if (bias.dtype == torch.float16 and bias.dim() == 1 and bias.numel() == qw.N
+            and bias.device == X.device and bias.is_contiguous() and _fusable(X, qw)):
+        return _fused(X, qw, 1, bias, qw.N)
+    return matmul(X, qw) + bias
+
+
+def matmul_swiglu(X: torch.Tensor, qw: QuantizedWeight) -> torch.Tensor:
+    """``silu(X @ W_gate) * (X @ W_up)`` for ``qw = interleave_swiglu(gate,
+    up)``, with the fp16 roundings of the unfused ops (the two products,
+    silu, then the product).  M <= 128 runs as one launch."""
+    _check_2d(X, qw)
+    if qw.N % (2 * SWIGLU_BLOCK):
+        raise ValueError(f"N={qw.N} is not an interleaved gate|up weight (multiple of 64)")
+    if _fusable(X, qw):
+        return _fused(X, qw, 2, None, qw.N // 2)
+    gate, up = split_swiglu(matmul(X, qw))
+    return torch.nn.functional.silu(gate) * up
+
+
 class QuantLinear(torch.nn.Module):
     """Drop-in replacement for ``nn.Linear`` with INT4 weights (reference
     ops.py:107-135).  Buffers ``qweight``, ``scales`` and ``bias`` keep the
@@ -290,6 +365,9 @@ class QuantLinear(torch.nn.Module):
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         shape = x.shape
-        y = matmul(x.reshape(-1, shape[-1]).contiguous(), self._qw())
-        y = y.reshape(*shape[:-1], self.N)
-        return y + self.bias if self.bias is not None else y
+        x2 = x.reshape(-1, shape[-1]).contiguous()
+        if self.bias is None:
+            y = matmul(x2, self._qw())
+        else:
+            y = matmul_bias(x2, self._qw(), self.bias)
+        return y.reshape(*shape[:-1], self.N)

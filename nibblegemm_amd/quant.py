@@ -141,6 +141,42 @@ def concat_columns(*qws: QuantizedWeight) -> QuantizedWeight:
                            g, K, sum(qw.N for qw in qws))
 
 
+#: Column block of :func:`interleave_swiglu` (half of the kernels' 64-column strip).
+SWIGLU_BLOCK = 32
+
+
+def interleave_swiglu(gate: QuantizedWeight, up: QuantizedWeight) -> QuantizedWeight:
+    """The gate and up projections of a SwiGLU MLP as one ``[K, 2N]`` weight
+    whose columns alternate in blocks of 32: gate 0..31, up 0..31, gate
+    32..63, ...  Every 64-column strip of the kernels then holds matching
+    gate and up columns, which lets one launch write ``silu(X Wg) * (X Wu)``
+    (``ops.matmul_swiglu``).  Packing runs along K, so permuting packed and
+    scale columns is exact."""
+    if gate.K != up.K or gate.group_size != up.group_size or gate.N != up.N:
+        raise ValueError("gate and up must share K, N and group_size")
+    if gate.N % SWIGLU_BLOCK:
+        raise ValueError(f"N={gate.N} must be a multiple of {SWIGLU_BLOCK}")
+
+    def mix(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+        rows, n = a.shape
+        blocks = n // SWIGLU_BLOCK
+        return torch.stack([a.reshape(rows, blocks, SWIGLU_BLOCK),
+                            b.reshape(rows, blocks, SWIGLU_BLOCK)], dim=2).reshape(rows, 2 * n)
+
+    return QuantizedWeight(mix(gate.qweight, up.qweight).contiguous(),
+                           mix(gate.scales, up.scales).contiguous(),
+                           gate.group_size, gate.K, 2 * gate.N)
+
+
+def split_swiglu(y: torch.Tensor):
+    """Inverse column order of :func:`interleave_swiglu` on a ``[M, 2N]``
+    output: returns the gate and up halves, each ``[M, N]``."""
+    rows, n2 = y.shape
+    blocks = n2 // (2 * SWIGLU_BLOCK)
+    v = y.reshape(rows, blocks, 2, SWIGLU_BLOCK)
+    return (v[:, :, 0, :].reshape(rows, n2 // 2), v[:, :, 1, :].reshape(rows, n2 // 2))
+
+
 def pack_nibbles(qu: np.ndarray) -> np.ndarray:
     """Pack ``uint8 [K, N]`` values in ``[0, 15]`` into ``int32 [K // 8, N]``.
 

@@ -241,3 +241,41 @@ def test_extension_exposes_the_reference_module_functions():
         ext.gemv_w4a16(X, qw.qweight, qw.scales, 128)
     with pytest.raises(RuntimeError, match="GPU"):
         ext.dequant_w4(qw.qweight, qw.scales, 128)
+
+
+def fused(ext, M, K, N, g=128, epilogue=1, bias=P, wq_rows=None, s_rows=None, s_cols=None, ptr=P):
+    wq_rows = K // 8 if wq_rows is None else wq_rows
+    s_rows = K // g if s_rows is None else s_rows
+    s_cols = N if s_cols is None else s_cols
+    return ext.matmul_fused(ptr, M, K, ptr, wq_rows, N, ptr, s_rows, s_cols, g, epilogue, bias, ptr,
+                            None, 0, None)
+
+
+@pytest.mark.parametrize("kwargs,needle", [
+    (dict(M=129, K=256, N=128), "M <= 128"),
+    (dict(M=4, K=256, N=128, epilogue=3), "epilogue"),
+    (dict(M=4, K=256, N=96, epilogue=2), "multiple of 64"),
+    (dict(M=4, K=256, N=130, epilogue=0), "multiple of 4"),
+    (dict(M=4, K=256, N=128, bias=None), "null bias"),
+    (dict(M=4, K=256, N=128, wq_rows=31), "packed weight rows"),
+    (dict(M=4, K=256, N=128, s_cols=132), "scale columns"),
+    (dict(M=4, K=0, N=128), "K and N must be positive"),
+    (dict(M=4, K=256, N=128, ptr=P + 8), "aligned"),
+])
+def test_fused_rejections(kwargs, needle):
+    ext = ng.extension()
+    assert fused(ext, **kwargs) == INVALID
+    assert needle in ext.last_error()
+
+
+def test_fused_workspace_matches_streaming_plan():
+    """The fused entry runs the streaming kernel's plan: the same workspace as
+    nibble_gemm_w4a16 for M <= 128 (and as nibble_gemv_w4a16 v4 for M <= 8)."""
+    ext = ng.extension()
+    for M, K, N in [(1, 4096, 14336), (1, 14336, 4096), (8, 14336, 512), (33, 14336, 4096),
+                    (128, 8192, 1024)]:
+        assert ext.matmul_fused_workspace_bytes(M, K, N, 128, None) == \
+            ext.gemm_workspace_bytes(M, K, N, 128, 6, None), (M, K, N)
+    assert ext.matmul_fused_workspace_bytes(1, 14336, 4096, 128, None) == \
+        ext.gemv_workspace_bytes(1, 14336, 4096, 128, 4, 0, 0, None)
+    assert ext.matmul_fused_workspace_bytes(129, 4096, 4096, 128, None) == (0, 0)

@@ -1,0 +1,101 @@
+"""The fused output epilogues of the streaming kernel (nibble_matmul_w4a16_fused).
+
+Both epilogues are defined as the unfused fp16 ops they replace, so the test
+is bit equality with those ops run separately on the GPU:
+  * bias:   matmul(X, W) + bias               (the reference QuantLinear, ops.py:131-135)
+  * swiglu: silu(X W_gate) * (X W_up)         (the fp16 torch composition)
+and, for SwiGLU, the north-star tolerance against an fp32 evaluation of the
+same MLP input from the oracle's products.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+import nibblegemm_amd as ng
+from nibblegemm_amd import ops
+from cases import host, oracle_y, synthetic, quantized
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(1, 4096, 1024, 128), (4, 512, 260, 64), (8, 14336, 512, 128), (16, 1024, 4100, 128),
+          (100, 2048, 640, 64), (128, 8192, 384, 128)]
+
+
+@pytest.mark.parametrize("M,K,N,g", SHAPES)
+def test_bias_epilogue_is_the_separate_add(M, K, N, g):
+    _, _, _, Xd, qw = synthetic(M, K, N, g, seed=M + K + N)
+    bias = (torch.randn(N, generator=torch.Generator().manual_seed(N)) * 0.5).half().cuda()
+    fused = ng.matmul_bias(Xd, qw, bias)
+    separate = ng.matmul(Xd, qw) + bias
+    assert fused.dtype == torch.float16 and fused.shape == (M, N)
+    assert torch.equal(fused, separate)
+
+
+SWIGLU = [(1, 4096, 1024, 128), (8, 14336, 512, 128), (33, 1024, 320, 64), (128, 2048, 96, 128)]
+
+
+@pytest.mark.parametrize("M,K,Nh,g", SWIGLU)
+def test_swiglu_epilogue_is_the_fp16_composition(M, K, Nh, g):
+    Xg, pg, sg, Xd, gate = quantized(M, K, Nh, g, seed=1)
+    _, pu, su, _, up = quantized(M, K, Nh, g, seed=2)
+    qw = ng.interleave_swiglu(gate, up)
+    fused = ng.matmul_swiglu(Xd, qw)
+    assert fused.shape == (M, Nh)
+    composed = torch.nn.functional.silu(ng.matmul(Xd, gate)) * ng.matmul(Xd, up)
+    assert torch.equal(fused, composed)
+    # against fp32 arithmetic on the oracle's products of the same inputs
+    yg = torch.from_numpy(oracle_y(Xg, pg, sg, K, g)).float()
+    yu = torch.from_numpy(oracle_y(Xg, pu, su, K, g)).float()
+    ref = torch.nn.functional.silu(yg) * yu
+    err = float((torch.from_numpy(host(fused)).float() - ref).abs().max() / ref.pow(2).mean().sqrt())
+    assert err <= 1e-2
+
+
+def test_swiglu_above_the_fused_batch_limit_composes():
+    M, K, Nh, g = 200, 512, 128, 128
+    _, _, _, Xd, gate = quantized(M, K, Nh, g, seed=3)
+    _, _, _, _, up = quantized(M, K, Nh, g, seed=4)
+    y = ng.matmul_swiglu(Xd, ng.interleave_swiglu(gate, up))
+    composed = torch.nn.functional.silu(ng.matmul(Xd, gate)) * ng.matmul(Xd, up)
+    assert torch.equal(y, composed)
+
+
+def test_quantlinear_bias_fused_and_promoting():
+    torch.manual_seed(0)
+    lin = torch.nn.Linear(512, 256, bias=True).half().cuda()
+    ql = ng.QuantLinear.from_linear(lin, group_size=128)
+    x = torch.randn(2, 3, 512, device="cuda").half()
+    y = ql(x)
+    expect = (ng.matmul(x.reshape(-1, 512), ql._qw()) + ql.bias).reshape(2, 3, 256)
+    assert torch.equal(y, expect)
+    # an fp32 bias promotes the result, as the reference's fp16 + fp32 add does
+    ql32 = ng.QuantLinear(ql._qw(), ql.bias.float())
+    y32 = ql32(x)
+    assert y32.dtype == torch.float32
+    assert torch.equal(y32, ng.matmul(x.reshape(-1, 512), ql._qw()).reshape(2, 3, 256) + ql32.bias)
+
+
+def test_fused_calls_replay_in_a_graph():
+    """Split-K counters of the fused launch are reset in-kernel: captured calls
+    replay correctly, with eager work between replays."""
+    M, K, N, g = 4, 14336, 512, 128
+    _, _, _, Xd, qw = synthetic(M, K, N, g, seed=5)
+    bias = torch.randn(N, generator=torch.Generator().manual_seed(5)).half().cuda()
+    ref = ng.matmul_bias(Xd, qw, bias)
+    assert ops._fused_workspace(ops._bind(), Xd.device, ops._stream(Xd.device), M, K, N, g)[0] is not None
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ng.matmul_bias(Xd, qw, bias)  # warm the capture-side workspace cache
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = ng.matmul_bias(Xd, qw, bias)
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref)
+        ng.matmul(Xd, qw)  # eager work between replays
+        torch.cuda.synchronize()

@@ -84,3 +84,20 @@ def test_quantized_weight_bytes_and_to():
     assert qw.weight_bytes == 32 * 16 * 4 + 2 * 16 * 2
     qw2 = qw.to("cpu")
     assert torch.equal(qw2.qweight, qw.qweight) and (qw2.K, qw2.N, qw2.group_size) == (256, 16, 128)
+
+
+def test_interleave_swiglu_column_order():
+    """Columns alternate gate/up in blocks of 32; split_swiglu inverts it."""
+    import torch
+    from nibblegemm_amd.quant import QuantizedWeight, interleave_swiglu, split_swiglu
+    K, N, g = 16, 64, 8
+    gq = torch.arange(K // 8 * N, dtype=torch.int32).reshape(K // 8, N)
+    uq = -1 - gq
+    gs = torch.arange(K // g * N, dtype=torch.float32).reshape(K // g, N).half()
+    us = -gs
+    qw = interleave_swiglu(QuantizedWeight(gq, gs, g, K, N), QuantizedWeight(uq, us, g, K, N))
+    assert (qw.K, qw.N) == (K, 2 * N)
+    assert torch.equal(qw.qweight[:, :32], gq[:, :32]) and torch.equal(qw.qweight[:, 32:64], uq[:, :32])
+    assert torch.equal(qw.qweight[:, 64:96], gq[:, 32:]) and torch.equal(qw.scales[:, 96:], us[:, 32:])
+    g_back, u_back = split_swiglu(qw.qweight)
+    assert torch.equal(g_back, gq) and torch.equal(u_back, uq)
