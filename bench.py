@@ -4,7 +4,9 @@
 BASELINE.json's metric is "M=1 W4A16 GEMV us & % HBM peak (4096x14336);
 8B-shape decode tok/s", quoted on configs[1]'s gate/up shape; the second half
 (configs[4], the Llama-3-8B-shaped decode step) is reported under
-``decode_8b`` by :mod:`nibblegemm_amd.decode_step`.  A *step* is
+``decode_8b`` by :mod:`nibblegemm_amd.decode_step`, and config 4's M=2048
+prefill GEMM points under ``prefill_2048`` (each checked against an fp32
+reference before it is timed).  A *step* is
 one ``nibblegemm_amd.gemv`` call (M=1) over one batch of synthetic inputs
 (nibbles U{0..15}, scales fp16 U(0.002, 0.02), activations fp16 N(0,1)).
 
@@ -76,6 +78,8 @@ def main() -> int:
                     help="skip the copy-bandwidth, hipBLASLt and eager side measurements")
     ap.add_argument("--skip-decode-step", action="store_true",
                     help="skip the 8B-shaped decode step (BASELINE config 5)")
+    ap.add_argument("--skip-prefill", action="store_true",
+                    help="skip the M=2048 prefill GEMM points (BASELINE config 4)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -162,6 +166,20 @@ def main() -> int:
             f"{decode['fused']['graph_tok_s']} tok/s ({decode['fused']['launches']} launches); "
             f"{time.perf_counter() - t0:.1f} s")
 
+    prefill = None
+    if not args.skip_prefill:
+        from nibblegemm_amd.bench_shapes import prefill_points  # noqa: PLC0415
+
+        torch.cuda.empty_cache()
+        t0 = time.perf_counter()
+        prefill = [{k: r[k] for k in ("M", "K", "N", "us", "TFLOP/s", "hipblaslt_fp16_us", "vs_fp16",
+                                      "max_err_rms")}
+                   for KN in ((4096, 14336), (14336, 4096))
+                   for r in prefill_points(*KN, [2048], trials=5, versions=(6,))]
+        log("prefill M=2048 (gemm v6): " + "; ".join(
+            f"{r['K']}x{r['N']} {r['us']} us {r['TFLOP/s']} TFLOP/s ({r['vs_fp16']}x hipBLASLt fp16)"
+            for r in prefill) + f"; {time.perf_counter() - t0:.1f} s")
+
     roofline = {
         "bound": "hbm",
         "achieved": round(gbps, 1),
@@ -199,6 +217,7 @@ def main() -> int:
         "roofline": roofline,
         "cpu_baseline": cpu,
         "decode_8b": decode,
+        "prefill_2048": prefill,
         **extras,
     }
     print(json.dumps(line), flush=True)

@@ -7,7 +7,8 @@ bench/autotune.py, for the BASELINE configs).
     python3 -m nibblegemm_amd.bench_shapes dequant     # standalone dequant
     python3 -m nibblegemm_amd.bench_shapes crossover   # gemv vs gemm over M
 
-Every timing is a HIP-graph replay of many calls.  Each call streams its
+Every timing is a HIP-graph replay of many calls; a kernel and its hipBLASLt
+baseline are timed with interleaved trials (the same clock state for both).  Each call streams its
 weights from HBM: copies of the weights rotate through at least 1 GiB, more
 than the 256 MiB Infinity Cache.  Inputs follow BASELINE's synthetic
 distributions: nibbles U{0..15}, scales U(0.002, 0.02), activations N(0, 1).
@@ -89,27 +90,36 @@ def decode(args, rows):
         torch.cuda.empty_cache()
 
 
+def prefill_points(K: int, N: int, Ms, group_size: int = 128, trials: int = 10,
+                   versions=(6, 7)):
+    """Rows of the prefill sweep at one weight shape (each checked first)."""
+    out = []
+    qws, gen = _weights(K, N, group_size, seed=K + N)
+    w16 = _fp16_baseline(qws[0])
+    for M in Ms:
+        X = torch.randn((M, K), generator=gen).to(torch.float16).cuda()
+        reps = 8 if M >= 512 else 32
+        for v in versions:
+            err = _check(ops.gemm(X, qws[0], version=v), X, qws[0], f"gemm v{v} {M}x{K}x{N}")
+            t, f = H.bench_graph_pair(lambda i: ops.gemm(X, qws[i], version=v),
+                                      lambda i: torch.mm(X, w16[i]), reps=reps, trials=trials)
+            tf = H.tflops(M, K, N, t.median_ms)
+            out.append({"bench": "prefill", "M": M, "K": K, "N": N, "impl": f"gemm v{v}",
+                        "us": round(t.median_ms * 1e3, 2), "TFLOP/s": round(tf, 1),
+                        "%2.5PF": round(100 * tf / H.FP16_MFMA_PEAK_TFLOPS, 1),
+                        "hipblaslt_fp16_us": round(f.median_ms * 1e3, 2),
+                        "vs_fp16": round(f.median_ms / t.median_ms, 2),
+                        "max_err_rms": float(f"{err:.2e}")})
+    del qws, w16
+    torch.cuda.empty_cache()
+    return out
+
+
 def prefill(args, rows):
     for K, N in PREFILL_SHAPES:
-        qws, gen = _weights(K, N, args.group_size, seed=K + N)
-        w16 = _fp16_baseline(qws[0])
-        for M in args.M or [16, 32, 128, 512, 2048]:
-            X = torch.randn((M, K), generator=gen).to(torch.float16).cuda()
-            reps = 8 if M >= 512 else 32
-            f = H.bench_graph(lambda i: torch.mm(X, w16[i]), reps=reps, trials=args.trials)
-            for v in (6, 7):
-                err = _check(ops.gemm(X, qws[0], version=v), X, qws[0], f"gemm v{v} {M}x{K}x{N}")
-                t = H.bench_graph(lambda i: ops.gemm(X, qws[i], version=v), reps=reps,
-                                  trials=args.trials)
-                tf = H.tflops(M, K, N, t.median_ms)
-                _emit(rows, {"bench": "prefill", "M": M, "K": K, "N": N, "impl": f"gemm v{v}",
-                             "us": round(t.median_ms * 1e3, 2), "TFLOP/s": round(tf, 1),
-                             "%2.5PF": round(100 * tf / H.FP16_MFMA_PEAK_TFLOPS, 1),
-                             "hipblaslt_fp16_us": round(f.median_ms * 1e3, 2),
-                             "vs_fp16": round(f.median_ms / t.median_ms, 2),
-                             "max_err_rms": float(f"{err:.2e}")})
-        del qws, w16
-        torch.cuda.empty_cache()
+        for row in prefill_points(K, N, args.M or [16, 32, 128, 512, 2048], args.group_size,
+                                  args.trials):
+            _emit(rows, row)
 
 
 def dequant(args, rows):

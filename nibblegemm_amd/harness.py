@@ -123,6 +123,30 @@ def bench_graph(fn: Callable[[int], object], *, reps: int = 32, trials: int = 20
     return GraphRunner(fn, reps, warmup).time(trials)
 
 
+def bench_graph_pair(fn_a: Callable[[int], object], fn_b: Callable[[int], object], *,
+                     reps: int = 32, trials: int = 20, warmup: int = 3):
+    """Two graph-timed candidates with their trials interleaved (a, b, a, b,
+    ...), so both see the same clock and thermal state -- a GPU under
+    sustained matrix-core load slows down, and timing one candidate after the
+    other would charge that to whichever runs second.  Returns (Timing a,
+    Timing b)."""
+    runners = (GraphRunner(fn_a, reps, warmup), GraphRunner(fn_b, reps, warmup))
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    for r in runners:
+        r.graph.replay()  # warm
+    torch.cuda.synchronize()
+    samples = ([], [])
+    for _ in range(trials):
+        for r, out in zip(runners, samples):
+            start.record()
+            r.graph.replay()
+            end.record()
+            end.synchronize()
+            out.append(start.elapsed_time(end) / reps)
+    return tuple(_summarise(s, trials, reps) for s in samples)
+
+
 def measured_copy_gbps(size_bytes: int = 2 << 30) -> float:
     """Achievable HBM bandwidth: a large device copy, read + write counted."""
     n = size_bytes // 2

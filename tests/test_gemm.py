@@ -190,3 +190,29 @@ def test_gemm_under_aligned_weights(M, K_, N):
     y_off = ng.gemm(Xd, qw_off)
     assert torch.equal(y, y_off)
     assert rms_err(host(y_off), oracle_y(X, packed, scales, K_, 128)) <= RMS_TOL
+
+
+def test_split_k_gemm_replays_in_a_graph():
+    """The producer/consumer kernel's K split (counters reset by the kernel
+    itself, no memset) is graph-capturable; every replay matches eager, with
+    eager work between replays."""
+    X, packed, scales, Xd, qw = synthetic(160, 14336, 512, 128, seed=11)
+    ext = ng.extension()
+    assert ext.gemm_workspace_bytes(160, 14336, 512, 128, 6, None)[1] > 0  # this plan splits K
+    eager = ng.gemm(Xd, qw)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ng.gemm(Xd, qw)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = ng.gemm(Xd, qw)
+    for _ in range(4):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+        ng.gemm(Xd, qw)
+        torch.cuda.synchronize()
+    assert rms_err(host(eager), oracle_y(X, packed, scales, 14336, 128)) <= RMS_TOL
