@@ -163,7 +163,8 @@ def main() -> int:
         decode = decode_step.run(32)
         log(f"8B decode step: {decode['projections']['graph_tok_s']} tok/s graph "
             f"({decode['projections']['launches']} launches), fused "
-            f"{decode['fused']['graph_tok_s']} tok/s ({decode['fused']['launches']} launches); "
+            f"{decode['fused']['graph_tok_s']} tok/s ({decode['fused']['launches']} launches), "
+            f"with the SwiGLU epilogue {decode['fused_swiglu']['graph_tok_s']} tok/s; "
             f"{time.perf_counter() - t0:.1f} s")
 
     prefill = None

@@ -17,7 +17,10 @@ the host quantiser).
 
 The fused variant concatenates q|k|v and gate|up along N
 (:func:`~nibblegemm_amd.quant.concat_columns`), so a layer is 4 launches
-instead of 7: 128 per step instead of 224.  The arithmetic is identical
+instead of 7: 128 per step instead of 224.  ``fused_swiglu`` interleaves
+gate and up instead and runs them through the SwiGLU epilogue
+(:func:`~nibblegemm_amd.ops.matmul_swiglu`), whose launch writes the
+[1, 14336] input of down directly.  The arithmetic is identical
 (each output column is computed from the same weights, scales and
 activations); it only removes launches.
 
@@ -33,8 +36,8 @@ from typing import Dict, List, Tuple
 import torch
 
 from . import harness as H
-from .ops import matmul
-from .quant import QuantizedWeight, concat_columns, quantize_device
+from .ops import matmul, matmul_swiglu
+from .quant import QuantizedWeight, concat_columns, interleave_swiglu, quantize_device
 
 LLAMA3_8B = {"hidden": 4096, "kv": 1024, "intermediate": 14336, "layers": 32}
 PROJECTIONS = ("q", "k", "v", "o", "gate", "up", "down")
@@ -64,10 +67,14 @@ def build_layers(layers: int, cfg=LLAMA3_8B, group_size: int = 128, device="cuda
     return out
 
 
-def fuse(layer: Dict[str, QuantizedWeight]) -> Dict[str, QuantizedWeight]:
-    """q|k|v and gate|up concatenated along N; o and down unchanged."""
+def fuse(layer: Dict[str, QuantizedWeight], swiglu: bool = False) -> Dict[str, QuantizedWeight]:
+    """q|k|v and gate|up concatenated along N; o and down unchanged.  With
+    ``swiglu`` gate and up are interleaved for the SwiGLU epilogue instead
+    (the launch then writes silu(gate) * up, [1, 14336], for down)."""
+    gate_up = (interleave_swiglu(layer["gate"], layer["up"]) if swiglu
+               else concat_columns(layer["gate"], layer["up"]))
     return {"qkv": concat_columns(layer["q"], layer["k"], layer["v"]), "o": layer["o"],
-            "gate_up": concat_columns(layer["gate"], layer["up"]), "down": layer["down"]}
+            ("gate_up_swiglu" if swiglu else "gate_up"): gate_up, "down": layer["down"]}
 
 
 def weight_bytes(layers: List[Dict[str, QuantizedWeight]]) -> int:
@@ -82,11 +89,12 @@ class DecodeStep:
         ks = sorted({qw.K for layer in layers for qw in layer.values()})
         self.acts = {k: torch.randn((1, k), generator=gen, device=device).to(torch.float16)
                      for k in ks}
-        self.calls = [(self.acts[qw.K], qw) for layer in layers for qw in layer.values()]
+        self.calls = [(self.acts[qw.K], qw, matmul_swiglu if name == "gate_up_swiglu" else matmul)
+                      for layer in layers for name, qw in layer.items()]
 
     def __call__(self, _i: int = 0) -> None:
-        for x, qw in self.calls:
-            matmul(x, qw)
+        for x, qw, fn in self.calls:
+            fn(x, qw)
 
     @property
     def launches(self) -> int:
@@ -119,6 +127,8 @@ def run(n_layers: int = 32, group_size: int = 128, trials: int = 10) -> dict:
     res["projections"] = measure(layers, trials)
     fused = [fuse(layer) for layer in layers]
     res["fused"] = measure(fused, trials)
+    del fused
+    res["fused_swiglu"] = measure([fuse(layer, swiglu=True) for layer in layers], trials)
     return res
 
 

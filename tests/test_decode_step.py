@@ -45,7 +45,16 @@ def test_decode_step_runs_and_counts_launches():
     fused = D.DecodeStep([D.fuse(layer) for layer in layers])
     assert fused.launches == 8
     fused()
+    sw = D.DecodeStep([D.fuse(layer, swiglu=True) for layer in layers])
+    assert sw.launches == 8
+    sw()
     torch.cuda.synchronize()
+    # the SwiGLU launch writes silu(gate) * up, the input width of down
+    layer = layers[0]
+    x = torch.randn(1, 512, device="cuda").half()
+    h = ng.matmul_swiglu(x, D.fuse(layer, swiglu=True)["gate_up_swiglu"])
+    assert h.shape == (1, 1024)
+    assert torch.equal(h, torch.nn.functional.silu(ng.matmul(x, layer["gate"])) * ng.matmul(x, layer["up"]))
     nbytes = D.weight_bytes(layers)
     shapes = D.projection_shapes(cfg)
     assert nbytes == 2 * sum(k * n // 2 + (k // 128) * n * 2 for k, n in shapes.values())
