@@ -413,7 +413,10 @@ int plan_stream(int64_t M, int64_t K, int64_t N, int64_t G, bool split_k, int64_
                 (long long)M, (long long)K, (long long)N, (long long)G);
   p->mt = mt_for(std::min<int64_t>(M, 32));
   p->mblocks = static_cast<int>(ceil_div(M, p->mt));
-  p->waves = threads_override > 0 ? static_cast<int>(threads_override / 64) : kDefaultWaves;
+  // A 32-thread block (accepted by the reference, csrc/gemv_w4a16.cu:384-385)
+  // runs as one wave64.
+  p->waves = threads_override > 0 ? std::max(1, static_cast<int>(threads_override / 64))
+                                  : kDefaultWaves;
   if (p->waves > max_waves_for(p->mt))
     return fail(NIBBLE_ERR_UNSUPPORTED, "block_threads=%lld too large for M=%lld (max %d)",
                 (long long)threads_override, (long long)M, max_waves_for(p->mt) * 64);
@@ -487,10 +490,11 @@ int validate_gemv(const void* X, int64_t x_rows, int64_t x_cols, const void* Wq,
                   int64_t wq_cols, const void* S, int64_t s_rows, int64_t s_cols, int64_t group_size,
                   int64_t version, int64_t splits_override, int64_t threads_override,
                   const void* Y) {
-  NIBBLE_CHECK(threads_override == 0 || threads_override == 64 || threads_override == 128 ||
-                   threads_override == 256 || threads_override == 512 || threads_override == 1024,
-               "block_threads must be 0 (heuristic) or 64, 128, 256, 512, 1024 (a wave is 64 lanes), "
-               "got %lld",
+  NIBBLE_CHECK(threads_override == 0 || threads_override == 32 || threads_override == 64 ||
+                   threads_override == 128 || threads_override == 256 ||
+                   threads_override == 512 || threads_override == 1024,
+               "block_threads must be 0 (heuristic) or 32, 64, 128, 256, 512, 1024 (32 runs as one "
+               "64-lane wave), got %lld",
                (long long)threads_override);
   NIBBLE_CHECK(splits_override >= 0, "splits must be >= 0");
   NIBBLE_CHECK(x_rows >= 0 && x_cols >= 0 && wq_rows >= 0 && wq_cols >= 0 && s_rows >= 0 &&

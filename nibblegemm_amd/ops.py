@@ -209,8 +209,9 @@ def gemv(X: torch.Tensor, qw: QuantizedWeight, version: int = 4, splits: int = 0
 
     ``version``: 0/1 scalar fp32 kernels, 2/3 streaming kernel with one K split,
     4 (default) streaming kernel with split-K.  ``splits`` and ``block_threads``
-    override the launch geometry (0 = heuristic); ``block_threads`` is a
-    multiple of the 64-lane wave.  Versions 3 and 4 serve M <= 8.
+    override the launch geometry (0 = heuristic); ``block_threads`` is 32 (run
+    as one 64-lane wave, as the reference accepts it) or a multiple of the
+    64-lane wave up to 1024.  Versions 3 and 4 serve M <= 8.
     """
     ext = _bind()
     Wq, S = qw.qweight, qw.scales

@@ -89,6 +89,9 @@ def test_gemv_threads_override_validated():
     ext = ng.extension()
     assert gemv(ext, 1, 256, 128, threads=96) == INVALID
     assert "block_threads" in ext.last_error()
+    # the reference's 32-thread block is accepted and planned as one wave
+    assert ext.gemv_workspace_bytes(1, 1024, 256, 64, 4, 16, 32, None) == \
+        ext.gemv_workspace_bytes(1, 1024, 256, 64, 4, 16, 64, None)
 
 
 def test_gemm_workspace_formula():

@@ -101,7 +101,7 @@ def test_v3_is_v4_with_one_split():
     assert torch.equal(ng.gemv(Xd, qw, version=4, splits=1), ng.gemv(Xd, qw, version=3))
 
 
-@pytest.mark.parametrize("threads", [64, 128, 256, 512, 1024])
+@pytest.mark.parametrize("threads", [32, 64, 128, 256, 512, 1024])
 def test_block_threads_override(threads):
     M = 1 if threads == 1024 else 2
     X, packed, scales, Xd, qw = synthetic(M, 2048, 1280, 128, seed=threads)
