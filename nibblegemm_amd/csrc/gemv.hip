@@ -113,8 +113,13 @@ __device__ __forceinline__ void emit_outputs(const GemvArgs& a, int strip, int m
   }
 }
 
-template <int MT, int GROUP, int WAVES>
+// STREAM: the launch reads every weight exactly once (a single row block), so
+// packed words and scales are loaded with the non-temporal hint -- measured
+// 1-2% faster at M <= 32; launches of several row blocks re-read the weights
+// from cache and keep the default policy.
+template <int MT, int GROUP, int WAVES, bool STREAM>
 __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs a) {
+  constexpr int kWPolicy = STREAM ? 2 : 0;  // buffer-load cache policy: 2 = nt
   constexpr int CPG = GROUP / 32;                  // 32-k chunks per quant group
   constexpr int TILES = (MT + 15) / 16;            // 16-row MFMA A tiles
   constexpr int LANE_ROWS = MT < 4 ? MT : 4;       // output rows a lane holds per tile
@@ -176,11 +181,12 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs a) {
         st.x[t][c] = __builtin_bit_cast(
             h8_t, __builtin_amdgcn_raw_buffer_load_b128(rx, voff_x[t], kx + c * 64, 0));
     st.s = __builtin_bit_cast(
-        h4_t, __builtin_amdgcn_raw_buffer_load_b64(rs, voff_s, static_cast<uint32_t>(g) * a.N * 2u, 0));
+        h4_t, __builtin_amdgcn_raw_buffer_load_b64(rs, voff_s, static_cast<uint32_t>(g) * a.N * 2u,
+                                                   kWPolicy));
 #pragma unroll
     for (int c = 0; c < CPG; ++c)
       st.w[c] = __builtin_bit_cast(
-          u4_t, __builtin_amdgcn_raw_buffer_load_b128(rw, voff_w, kw + c * 4 * row_bytes, 0));
+          u4_t, __builtin_amdgcn_raw_buffer_load_b128(rw, voff_w, kw + c * 4 * row_bytes, kWPolicy));
   };
 
   f4_t tot[TILES][4];
@@ -368,17 +374,17 @@ constexpr int kDefaultWaves = 4;
 // eight groups -- 14336 x 4096 is fastest at 4 splits, 8192 x 8192 at 2.
 constexpr int kGroupsPerWave = 8;
 
-template <int MT, int GROUP>
-hipError_t launch_mt(const GemvArgs& a, const StreamPlan& p, hipStream_t stream) {
+template <int MT, int GROUP, bool STREAM>
+hipError_t launch_mts(const GemvArgs& a, const StreamPlan& p, hipStream_t stream) {
   dim3 grid(p.strips, p.splits, p.mblocks);
   switch (p.waves) {
-    case 1: gemv_mfma_kernel<MT, GROUP, 1><<<grid, 64, 0, stream>>>(a); break;
-    case 2: gemv_mfma_kernel<MT, GROUP, 2><<<grid, 128, 0, stream>>>(a); break;
-    case 4: gemv_mfma_kernel<MT, GROUP, 4><<<grid, 256, 0, stream>>>(a); break;
-    case 8: gemv_mfma_kernel<MT, GROUP, 8><<<grid, 512, 0, stream>>>(a); break;
+    case 1: gemv_mfma_kernel<MT, GROUP, 1, STREAM><<<grid, 64, 0, stream>>>(a); break;
+    case 2: gemv_mfma_kernel<MT, GROUP, 2, STREAM><<<grid, 128, 0, stream>>>(a); break;
+    case 4: gemv_mfma_kernel<MT, GROUP, 4, STREAM><<<grid, 256, 0, stream>>>(a); break;
+    case 8: gemv_mfma_kernel<MT, GROUP, 8, STREAM><<<grid, 512, 0, stream>>>(a); break;
     case 16:
       if constexpr (MT <= 16) {
-        gemv_mfma_kernel<MT, GROUP, 16><<<grid, 1024, 0, stream>>>(a);
+        gemv_mfma_kernel<MT, GROUP, 16, STREAM><<<grid, 1024, 0, stream>>>(a);
         break;
       } else {
         return hipErrorInvalidValue;
@@ -386,6 +392,18 @@ hipError_t launch_mt(const GemvArgs& a, const StreamPlan& p, hipStream_t stream)
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+// Row blocks of fewer than 32 rows always fit one block; 32-row blocks take
+// the non-temporal loads only when the batch is a single block.
+template <int MT, int GROUP>
+hipError_t launch_mt(const GemvArgs& a, const StreamPlan& p, hipStream_t stream) {
+  if constexpr (MT < 32) {
+    return launch_mts<MT, GROUP, true>(a, p, stream);
+  } else {
+    return p.mblocks == 1 ? launch_mts<MT, GROUP, true>(a, p, stream)
+                          : launch_mts<MT, GROUP, false>(a, p, stream);
+  }
 }
 
 template <int GROUP>
