@@ -50,7 +50,7 @@
 extern "C" {
 #endif
 
-#define NIBBLE_ABI_VERSION 3
+#define NIBBLE_ABI_VERSION 4
 
 #if defined(__GNUC__) || defined(__clang__)
 #define NIBBLE_API __attribute__((visibility("default")))
@@ -166,6 +166,48 @@ NIBBLE_API size_t nibble_matmul_fused_counter_bytes(int64_t M, int64_t K, int64_
 NIBBLE_API int nibble_dequant_w4(const void* Wq, int64_t wq_rows, int64_t wq_cols,
                       const void* S, int64_t s_rows, int64_t s_cols,
                       int64_t group_size, int fast, void* W, void* stream);
+
+/*
+ * Decode-step glue.  No counterpart in the reference's extension: its model
+ * decode (bench/bench_model.py:177-188, a transformers Llama with its Linear
+ * layers swapped for QuantLinear, :131-154) runs these as PyTorch ops.  For
+ * callers that capture a whole batch-1 decode step in one HIP graph.
+ *
+ * RMSNorm of each row: Y[r, :] = fp16(X[r, :] * r_r * W) with
+ * r_r = 1 / sqrt(mean_c(X[r, c]^2) + eps), all in fp32.  X, Y fp16
+ * [rows, cols], W fp16 [cols]; cols a multiple of 8 up to 16384; all three
+ * 16-byte aligned.
+ */
+NIBBLE_API int nibble_rmsnorm_f16(const void* X, int64_t rows, int64_t cols, const void* W,
+                                  float eps, void* Y, void* stream);
+
+/*
+ * Grouped-query attention of one decode token at position `pos`.
+ * QKV fp16 [n_heads * 128 | n_kv_heads * 128 | n_kv_heads * 128] is the
+ * token's q, k and v (the q|k|v projection's output row).  K_cache and
+ * V_cache fp16 [n_kv_heads][max_seq][128] hold tokens 0 .. pos - 1; the call
+ * writes the token's k (rotated) and v at row `pos` and returns
+ * Out fp16 [n_heads * 128] = softmax(q k^T / sqrt(128)) v over tokens
+ * 0 .. pos, query head i reading kv head i / (n_heads / n_kv_heads).
+ * rope_cos / rope_sin fp32 [max_seq][64] (both or neither) apply the
+ * rotary embedding to q and k in the rotate-half pairing; NULL skips it.
+ * head_dim must be 128 and n_heads / n_kv_heads 1, 2, 4 or 8.  Positions
+ * beyond 127 split across workgroups: `workspace` (256-byte aligned, its
+ * leading nibble_attention_decode_counter_bytes(...) zero before the first
+ * call, restored to zero by each call) must then hold
+ * nibble_attention_decode_workspace_bytes(...) bytes; NULL when that is 0.
+ */
+NIBBLE_API int nibble_attention_decode_f16(const void* QKV, int64_t n_heads, int64_t n_kv_heads,
+                                           int64_t head_dim, void* K_cache, void* V_cache,
+                                           int64_t max_seq, int64_t pos, const void* rope_cos,
+                                           const void* rope_sin, void* Out, void* workspace,
+                                           size_t workspace_bytes, void* stream);
+NIBBLE_API size_t nibble_attention_decode_workspace_bytes(int64_t n_heads, int64_t n_kv_heads,
+                                                          int64_t head_dim, int64_t max_seq,
+                                                          int64_t pos, void* stream);
+NIBBLE_API size_t nibble_attention_decode_counter_bytes(int64_t n_heads, int64_t n_kv_heads,
+                                                        int64_t head_dim, int64_t max_seq,
+                                                        int64_t pos, void* stream);
 
 #ifdef __cplusplus
 }

@@ -131,6 +131,52 @@ static PyObject* py_fused_ws(PyObject* self, PyObject* const* a, Py_ssize_t n) {
   return Py_BuildValue("(nn)", (Py_ssize_t)ws, (Py_ssize_t)cb);
 }
 
+/* rmsnorm(X, rows, cols, W, eps, Y, stream) */
+static PyObject* py_rmsnorm(PyObject* self, PyObject* const* a, Py_ssize_t n) {
+  (void)self;
+  if (!nargs_is(n, 7, "rmsnorm")) return NULL;
+  void *X, *W, *Y, *stream;
+  long long rows, cols;
+  double eps = PyFloat_AsDouble(a[4]);
+  if (eps == -1.0 && PyErr_Occurred()) return NULL;
+  if (!take_ptr(a[0], &X) || !take_i64(a[1], &rows) || !take_i64(a[2], &cols) ||
+      !take_ptr(a[3], &W) || !take_ptr(a[5], &Y) || !take_ptr(a[6], &stream))
+    return NULL;
+  return PyLong_FromLong(nibble_rmsnorm_f16(X, rows, cols, W, (float)eps, Y, stream));
+}
+
+/* attention(QKV, n_heads, n_kv, head_dim, Kc, Vc, max_seq, pos, cos, sin, Out, ws, ws_bytes,
+ * stream) */
+static PyObject* py_attention(PyObject* self, PyObject* const* a, Py_ssize_t n) {
+  (void)self;
+  if (!nargs_is(n, 14, "attention")) return NULL;
+  void *qkv, *kc, *vc, *rc, *rs, *out, *ws, *stream;
+  long long nh, nkv, hd, ms, pos, wsb;
+  if (!take_ptr(a[0], &qkv) || !take_i64(a[1], &nh) || !take_i64(a[2], &nkv) ||
+      !take_i64(a[3], &hd) || !take_ptr(a[4], &kc) || !take_ptr(a[5], &vc) ||
+      !take_i64(a[6], &ms) || !take_i64(a[7], &pos) || !take_ptr(a[8], &rc) ||
+      !take_ptr(a[9], &rs) || !take_ptr(a[10], &out) || !take_ptr(a[11], &ws) ||
+      !take_i64(a[12], &wsb) || !take_ptr(a[13], &stream))
+    return NULL;
+  int rc_ = nibble_attention_decode_f16(qkv, nh, nkv, hd, kc, vc, ms, pos, rc, rs, out, ws,
+                                        (size_t)(wsb < 0 ? 0 : wsb), stream);
+  return PyLong_FromLong(rc_);
+}
+
+/* attention_workspace_bytes(n_heads, n_kv, head_dim, max_seq, pos, stream) */
+static PyObject* py_attention_ws(PyObject* self, PyObject* const* a, Py_ssize_t n) {
+  (void)self;
+  if (!nargs_is(n, 6, "attention_workspace_bytes")) return NULL;
+  long long nh, nkv, hd, ms, pos;
+  void* stream;
+  if (!take_i64(a[0], &nh) || !take_i64(a[1], &nkv) || !take_i64(a[2], &hd) ||
+      !take_i64(a[3], &ms) || !take_i64(a[4], &pos) || !take_ptr(a[5], &stream))
+    return NULL;
+  size_t ws = nibble_attention_decode_workspace_bytes(nh, nkv, hd, ms, pos, stream);
+  size_t cb = nibble_attention_decode_counter_bytes(nh, nkv, hd, ms, pos, stream);
+  return Py_BuildValue("(nn)", (Py_ssize_t)ws, (Py_ssize_t)cb);
+}
+
 /* dequant(Wq, wr, wc, S, sr, sc, g, fast, W, stream) */
 static PyObject* py_dequant(PyObject* self, PyObject* const* a, Py_ssize_t n) {
   (void)self;
@@ -170,6 +216,11 @@ static PyMethodDef kMethods[] = {
      "nibble_matmul_w4a16_fused"},
     {"matmul_fused_workspace_bytes", (PyCFunction)(void (*)(void))py_fused_ws, METH_FASTCALL,
      "nibble_matmul_fused_workspace_bytes / nibble_matmul_fused_counter_bytes"},
+    {"rmsnorm", (PyCFunction)(void (*)(void))py_rmsnorm, METH_FASTCALL, "nibble_rmsnorm_f16"},
+    {"attention", (PyCFunction)(void (*)(void))py_attention, METH_FASTCALL,
+     "nibble_attention_decode_f16"},
+    {"attention_workspace_bytes", (PyCFunction)(void (*)(void))py_attention_ws, METH_FASTCALL,
+     "(nibble_attention_decode_workspace_bytes, nibble_attention_decode_counter_bytes)"},
     {"last_error", py_last_error, METH_NOARGS, "nibble_last_error"},
     {"abi_version", py_abi_version, METH_NOARGS, "nibble_abi_version"},
     {NULL, NULL, 0, NULL}};

@@ -1,0 +1,445 @@
+// Decode-step glue of a Llama-shaped layer at batch 1, around the W4A16
+// projections: RMSNorm and grouped-query attention over a KV cache.
+//
+// In the reference these are PyTorch / transformers operations of the model
+// that bench/bench_model.py decodes token by token with its Linear layers
+// swapped for QuantLinear (decode_tokens_per_s, bench/bench_model.py:177-188;
+// the swap, :131-154).  Here they are kernels, so that a whole decode step --
+// norms, projections, attention, residual adds -- is captured in one HIP
+// graph.  The residual adds need no kernel of their own: at M = 1 the residual
+// is a bias vector of the o and down projections (the fused bias epilogue of
+// the matmul).
+//
+// Both kernels are memory-latency work of a few hundred KB; they are written
+// for short, dependency-free loads (16-byte rows, no LDS staging of the
+// cache) and deterministic reductions (fixed orders, no float atomics).
+#include <cmath>
+
+#include "nibble_common.h"
+#include "nibble_decode.h"
+
+namespace nibble {
+
+namespace {
+
+constexpr int kHeadDim = 128;
+constexpr int kRopeHalf = kHeadDim / 2;
+constexpr int kChunk = 128;  // cached tokens per attention workgroup
+constexpr int kGlueThreads = 256;
+constexpr int kRmsMaxCols = kGlueThreads * 8 * 8;
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+  return v;
+}
+
+// y = fp16(x * r * w) with r = 1 / sqrt(mean(x^2) + eps), in fp32 (the
+// transformers LlamaRMSNorm computes the same in fp32 and rounds x * r to
+// fp16 before the weight; this rounds once).  One workgroup per row; each
+// thread holds CH 16-byte chunks of the row.  The sum of squares is reduced
+// per wave by a butterfly and across waves in wave order: deterministic.
+template <int CH>
+__global__ __launch_bounds__(kGlueThreads) void rmsnorm_kernel(const _Float16* __restrict__ X,
+                                                               const _Float16* __restrict__ W,
+                                                               _Float16* __restrict__ Y, int cols,
+                                                               float eps) {
+  __shared__ float part[kGlueThreads / 64];
+  const int tid = threadIdx.x;
+  const size_t base = static_cast<size_t>(blockIdx.x) * cols;
+  h8_t v[CH];
+  float ss = 0.0f;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int col = (c * kGlueThreads + tid) * 8;
+    v[c] = col < cols ? *reinterpret_cast<const h8_t*>(X + base + col) : h8_t{};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float f = static_cast<float>(v[c][i]);
+      ss = __builtin_fmaf(f, f, ss);
+    }
+  }
+  ss = wave_sum(ss);
+  if ((tid & 63) == 0) part[tid >> 6] = ss;
+  __syncthreads();
+  float tot = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kGlueThreads / 64; ++w) tot += part[w];
+  const float r = 1.0f / sqrtf(tot / static_cast<float>(cols) + eps);
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int col = (c * kGlueThreads + tid) * 8;
+    if (col < cols) {
+      const h8_t w = *reinterpret_cast<const h8_t*>(W + col);
+      h8_t y;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        y[i] = static_cast<_Float16>(static_cast<float>(v[c][i]) * r * static_cast<float>(w[i]));
+      *reinterpret_cast<h8_t*>(Y + base + col) = y;
+    }
+  }
+}
+
+struct AttnArgs {
+  const _Float16* qkv;     // [n_heads * 128 | n_kv * 128 | n_kv * 128]: q, k, v of this token
+  _Float16* k_cache;       // [n_kv][max_seq][128]
+  _Float16* v_cache;       // [n_kv][max_seq][128]
+  const float* rope_cos;   // [max_seq][64], or null: no rotary embedding
+  const float* rope_sin;   // [max_seq][64]
+  _Float16* out;           // [n_heads * 128]
+  float* partial;          // [n_kv][chunks][QPK][2 + 128] when chunks > 1
+  uint32_t* counters;      // [n_kv], zero on entry and on exit
+  int n_kv, max_seq, pos, chunks;
+};
+
+// Element d of the rotary embedding of a 128-vector x at position pos, in the
+// rotate-half pairing of transformers' apply_rotary_pos_emb (d with d +- 64):
+//   d <  64: x[d] cos - x[d + 64] sin;   d >= 64: x[d] cos + x[d - 64] sin.
+__device__ __forceinline__ float rope_at(const _Float16* x, int d, const AttnArgs& a) {
+  const float v = static_cast<float>(x[d]);
+  if (a.rope_cos == nullptr) return v;
+  const size_t i = static_cast<size_t>(a.pos) * kRopeHalf + (d & (kRopeHalf - 1));
+  const float c = a.rope_cos[i], s = a.rope_sin[i];
+  return d < kRopeHalf ? v * c - static_cast<float>(x[d + kRopeHalf]) * s
+                       : v * c + static_cast<float>(x[d - kRopeHalf]) * s;
+}
+
+// Grouped-query attention of one decode token: QPK query heads share each
+// kv head.  Workgroup (h, c) takes kv head h, its QPK query heads and cached
+// tokens [128 c, min(128 c + 128, pos + 1)).  Token pos is the current one:
+// its k (rotated, rounded to fp16 as the cache holds it) and v come from qkv
+// and are written into the caches by the workgroup of the last chunk.
+//
+//   1. scores: 16 groups of 16 lanes, a group per token row (lane j holds
+//      dims 8j..8j+7: one 16-byte load), summed over the group by butterfly;
+//   2. softmax within the chunk: max, exp, sum per head (one wave a head);
+//   3. P V: the same row layout, each lane accumulating QPK x 8 outputs,
+//      then the 16 groups summed in LDS in group order.
+// With one chunk the output is written directly.  Otherwise each workgroup
+// publishes (max, sum, unnormalised P V) with device-coherent stores and the
+// last workgroup of the kv head (agent-scope counter) combines the chunks in
+// chunk order: deterministic, one launch.
+template <int QPK>
+__global__ __launch_bounds__(kGlueThreads) void attention_decode_kernel(AttnArgs a) {
+  constexpr int HD = kHeadDim;
+  constexpr float kScale = 0.08838834764831845f;  // 1 / sqrt(128)
+  __shared__ float qs[QPK][HD];
+  __shared__ __attribute__((aligned(16))) _Float16 knew[HD];
+  __shared__ __attribute__((aligned(16))) _Float16 vnew[HD];
+  __shared__ float sc[QPK][kChunk];
+  __shared__ float red[16][QPK][HD];
+  __shared__ float mrow[QPK], lrow[QPK];
+  __shared__ int s_last;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int h = blockIdx.x;
+  const int c = blockIdx.y;
+  const int n_heads = a.n_kv * QPK;
+  const int t0 = c * kChunk;
+  const int t1 = min(t0 + kChunk, a.pos + 1);
+  const _Float16* qh = a.qkv + static_cast<size_t>(h) * QPK * HD;
+  const _Float16* kx = a.qkv + static_cast<size_t>(n_heads) * HD + static_cast<size_t>(h) * HD;
+  const _Float16* vx = kx + static_cast<size_t>(a.n_kv) * HD;
+  const size_t row0 = static_cast<size_t>(h) * a.max_seq;  // cache row of token 0
+
+  for (int e = tid; e < QPK * HD; e += kGlueThreads) {
+    const int hq = e / HD, d = e % HD;
+    qs[hq][d] = rope_at(qh + hq * HD, d, a) * kScale;
+  }
+  if (t1 == a.pos + 1 && tid < HD) {
+    const _Float16 kn = static_cast<_Float16>(rope_at(kx, tid, a));
+    const _Float16 vn = vx[tid];
+    knew[tid] = kn;
+    vnew[tid] = vn;
+    a.k_cache[(row0 + a.pos) * HD + tid] = kn;
+    a.v_cache[(row0 + a.pos) * HD + tid] = vn;
+  }
+  __syncthreads();
+
+  const int g16 = tid >> 4;
+  const int j = tid & 15;
+  float qr[QPK][8];
+#pragma unroll
+  for (int hq = 0; hq < QPK; ++hq)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) qr[hq][i] = qs[hq][8 * j + i];
+  for (int t = t0 + g16; t < t1; t += 16) {
+    const h8_t k8 = t == a.pos
+                        ? *reinterpret_cast<const h8_t*>(&knew[8 * j])
+                        : *reinterpret_cast<const h8_t*>(a.k_cache + (row0 + t) * HD + 8 * j);
+    float s[QPK];
+#pragma unroll
+    for (int hq = 0; hq < QPK; ++hq) {
+      s[hq] = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) s[hq] = __builtin_fmaf(qr[hq][i], static_cast<float>(k8[i]), s[hq]);
+    }
+    // Partners of a 16-lane group stay in the group, whose lanes share t.
+#pragma unroll
+    for (int off = 8; off > 0; off >>= 1)
+#pragma unroll
+      for (int hq = 0; hq < QPK; ++hq) s[hq] += __shfl_xor(s[hq], off);
+    if (j == 0) {
+#pragma unroll
+      for (int hq = 0; hq < QPK; ++hq) sc[hq][t - t0] = s[hq];
+    }
+  }
+  __syncthreads();
+
+  const int nt = t1 - t0;  // >= 1: the host sizes the grid so every chunk has a token
+  for (int hq = wave; hq < QPK; hq += kGlueThreads / 64) {
+    float m = -INFINITY;
+    for (int t = lane; t < nt; t += 64) m = fmaxf(m, sc[hq][t]);
+    m = wave_max(m);
+    float l = 0.0f;
+    for (int t = lane; t < nt; t += 64) {
+      const float p = __expf(sc[hq][t] - m);
+      sc[hq][t] = p;
+      l += p;
+    }
+    l = wave_sum(l);
+    if (lane == 0) {
+      mrow[hq] = m;
+      lrow[hq] = l;
+    }
+  }
+  __syncthreads();
+
+  float acc[QPK][8];
+#pragma unroll
+  for (int hq = 0; hq < QPK; ++hq)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[hq][i] = 0.0f;
+  for (int t = t0 + g16; t < t1; t += 16) {
+    const h8_t v8 = t == a.pos
+                        ? *reinterpret_cast<const h8_t*>(&vnew[8 * j])
+                        : *reinterpret_cast<const h8_t*>(a.v_cache + (row0 + t) * HD + 8 * j);
+#pragma unroll
+    for (int hq = 0; hq < QPK; ++hq) {
+      const float p = sc[hq][t - t0];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[hq][i] = __builtin_fmaf(p, static_cast<float>(v8[i]), acc[hq][i]);
+    }
+  }
+#pragma unroll
+  for (int hq = 0; hq < QPK; ++hq)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) red[g16][hq][8 * j + i] = acc[hq][i];
+  __syncthreads();
+
+  const bool direct = a.chunks == 1;
+  for (int e = tid; e < QPK * HD; e += kGlueThreads) {
+    const int hq = e / HD, d = e % HD;
+    float o = 0.0f;
+#pragma unroll
+    for (int g = 0; g < 16; ++g) o += red[g][hq][d];
+    if (direct) {
+      a.out[static_cast<size_t>(h * QPK + hq) * HD + d] = static_cast<_Float16>(o / lrow[hq]);
+    } else {
+      float* P = a.partial + ((static_cast<size_t>(h) * a.chunks + c) * QPK + hq) * (HD + 2);
+      store_coherent(P + 2 + d, o);
+      if (d == 0) {
+        store_coherent(P, mrow[hq]);
+        store_coherent(P + 1, lrow[hq]);
+      }
+    }
+  }
+  if (direct) return;
+
+  wait_vm_stores();
+  __syncthreads();
+  if (tid == 0) {
+    const uint32_t prev =
+        __hip_atomic_fetch_add(a.counters + h, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = prev == static_cast<uint32_t>(a.chunks - 1);
+  }
+  __syncthreads();
+  if (!s_last) return;
+
+  auto chunk_part = [&](int cc, int hq) {
+    return a.partial + ((static_cast<size_t>(h) * a.chunks + cc) * QPK + hq) * (HD + 2);
+  };
+  if (tid < QPK) {
+    float M = -INFINITY;
+    for (int cc = 0; cc < a.chunks; ++cc) M = fmaxf(M, load_coherent(chunk_part(cc, tid)));
+    float L = 0.0f;
+    for (int cc = 0; cc < a.chunks; ++cc) {
+      const float* P = chunk_part(cc, tid);
+      L += load_coherent(P + 1) * __expf(load_coherent(P) - M);
+    }
+    mrow[tid] = M;
+    lrow[tid] = L;
+  }
+  __syncthreads();
+  for (int e = tid; e < QPK * HD; e += kGlueThreads) {
+    const int hq = e / HD, d = e % HD;
+    const float M = mrow[hq];
+    float o = 0.0f;
+    for (int cc = 0; cc < a.chunks; ++cc) {
+      const float* P = chunk_part(cc, hq);
+      o += load_coherent(P + 2 + d) * __expf(load_coherent(P) - M);
+    }
+    a.out[static_cast<size_t>(h * QPK + hq) * HD + d] = static_cast<_Float16>(o / lrow[hq]);
+  }
+  if (tid == 0) __hip_atomic_store(a.counters + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+int attn_chunks(int64_t pos) { return static_cast<int>(ceil_div(pos + 1, kChunk)); }
+
+struct AttnPlan {
+  int qpk = 0, chunks = 0;
+  size_t counter_bytes = 0, workspace_bytes = 0;
+};
+
+int plan_attention(int64_t n_heads, int64_t n_kv, int64_t head_dim, int64_t max_seq, int64_t pos,
+                   AttnPlan* p) {
+  NIBBLE_CHECK(head_dim == kHeadDim, "head_dim must be %d, got %lld", kHeadDim,
+               (long long)head_dim);
+  NIBBLE_CHECK(n_kv >= 1 && n_kv <= 65535, "n_kv_heads must be in [1, 65535], got %lld",
+               (long long)n_kv);
+  NIBBLE_CHECK(n_heads >= n_kv && n_heads % n_kv == 0,
+               "n_heads (%lld) must be a multiple of n_kv_heads (%lld)", (long long)n_heads,
+               (long long)n_kv);
+  const int64_t qpk = n_heads / n_kv;
+  NIBBLE_CHECK(qpk == 1 || qpk == 2 || qpk == 4 || qpk == 8,
+               "query heads per kv head must be 1, 2, 4 or 8, got %lld", (long long)qpk);
+  NIBBLE_CHECK(pos >= 0 && pos < max_seq, "pos (%lld) must be in [0, max_seq = %lld)",
+               (long long)pos, (long long)max_seq);
+  // Keeps the chunk count within a grid dimension (<= 8192 chunks).
+  NIBBLE_CHECK(max_seq <= (int64_t(1) << 20), "max_seq above 2^20");
+  p->qpk = static_cast<int>(qpk);
+  p->chunks = attn_chunks(pos);
+  if (p->chunks > 1) {
+    p->counter_bytes = align_up(static_cast<size_t>(n_kv) * 4, 256);
+    p->workspace_bytes = p->counter_bytes + static_cast<size_t>(n_kv) * p->chunks * qpk *
+                                                (kHeadDim + 2) * sizeof(float);
+  }
+  return NIBBLE_OK;
+}
+
+template <int QPK>
+hipError_t launch_attention(const AttnArgs& a, hipStream_t stream) {
+  dim3 grid(static_cast<unsigned>(a.n_kv), static_cast<unsigned>(a.chunks));
+  attention_decode_kernel<QPK><<<grid, kGlueThreads, 0, stream>>>(a);
+  return hipGetLastError();
+}
+
+template <int CH>
+hipError_t launch_rmsnorm(const _Float16* X, const _Float16* W, _Float16* Y, int64_t rows,
+                          int cols, float eps, hipStream_t stream) {
+  rmsnorm_kernel<CH><<<dim3(static_cast<unsigned>(rows)), kGlueThreads, 0, stream>>>(X, W, Y, cols,
+                                                                                    eps);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+}  // namespace nibble
+
+using namespace nibble;
+
+extern "C" int nibble_rmsnorm_f16(const void* X, int64_t rows, int64_t cols, const void* W,
+                                  float eps, void* Y, void* stream_) {
+  NIBBLE_CHECK(rows >= 0 && rows <= 0x7fffffff, "rows must be in [0, 2^31), got %lld",
+               (long long)rows);
+  NIBBLE_CHECK(cols > 0 && cols % 8 == 0 && cols <= kRmsMaxCols,
+               "cols must be a positive multiple of 8 up to %d, got %lld", kRmsMaxCols,
+               (long long)cols);
+  NIBBLE_CHECK(std::isfinite(eps) && eps >= 0.0f, "eps must be finite and >= 0");
+  if (rows == 0) return ok();
+  NIBBLE_CHECK(X != nullptr && W != nullptr && Y != nullptr, "null pointer");
+  NIBBLE_CHECK(aligned(X, 16) && aligned(W, 16) && aligned(Y, 16),
+               "X, W and Y must be 16-byte aligned");
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  DeviceGuard guard;
+  int dev = 0;
+  NIBBLE_HIP(guard.enter(stream, &dev));
+  const auto* x = static_cast<const _Float16*>(X);
+  const auto* w = static_cast<const _Float16*>(W);
+  auto* y = static_cast<_Float16*>(Y);
+  const int c = static_cast<int>(cols);
+  const int ch = static_cast<int>(ceil_div(cols, kGlueThreads * 8));
+  hipError_t e = ch <= 1   ? launch_rmsnorm<1>(x, w, y, rows, c, eps, stream)
+                 : ch <= 2 ? launch_rmsnorm<2>(x, w, y, rows, c, eps, stream)
+                 : ch <= 4 ? launch_rmsnorm<4>(x, w, y, rows, c, eps, stream)
+                           : launch_rmsnorm<8>(x, w, y, rows, c, eps, stream);
+  NIBBLE_HIP(e);
+  return ok();
+}
+
+extern "C" size_t nibble_attention_decode_workspace_bytes(int64_t n_heads, int64_t n_kv_heads,
+                                                          int64_t head_dim, int64_t max_seq,
+                                                          int64_t pos, void* stream) {
+  (void)stream;
+  AttnPlan p;
+  if (plan_attention(n_heads, n_kv_heads, head_dim, max_seq, pos, &p) != NIBBLE_OK) return 0;
+  return p.workspace_bytes;
+}
+
+extern "C" size_t nibble_attention_decode_counter_bytes(int64_t n_heads, int64_t n_kv_heads,
+                                                        int64_t head_dim, int64_t max_seq,
+                                                        int64_t pos, void* stream) {
+  (void)stream;
+  AttnPlan p;
+  if (plan_attention(n_heads, n_kv_heads, head_dim, max_seq, pos, &p) != NIBBLE_OK) return 0;
+  return p.counter_bytes;
+}
+
+extern "C" int nibble_attention_decode_f16(const void* QKV, int64_t n_heads, int64_t n_kv_heads,
+                                           int64_t head_dim, void* K_cache, void* V_cache,
+                                           int64_t max_seq, int64_t pos, const void* rope_cos,
+                                           const void* rope_sin, void* Out, void* workspace,
+                                           size_t workspace_bytes, void* stream_) {
+  AttnPlan p;
+  int rc = plan_attention(n_heads, n_kv_heads, head_dim, max_seq, pos, &p);
+  if (rc != NIBBLE_OK) return rc;
+  NIBBLE_CHECK(QKV != nullptr && K_cache != nullptr && V_cache != nullptr && Out != nullptr,
+               "null pointer");
+  NIBBLE_CHECK(aligned(QKV, 16) && aligned(K_cache, 16) && aligned(V_cache, 16) &&
+                   aligned(Out, 16),
+               "qkv, caches and output must be 16-byte aligned");
+  NIBBLE_CHECK((rope_cos == nullptr) == (rope_sin == nullptr),
+               "rope_cos and rope_sin must both be given or both be null");
+  NIBBLE_CHECK(rope_cos == nullptr || (aligned(rope_cos, 4) && aligned(rope_sin, 4)),
+               "rope tables must be 4-byte aligned");
+  if (p.workspace_bytes > 0) {
+    if (workspace == nullptr || workspace_bytes < p.workspace_bytes)
+      return fail(NIBBLE_ERR_WORKSPACE, "attention needs %zu bytes of workspace, got %zu",
+                  p.workspace_bytes, workspace == nullptr ? size_t(0) : workspace_bytes);
+    if (!aligned(workspace, 256))
+      return fail(NIBBLE_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  }
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  DeviceGuard guard;
+  int dev = 0;
+  NIBBLE_HIP(guard.enter(stream, &dev));
+  AttnArgs a;
+  a.qkv = static_cast<const _Float16*>(QKV);
+  a.k_cache = static_cast<_Float16*>(K_cache);
+  a.v_cache = static_cast<_Float16*>(V_cache);
+  a.rope_cos = static_cast<const float*>(rope_cos);
+  a.rope_sin = static_cast<const float*>(rope_sin);
+  a.out = static_cast<_Float16*>(Out);
+  a.counters = p.chunks > 1 ? static_cast<uint32_t*>(workspace) : nullptr;
+  a.partial = p.chunks > 1
+                  ? reinterpret_cast<float*>(static_cast<char*>(workspace) + p.counter_bytes)
+                  : nullptr;
+  a.n_kv = static_cast<int>(n_kv_heads);
+  a.max_seq = static_cast<int>(max_seq);
+  a.pos = static_cast<int>(pos);
+  a.chunks = p.chunks;
+  hipError_t e = p.qpk == 1   ? launch_attention<1>(a, stream)
+                 : p.qpk == 2 ? launch_attention<2>(a, stream)
+                 : p.qpk == 4 ? launch_attention<4>(a, stream)
+                              : launch_attention<8>(a, stream);
+  NIBBLE_HIP(e);
+  return ok();
+}

@@ -24,6 +24,15 @@ gate and up instead and runs them through the SwiGLU epilogue
 (each output column is computed from the same weights, scales and
 activations); it only removes launches.
 
+``glue`` runs a whole token step instead (:class:`GlueDecodeStep`): per
+layer RMSNorm, the q|k|v projection, rotary embedding and grouped-query
+attention over a KV cache of ``pos`` tokens, the o projection with the
+residual add in its epilogue, RMSNorm, gate|up through the SwiGLU epilogue
+and the down projection with the second residual add -- 7 launches per
+layer, every one a kernel of this library.  This is the per-token forward of
+the reference's model decode (bench/bench_model.py:177-188) without the
+embedding lookup and the fp16 lm_head, which are not W4A16.
+
     python -m nibblegemm_amd.decode_step --layers 32
 """
 from __future__ import annotations
@@ -36,10 +45,12 @@ from typing import Dict, List, Tuple
 import torch
 
 from . import harness as H
-from .ops import matmul, matmul_swiglu
+from .glue import attention_bytes, attention_decode, rmsnorm, rope_tables
+from .ops import matmul, matmul_bias, matmul_swiglu
 from .quant import QuantizedWeight, concat_columns, interleave_swiglu, quantize_device
 
-LLAMA3_8B = {"hidden": 4096, "kv": 1024, "intermediate": 14336, "layers": 32}
+LLAMA3_8B = {"hidden": 4096, "kv": 1024, "intermediate": 14336, "layers": 32,
+             "heads": 32, "kv_heads": 8, "rms_eps": 1e-5}
 PROJECTIONS = ("q", "k", "v", "o", "gate", "up", "down")
 
 
@@ -101,6 +112,83 @@ class DecodeStep:
         return len(self.calls)
 
 
+class GlueDecodeStep:
+    """One batch-1 token step of a Llama-shaped decoder at position ``pos``.
+
+    ``layers`` are ``fuse(layer, swiglu=True)`` weight sets.  Each layer owns
+    RMSNorm weights (``1 + 0.05 randn``), and k / v caches
+    [kv_heads, max_seq, 128] whose rows ``0 .. pos - 1`` hold ``randn``
+    (earlier tokens); a step writes row ``pos`` of each.  Replaying a step
+    recomputes the same token at the same position.  The residual stream
+    enters as ``x`` (a ``randn`` row, the embedding lookup's stand-in).  At
+    M = 1 each residual add is the bias of the o / down projection's fused
+    epilogue: ``fp16(fp16(a @ W) + h)``, the bits of the separate adds.
+    """
+
+    def __init__(self, layers: List[Dict[str, QuantizedWeight]], pos: int = 1023,
+                 max_seq: int = 0, cfg=LLAMA3_8B, rope: bool = True, device="cuda",
+                 seed: int = 2):
+        gen = torch.Generator(device=device).manual_seed(seed)
+        h, kvh = cfg["hidden"], cfg["kv_heads"]
+        self.pos = int(pos)
+        self.max_seq = int(max_seq) or self.pos + 1
+        self.eps = float(cfg["rms_eps"])
+        self.layers = layers
+        self.x = torch.randn((1, h), generator=gen, device=device).to(torch.float16)
+        self.norms = []
+        self.caches = []
+        for _ in layers:
+            self.norms.append(tuple(
+                (1.0 + 0.05 * torch.randn(h, generator=gen, device=device)).to(torch.float16)
+                for _ in range(2)))
+            kc = torch.zeros((kvh, self.max_seq, 128), dtype=torch.float16, device=device)
+            vc = torch.zeros_like(kc)
+            kc[:, :self.pos] = torch.randn((kvh, self.pos, 128), generator=gen, device=device)
+            vc[:, :self.pos] = torch.randn((kvh, self.pos, 128), generator=gen, device=device)
+            self.caches.append((kc, vc))
+        self.rope = rope_tables(self.max_seq, device=device) if rope else None
+        self.kv_heads = kvh
+
+    def __call__(self, _i: int = 0) -> torch.Tensor:
+        hs = self.x
+        for layer, (w_attn, w_ffn), (kc, vc) in zip(self.layers, self.norms, self.caches):
+            a = rmsnorm(hs, w_attn, self.eps)
+            qkv = matmul(a, layer["qkv"])
+            att = attention_decode(qkv, kc, vc, self.pos, self.rope)
+            h1 = matmul_bias(att, layer["o"], hs.view(-1))
+            b = rmsnorm(h1, w_ffn, self.eps)
+            g = matmul_swiglu(b, layer["gate_up_swiglu"])
+            hs = matmul_bias(g, layer["down"], h1.view(-1))
+        return hs
+
+    @property
+    def launches(self) -> int:
+        return 7 * len(self.layers)
+
+    def step_bytes(self) -> int:
+        """Weights, caches and norm weights one step reads (activations aside)."""
+        per_layer = attention_bytes(self.kv_heads, self.pos) + 2 * 2 * self.x.numel()
+        return weight_bytes(self.layers) + len(self.layers) * per_layer
+
+
+def measure_glue(layers: List[Dict[str, QuantizedWeight]], pos: int = 1023, trials: int = 10,
+                 warmup: int = 3) -> dict:
+    step = GlueDecodeStep(layers, pos=pos)
+    eager = H.bench(step, reps=1, trials=trials, warmup=warmup)
+    graph = H.bench_graph(step, reps=1, trials=trials, warmup=warmup)
+    nbytes = step.step_bytes()
+    return {
+        "launches": step.launches,
+        "context": pos + 1,
+        "step_gib": round(nbytes / 2**30, 3),
+        "eager_ms": round(eager.median_ms, 4),
+        "graph_ms": round(graph.median_ms, 4),
+        "tok_s": round(1000.0 / eager.median_ms, 1),
+        "graph_tok_s": round(1000.0 / graph.median_ms, 1),
+        "graph_gbps": round(nbytes / (graph.median_ms * 1e-3) / 1e9, 1),
+    }
+
+
 def measure(layers: List[Dict[str, QuantizedWeight]], trials: int = 10, warmup: int = 3) -> dict:
     """Eager and graph-replayed time of one step, as the reference reports it
     (bench_model.py:100-113)."""
@@ -119,7 +207,7 @@ def measure(layers: List[Dict[str, QuantizedWeight]], trials: int = 10, warmup: 
     }
 
 
-def run(n_layers: int = 32, group_size: int = 128, trials: int = 10) -> dict:
+def run(n_layers: int = 32, group_size: int = 128, trials: int = 10, glue_pos: int = 1023) -> dict:
     layers = build_layers(n_layers, group_size=group_size)
     nbytes = weight_bytes(layers)
     res = {"config": f"Llama-3-8B shapes, {n_layers} distinct layers, g={group_size}, M=1",
@@ -128,7 +216,10 @@ def run(n_layers: int = 32, group_size: int = 128, trials: int = 10) -> dict:
     fused = [fuse(layer) for layer in layers]
     res["fused"] = measure(fused, trials)
     del fused
-    res["fused_swiglu"] = measure([fuse(layer, swiglu=True) for layer in layers], trials)
+    swiglu = [fuse(layer, swiglu=True) for layer in layers]
+    res["fused_swiglu"] = measure(swiglu, trials)
+    if glue_pos >= 0:
+        res["glue"] = measure_glue(swiglu, glue_pos, trials)
     return res
 
 
@@ -137,11 +228,13 @@ def main(argv=None) -> int:
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--group-size", type=int, default=128)
     ap.add_argument("--trials", type=int, default=10)
+    ap.add_argument("--glue-pos", type=int, default=1023,
+                    help="position of the full-step (glue) variant's token; -1 skips it")
     args = ap.parse_args(argv)
     if not torch.cuda.is_available():
         print("decode_step needs a GPU", file=sys.stderr)
         return 1
-    print(json.dumps(run(args.layers, args.group_size, args.trials)), flush=True)
+    print(json.dumps(run(args.layers, args.group_size, args.trials, args.glue_pos)), flush=True)
     return 0
 
 
