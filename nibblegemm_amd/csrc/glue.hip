@@ -27,24 +27,61 @@ constexpr int kRopeHalf = kHeadDim / 2;
 constexpr int kChunk = 128;  // cached tokens per attention workgroup
 constexpr int kGlueThreads = 256;
 constexpr int kRmsMaxCols = kGlueThreads * 8 * 8;
+constexpr int kAttnMaxSeq = 1 << 16;
+constexpr int kAttnMaxChunks = kAttnMaxSeq / kChunk;
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+// Cross-lane reductions on DPP moves (VALU latency, no LDS round trip).
+// Within each 16-lane row: partners lane ^ 1, lane ^ 2 (quad permutes), then
+// the mirrored lane of the 8-lane half and of the row, so after four steps
+// every lane of the row holds the row's total -- the same bits in every lane,
+// since each step adds the same two values in either lane.  A wave's total
+// adds its four row totals in row order (readlane).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+constexpr int kDppXor1 = 0xB1;         // quad_perm [1, 0, 3, 2]
+constexpr int kDppXor2 = 0x4E;         // quad_perm [2, 3, 0, 1]
+constexpr int kDppHalfMirror = 0x141;  // lane i <-> 7 - i within each 8 lanes
+constexpr int kDppMirror = 0x140;      // lane i <-> 15 - i within each 16 lanes
+
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp<kDppXor1>(v);
+  v += dpp<kDppXor2>(v);
+  v += dpp<kDppHalfMirror>(v);
+  v += dpp<kDppMirror>(v);
   return v;
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp<kDppXor1>(v));
+  v = fmaxf(v, dpp<kDppXor2>(v));
+  v = fmaxf(v, dpp<kDppHalfMirror>(v));
+  v = fmaxf(v, dpp<kDppMirror>(v));
   return v;
+}
+
+__device__ __forceinline__ float lane_value(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+  v = row16_sum(v);
+  return ((lane_value(v, 0) + lane_value(v, 16)) + lane_value(v, 32)) + lane_value(v, 48);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+  v = row16_max(v);
+  return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
 }
 
 // y = fp16(x * r * w) with r = 1 / sqrt(mean(x^2) + eps), in fp32 (the
 // transformers LlamaRMSNorm computes the same in fp32 and rounds x * r to
 // fp16 before the weight; this rounds once).  One workgroup per row; each
 // thread holds CH 16-byte chunks of the row.  The sum of squares is reduced
-// per wave by a butterfly and across waves in wave order: deterministic.
+// per wave (DPP rows, then rows in order) and across waves in wave order:
+// deterministic.
 template <int CH>
 __global__ __launch_bounds__(kGlueThreads) void rmsnorm_kernel(const _Float16* __restrict__ X,
                                                                const _Float16* __restrict__ W,
@@ -53,12 +90,13 @@ __global__ __launch_bounds__(kGlueThreads) void rmsnorm_kernel(const _Float16* _
   __shared__ float part[kGlueThreads / 64];
   const int tid = threadIdx.x;
   const size_t base = static_cast<size_t>(blockIdx.x) * cols;
-  h8_t v[CH];
+  h8_t v[CH], w[CH];
   float ss = 0.0f;
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     const int col = (c * kGlueThreads + tid) * 8;
     v[c] = col < cols ? *reinterpret_cast<const h8_t*>(X + base + col) : h8_t{};
+    w[c] = col < cols ? *reinterpret_cast<const h8_t*>(W + col) : h8_t{};  // before the reduction
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const float f = static_cast<float>(v[c][i]);
@@ -76,11 +114,10 @@ __global__ __launch_bounds__(kGlueThreads) void rmsnorm_kernel(const _Float16* _
   for (int c = 0; c < CH; ++c) {
     const int col = (c * kGlueThreads + tid) * 8;
     if (col < cols) {
-      const h8_t w = *reinterpret_cast<const h8_t*>(W + col);
       h8_t y;
 #pragma unroll
       for (int i = 0; i < 8; ++i)
-        y[i] = static_cast<_Float16>(static_cast<float>(v[c][i]) * r * static_cast<float>(w[i]));
+        y[i] = static_cast<_Float16>(static_cast<float>(v[c][i]) * r * static_cast<float>(w[c][i]));
       *reinterpret_cast<h8_t*>(Y + base + col) = y;
     }
   }
@@ -116,18 +153,27 @@ __device__ __forceinline__ float rope_at(const _Float16* x, int d, const AttnArg
 // its k (rotated, rounded to fp16 as the cache holds it) and v come from qkv
 // and are written into the caches by the workgroup of the last chunk.
 //
-//   1. scores: 16 groups of 16 lanes, a group per token row (lane j holds
-//      dims 8j..8j+7: one 16-byte load), summed over the group by butterfly;
+// 16 groups of 16 lanes each take every 16th token of the chunk; lane j of a
+// group holds dims 8j..8j+7 of the token's rows (one 16-byte load each).  All
+// of a lane's k and v rows are loaded at entry, before anything else: they
+// depend on nothing, so the chunk costs one memory round trip instead of one
+// per token.
+//   1. scores: per token, QPK dot products summed over the 16-lane group
+//      (one DPP row);
 //   2. softmax within the chunk: max, exp, sum per head (one wave a head);
-//   3. P V: the same row layout, each lane accumulating QPK x 8 outputs,
-//      then the 16 groups summed in LDS in group order.
+//   3. P V: each lane accumulates QPK x 8 outputs, then the 16 groups are
+//      summed in LDS in group order.
 // With one chunk the output is written directly.  Otherwise each workgroup
 // publishes (max, sum, unnormalised P V) with device-coherent stores and the
-// last workgroup of the kv head (agent-scope counter) combines the chunks in
-// chunk order: deterministic, one launch.
+// last workgroup of the kv head (agent-scope counter) combines the chunks:
+// per head, the global max, the chunk weights exp(max_c - max) and the total
+// are formed in LDS (fixed order), then every output sums its chunks in chunk
+// order.  The first 8 to 32 chunks' partial outputs are loaded in the same
+// round as the maxima and sums.  Deterministic, one launch.
 template <int QPK>
 __global__ __launch_bounds__(kGlueThreads) void attention_decode_kernel(AttnArgs a) {
   constexpr int HD = kHeadDim;
+  constexpr int TPG = kChunk / 16;  // tokens per 16-lane group
   constexpr float kScale = 0.08838834764831845f;  // 1 / sqrt(128)
   __shared__ float qs[QPK][HD];
   __shared__ __attribute__((aligned(16))) _Float16 knew[HD];
@@ -135,6 +181,8 @@ __global__ __launch_bounds__(kGlueThreads) void attention_decode_kernel(AttnArgs
   __shared__ float sc[QPK][kChunk];
   __shared__ float red[16][QPK][HD];
   __shared__ float mrow[QPK], lrow[QPK];
+  __shared__ float wchunk[kAttnMaxChunks][QPK];  // chunk max, then chunk weight
+  __shared__ float lchunk[kAttnMaxChunks][QPK];  // chunk sum
   __shared__ int s_last;
 
   const int tid = threadIdx.x;
@@ -149,6 +197,21 @@ __global__ __launch_bounds__(kGlueThreads) void attention_decode_kernel(AttnArgs
   const _Float16* kx = a.qkv + static_cast<size_t>(n_heads) * HD + static_cast<size_t>(h) * HD;
   const _Float16* vx = kx + static_cast<size_t>(a.n_kv) * HD;
   const size_t row0 = static_cast<size_t>(h) * a.max_seq;  // cache row of token 0
+  const int g16 = tid >> 4;
+  const int j = tid & 15;
+
+  h8_t kr[TPG], vr[TPG];
+#pragma unroll
+  for (int u = 0; u < TPG; ++u) {
+    const int t = t0 + g16 + 16 * u;
+    kr[u] = h8_t{};
+    vr[u] = h8_t{};
+    if (t < t1 && t != a.pos) {
+      const size_t off = (row0 + t) * HD + 8 * j;
+      kr[u] = *reinterpret_cast<const h8_t*>(a.k_cache + off);
+      vr[u] = *reinterpret_cast<const h8_t*>(a.v_cache + off);
+    }
+  }
 
   for (int e = tid; e < QPK * HD; e += kGlueThreads) {
     const int hq = e / HD, d = e % HD;
@@ -164,32 +227,34 @@ __global__ __launch_bounds__(kGlueThreads) void attention_decode_kernel(AttnArgs
   }
   __syncthreads();
 
-  const int g16 = tid >> 4;
-  const int j = tid & 15;
   float qr[QPK][8];
 #pragma unroll
   for (int hq = 0; hq < QPK; ++hq)
 #pragma unroll
     for (int i = 0; i < 8; ++i) qr[hq][i] = qs[hq][8 * j + i];
-  for (int t = t0 + g16; t < t1; t += 16) {
-    const h8_t k8 = t == a.pos
-                        ? *reinterpret_cast<const h8_t*>(&knew[8 * j])
-                        : *reinterpret_cast<const h8_t*>(a.k_cache + (row0 + t) * HD + 8 * j);
-    float s[QPK];
 #pragma unroll
-    for (int hq = 0; hq < QPK; ++hq) {
-      s[hq] = 0.0f;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) s[hq] = __builtin_fmaf(qr[hq][i], static_cast<float>(k8[i]), s[hq]);
+  for (int u = 0; u < TPG; ++u) {
+    const int t = t0 + g16 + 16 * u;
+    if (t == a.pos) {
+      kr[u] = *reinterpret_cast<const h8_t*>(&knew[8 * j]);
+      vr[u] = *reinterpret_cast<const h8_t*>(&vnew[8 * j]);
     }
-    // Partners of a 16-lane group stay in the group, whose lanes share t.
+    // The whole 16-lane group (a DPP row) shares t, so all its lanes take
+    // part in the row sum.
+    if (t < t1) {
+      float s[QPK];
 #pragma unroll
-    for (int off = 8; off > 0; off >>= 1)
+      for (int hq = 0; hq < QPK; ++hq) {
+        s[hq] = 0.0f;
 #pragma unroll
-      for (int hq = 0; hq < QPK; ++hq) s[hq] += __shfl_xor(s[hq], off);
-    if (j == 0) {
+        for (int i = 0; i < 8; ++i)
+          s[hq] = __builtin_fmaf(qr[hq][i], static_cast<float>(kr[u][i]), s[hq]);
+        s[hq] = row16_sum(s[hq]);
+      }
+      if (j == 0) {
 #pragma unroll
-      for (int hq = 0; hq < QPK; ++hq) sc[hq][t - t0] = s[hq];
+        for (int hq = 0; hq < QPK; ++hq) sc[hq][t - t0] = s[hq];
+      }
     }
   }
   __syncthreads();
@@ -218,15 +283,17 @@ __global__ __launch_bounds__(kGlueThreads) void attention_decode_kernel(AttnArgs
   for (int hq = 0; hq < QPK; ++hq)
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[hq][i] = 0.0f;
-  for (int t = t0 + g16; t < t1; t += 16) {
-    const h8_t v8 = t == a.pos
-                        ? *reinterpret_cast<const h8_t*>(&vnew[8 * j])
-                        : *reinterpret_cast<const h8_t*>(a.v_cache + (row0 + t) * HD + 8 * j);
 #pragma unroll
-    for (int hq = 0; hq < QPK; ++hq) {
-      const float p = sc[hq][t - t0];
+  for (int u = 0; u < TPG; ++u) {
+    const int t = t0 + g16 + 16 * u;
+    if (t < t1) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[hq][i] = __builtin_fmaf(p, static_cast<float>(v8[i]), acc[hq][i]);
+      for (int hq = 0; hq < QPK; ++hq) {
+        const float p = sc[hq][t - t0];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          acc[hq][i] = __builtin_fmaf(p, static_cast<float>(vr[u][i]), acc[hq][i]);
+      }
     }
   }
 #pragma unroll
@@ -267,25 +334,63 @@ __global__ __launch_bounds__(kGlueThreads) void attention_decode_kernel(AttnArgs
   auto chunk_part = [&](int cc, int hq) {
     return a.partial + ((static_cast<size_t>(h) * a.chunks + cc) * QPK + hq) * (HD + 2);
   };
+  // One round of loads for up to PRE chunks: every chunk's (max, sum) into
+  // LDS, and this thread's partial outputs of the first PRE chunks into
+  // registers, all issued together.
+  constexpr int OUTS = (QPK * HD + kGlueThreads - 1) / kGlueThreads;  // outputs per thread
+  constexpr int PRE = 32 / OUTS;
+  float pv[OUTS][PRE];
+#pragma unroll
+  for (int k = 0; k < OUTS; ++k) {
+    const int e = tid + k * kGlueThreads;
+#pragma unroll
+    for (int u = 0; u < PRE; ++u)
+      pv[k][u] = e < QPK * HD && u < a.chunks
+                     ? load_coherent(chunk_part(u, e / HD) + 2 + e % HD)
+                     : 0.0f;
+  }
+  for (int e = tid; e < a.chunks * QPK; e += kGlueThreads) {
+    const float* P = chunk_part(e / QPK, e % QPK);
+    wchunk[e / QPK][e % QPK] = load_coherent(P);
+    lchunk[e / QPK][e % QPK] = load_coherent(P + 1);
+  }
+  __syncthreads();
+  // Per head, over the chunks in order: the global max M, the chunk weights
+  // exp(max_c - M), and the total L = sum_c sum_c * weight_c.
   if (tid < QPK) {
     float M = -INFINITY;
-    for (int cc = 0; cc < a.chunks; ++cc) M = fmaxf(M, load_coherent(chunk_part(cc, tid)));
-    float L = 0.0f;
-    for (int cc = 0; cc < a.chunks; ++cc) {
-      const float* P = chunk_part(cc, tid);
-      L += load_coherent(P + 1) * __expf(load_coherent(P) - M);
-    }
+    for (int cc = 0; cc < a.chunks; ++cc) M = fmaxf(M, wchunk[cc][tid]);
     mrow[tid] = M;
+  }
+  __syncthreads();
+  for (int e = tid; e < a.chunks * QPK; e += kGlueThreads) {
+    const int cc = e / QPK, hq = e % QPK;
+    wchunk[cc][hq] = __expf(wchunk[cc][hq] - mrow[hq]);
+  }
+  __syncthreads();
+  if (tid < QPK) {
+    float L = 0.0f;
+    for (int cc = 0; cc < a.chunks; ++cc) L += lchunk[cc][tid] * wchunk[cc][tid];
     lrow[tid] = L;
   }
   __syncthreads();
-  for (int e = tid; e < QPK * HD; e += kGlueThreads) {
+#pragma unroll
+  for (int k = 0; k < OUTS; ++k) {
+    const int e = tid + k * kGlueThreads;
+    if (e >= QPK * HD) continue;
     const int hq = e / HD, d = e % HD;
-    const float M = mrow[hq];
     float o = 0.0f;
-    for (int cc = 0; cc < a.chunks; ++cc) {
-      const float* P = chunk_part(cc, hq);
-      o += load_coherent(P + 2 + d) * __expf(load_coherent(P) - M);
+#pragma unroll
+    for (int u = 0; u < PRE; ++u)
+      if (u < a.chunks) o += pv[k][u] * wchunk[u][hq];
+    for (int c0 = PRE; c0 < a.chunks; c0 += 8) {  // beyond the prefetch: eight loads a round
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        v[u] = c0 + u < a.chunks ? load_coherent(chunk_part(c0 + u, hq) + 2 + d) : 0.0f;
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (c0 + u < a.chunks) o += v[u] * wchunk[c0 + u][hq];
     }
     a.out[static_cast<size_t>(h * QPK + hq) * HD + d] = static_cast<_Float16>(o / lrow[hq]);
   }
@@ -313,8 +418,8 @@ int plan_attention(int64_t n_heads, int64_t n_kv, int64_t head_dim, int64_t max_
                "query heads per kv head must be 1, 2, 4 or 8, got %lld", (long long)qpk);
   NIBBLE_CHECK(pos >= 0 && pos < max_seq, "pos (%lld) must be in [0, max_seq = %lld)",
                (long long)pos, (long long)max_seq);
-  // Keeps the chunk count within a grid dimension (<= 8192 chunks).
-  NIBBLE_CHECK(max_seq <= (int64_t(1) << 20), "max_seq above 2^20");
+  // The combine keeps every chunk's (max, sum) in LDS: at most 512 chunks.
+  NIBBLE_CHECK(max_seq <= kAttnMaxSeq, "max_seq above %d", kAttnMaxSeq);
   p->qpk = static_cast<int>(qpk);
   p->chunks = attn_chunks(pos);
   if (p->chunks > 1) {
