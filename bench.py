@@ -165,7 +165,9 @@ def main() -> int:
             f"({decode['projections']['launches']} launches), fused "
             f"{decode['fused']['graph_tok_s']} tok/s ({decode['fused']['launches']} launches), "
             f"with the SwiGLU epilogue {decode['fused_swiglu']['graph_tok_s']} tok/s; "
-            f"{time.perf_counter() - t0:.1f} s")
+            f"full step with norms, attention over {decode['glue']['context']} tokens and "
+            f"residual adds {decode['glue']['graph_tok_s']} tok/s ({decode['glue']['launches']} "
+            f"launches); {time.perf_counter() - t0:.1f} s")
 
     prefill = None
     if not args.skip_prefill:
