@@ -50,7 +50,7 @@
 extern "C" {
 #endif
 
-#define NIBBLE_ABI_VERSION 4
+#define NIBBLE_ABI_VERSION 5
 
 #if defined(__GNUC__) || defined(__clang__)
 #define NIBBLE_API __attribute__((visibility("default")))
@@ -142,6 +142,12 @@ NIBBLE_API size_t nibble_gemm_counter_bytes(int64_t M, int64_t K, int64_t N, int
  *               multiple of 64, nibblegemm_amd.quant.interleave_swiglu);
  *               Y [M, N/2] = silu(G) * U with G, U and silu(G) rounded to
  *               fp16 as the unfused fp16 ops would.
+ * A non-null `norm_weight` (fp16 [K], 16-byte aligned) fuses an RMSNorm
+ * prologue: the product is taken with fp16(x * r * norm_weight) per row of X,
+ * r = 1 / sqrt(mean(x^2) + norm_eps) -- the same bits as nibble_rmsnorm_f16
+ * followed by this call without it.  It needs M <= 8, K <= 16384 and the
+ * normalised row block (M rounded up to 1, 2, 4 or 8 rows, times K fp16)
+ * within 64 KiB.
  * Requires N % 4 == 0, group_size in {64, 128}, X and Wq 16-byte and S, Y
  * 8-byte aligned (NIBBLE_ERR_INVALID_ARGUMENT otherwise; there is no other
  * kernel to fall back to).  `workspace` as for nibble_gemv_w4a16, sized by
@@ -150,7 +156,8 @@ NIBBLE_API size_t nibble_gemm_counter_bytes(int64_t M, int64_t K, int64_t N, int
 NIBBLE_API int nibble_matmul_w4a16_fused(const void* X, int64_t x_rows, int64_t x_cols,
                       const void* Wq, int64_t wq_rows, int64_t wq_cols,
                       const void* S, int64_t s_rows, int64_t s_cols,
-                      int64_t group_size, int64_t epilogue, const void* bias, void* Y,
+                      int64_t group_size, int64_t epilogue, const void* bias,
+                      const void* norm_weight, float norm_eps, void* Y,
                       void* workspace, size_t workspace_bytes, void* stream);
 NIBBLE_API size_t nibble_matmul_fused_workspace_bytes(int64_t M, int64_t K, int64_t N,
                                            int64_t group_size, void* stream);
@@ -191,7 +198,8 @@ NIBBLE_API int nibble_rmsnorm_f16(const void* X, int64_t rows, int64_t cols, con
  * 0 .. pos, query head i reading kv head i / (n_heads / n_kv_heads).
  * rope_cos / rope_sin fp32 [max_seq][64] (both or neither) apply the
  * rotary embedding to q and k in the rotate-half pairing; NULL skips it.
- * head_dim must be 128 and n_heads / n_kv_heads 1, 2, 4 or 8.  Positions
+ * head_dim must be 128, n_heads / n_kv_heads 1, 2, 4 or 8, and
+ * 0 <= pos < max_seq <= 65536.  Positions
  * beyond 127 split across workgroups: `workspace` (256-byte aligned, its
  * leading nibble_attention_decode_counter_bytes(...) zero before the first
  * call, restored to zero by each call) must then hold

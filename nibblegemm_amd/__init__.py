@@ -14,7 +14,7 @@ of this package.  Symmetric GPTQ / AWQ 4-bit checkpoints are ingested by
 
 from . import convert
 from .ops import (DECODE_MAX_M, QuantLinear, dequant, extension, gemm, gemv, matmul, matmul_bias,
-                  matmul_swiglu)
+                  matmul_swiglu, rmsnorm_matmul)
 from .quant import (
     QuantizedWeight,
     concat_columns,
@@ -46,6 +46,7 @@ __all__ = [
     "quantize",
     "quantize_device",
     "reference_matmul",
+    "rmsnorm_matmul",
     "unpack_nibbles",
 ]
 __version__ = "0.1.0"

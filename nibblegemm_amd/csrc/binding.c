@@ -99,21 +99,24 @@ static PyObject* py_gemm_ws(PyObject* self, PyObject* const* a, Py_ssize_t n) {
   return Py_BuildValue("(nn)", (Py_ssize_t)ws, (Py_ssize_t)cb);
 }
 
-/* matmul_fused(X, xr, xc, Wq, wr, wc, S, sr, sc, g, epilogue, bias, Y, ws, ws_bytes, stream) */
+/* matmul_fused(X, xr, xc, Wq, wr, wc, S, sr, sc, g, epilogue, bias, norm_w, norm_eps, Y, ws,
+ *              ws_bytes, stream) */
 static PyObject* py_fused(PyObject* self, PyObject* const* a, Py_ssize_t n) {
   (void)self;
-  if (!nargs_is(n, 16, "matmul_fused")) return NULL;
-  void *X, *Wq, *S, *bias, *Y, *ws, *stream;
+  if (!nargs_is(n, 18, "matmul_fused")) return NULL;
+  void *X, *Wq, *S, *bias, *norm, *Y, *ws, *stream;
   long long xr, xc, wr, wc, sr, sc, g, ep, wsb;
+  double eps = PyFloat_AsDouble(a[13]);
+  if (eps == -1.0 && PyErr_Occurred()) return NULL;
   if (!take_ptr(a[0], &X) || !take_i64(a[1], &xr) || !take_i64(a[2], &xc) ||
       !take_ptr(a[3], &Wq) || !take_i64(a[4], &wr) || !take_i64(a[5], &wc) ||
       !take_ptr(a[6], &S) || !take_i64(a[7], &sr) || !take_i64(a[8], &sc) ||
       !take_i64(a[9], &g) || !take_i64(a[10], &ep) || !take_ptr(a[11], &bias) ||
-      !take_ptr(a[12], &Y) || !take_ptr(a[13], &ws) || !take_i64(a[14], &wsb) ||
-      !take_ptr(a[15], &stream))
+      !take_ptr(a[12], &norm) || !take_ptr(a[14], &Y) || !take_ptr(a[15], &ws) ||
+      !take_i64(a[16], &wsb) || !take_ptr(a[17], &stream))
     return NULL;
-  int rc = nibble_matmul_w4a16_fused(X, xr, xc, Wq, wr, wc, S, sr, sc, g, ep, bias, Y, ws,
-                                     (size_t)(wsb < 0 ? 0 : wsb), stream);
+  int rc = nibble_matmul_w4a16_fused(X, xr, xc, Wq, wr, wc, S, sr, sc, g, ep, bias, norm,
+                                     (float)eps, Y, ws, (size_t)(wsb < 0 ? 0 : wsb), stream);
   return PyLong_FromLong(rc);
 }
 

@@ -34,9 +34,11 @@
 // Versions 0 and 1 are scalar fp32 kernels, one thread per output (the
 // reference's v0/v1, :30-72): an on-device reference, not a fast path.
 #include <algorithm>
+#include <cmath>
 
 #include "nibble_common.h"
 #include "nibble_decode.h"
+#include "nibble_reduce.h"
 #include "stream_matmul.h"
 
 namespace nibble {
@@ -57,6 +59,8 @@ struct GemvArgs {
   int splits;
   int epilogue;           // kEpilogueNone / kEpilogueBias / kEpilogueSwiglu
   const _Float16* bias;   // [N] for kEpilogueBias
+  const _Float16* norm_w; // [K]: the activations are RMSNorm(X) * norm_w (fused prologue), or null
+  float norm_eps;
 };
 
 // Output epilogues of the streaming kernel (fused forms of what a caller
@@ -117,7 +121,12 @@ __device__ __forceinline__ void emit_outputs(const GemvArgs& a, int strip, int m
 // packed words and scales are loaded with the non-temporal hint -- measured
 // 1-2% faster at M <= 32; launches of several row blocks re-read the weights
 // from cache and keep the default policy.
-template <int MT, int GROUP, int WAVES, bool STREAM>
+// NORM: the activations are RMSNorm rows of X, fp16(x * r * norm_w) with r
+// the row's 1 / sqrt(mean(x^2) + eps).  A prologue computes r exactly as the
+// RMSNorm kernel does (same chunking, same fixed-order reduction, so the
+// same bits), writes the normalised rows of the workgroup's block to LDS
+// once, and the loop reads its activation chunks from there instead of X.
+template <int MT, int GROUP, int WAVES, bool STREAM, bool NORM = false>
 __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs a) {
   constexpr int kWPolicy = STREAM ? 2 : 0;  // buffer-load cache policy: 2 = nt
   constexpr int CPG = GROUP / 32;                  // 32-k chunks per quant group
@@ -126,6 +135,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs a) {
   constexpr int THREADS = WAVES * 64;
   __shared__ f4_t red[WAVES][MT][16];              // [wave][row][column quad]
   __shared__ int s_last;
+  extern __shared__ __attribute__((aligned(16))) _Float16 xnorm[];  // NORM: [MT][K]
+  static_assert(!NORM || THREADS == kRmsThreads, "the RMSNorm prologue runs on 256 threads");
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -160,6 +171,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs a) {
     h8_t x[TILES][CPG];
     h4_t s;
     u4_t w[CPG];
+    int g;
   };
   // Loads of group g.  A prefetch past the split re-reads the split's last
   // group (just loaded, so an L2 hit) instead of being predicated off: the
@@ -174,12 +186,15 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs a) {
     g = enabled ? g : ge - 1;
     const uint32_t kx = static_cast<uint32_t>(g) * GROUP * 2u;
     const uint32_t kw = static_cast<uint32_t>(g) * (GROUP / 8) * row_bytes;
+    st.g = g;
+    if constexpr (!NORM) {
 #pragma unroll
-    for (int t = 0; t < TILES; ++t)
+      for (int t = 0; t < TILES; ++t)
 #pragma unroll
-      for (int c = 0; c < CPG; ++c)
-        st.x[t][c] = __builtin_bit_cast(
-            h8_t, __builtin_amdgcn_raw_buffer_load_b128(rx, voff_x[t], kx + c * 64, 0));
+        for (int c = 0; c < CPG; ++c)
+          st.x[t][c] = __builtin_bit_cast(
+              h8_t, __builtin_amdgcn_raw_buffer_load_b128(rx, voff_x[t], kx + c * 64, 0));
+    }
     st.s = __builtin_bit_cast(
         h4_t, __builtin_amdgcn_raw_buffer_load_b64(rs, voff_s, static_cast<uint32_t>(g) * a.N * 2u,
                                                    kWPolicy));
@@ -203,8 +218,19 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs a) {
     f4_t acc[TILES][4];
 #pragma unroll
     for (int t = 0; t < TILES; ++t) {
+      if constexpr (NORM) {
+        // Lane (q, kb) takes row 16 t + q, k = g GROUP + 32 c + 8 kb + 0..7.
+        const int m = 16 * t + q;
 #pragma unroll
-      for (int c = 0; c < CPG; ++c) xs[t][c] = st.x[t][c] * xscale;
+        for (int c = 0; c < CPG; ++c)
+          xs[t][c] = (m < mrows ? *reinterpret_cast<const h8_t*>(
+                                      &xnorm[m * a.K + st.g * GROUP + 32 * c + 8 * kb])
+                                : h8_t{}) *
+                     xscale;
+      } else {
+#pragma unroll
+        for (int c = 0; c < CPG; ++c) xs[t][c] = st.x[t][c] * xscale;
+      }
       f4_t corr = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int c = 0; c < CPG; ++c) corr = mfma16(xs[t][c], bcorr, corr);
@@ -230,6 +256,34 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs a) {
           tot[t][j][i] = __builtin_fmaf(sj, acc[t][j][i], tot[t][j][i]);
     }
   };
+
+  if constexpr (NORM) {
+    // Rows of this block, normalised into LDS.  Thread t holds chunks
+    // (256 c + t) * 8 of a row (K <= 16384: at most 8), x and the weight
+    // loaded before the reduction, as in the RMSNorm kernel.
+    __shared__ float part[kRmsThreads / 64];
+    constexpr int kMaxChunks = 8;
+    const int tid = threadIdx.x;
+    for (int r = 0; r < mrows; ++r) {
+      const _Float16* xr = a.X + static_cast<size_t>(m_base + r) * a.K;
+      h8_t v[kMaxChunks], w[kMaxChunks];
+      float ss = 0.0f;
+#pragma unroll
+      for (int c = 0; c < kMaxChunks; ++c) {
+        const int col = (c * kRmsThreads + tid) * 8;
+        v[c] = col < a.K ? *reinterpret_cast<const h8_t*>(xr + col) : h8_t{};
+        w[c] = col < a.K ? *reinterpret_cast<const h8_t*>(a.norm_w + col) : h8_t{};
+        ss = sumsq_chunk(v[c], ss);
+      }
+      const float rr = rms_scale(block256_sum(ss, part), a.K, a.norm_eps);
+#pragma unroll
+      for (int c = 0; c < kMaxChunks; ++c) {
+        const int col = (c * kRmsThreads + tid) * 8;
+        if (col < a.K) *reinterpret_cast<h8_t*>(&xnorm[r * a.K + col]) = rms_apply(v[c], w[c], rr);
+      }
+      __syncthreads();  // before `part` is written again, and before the loop reads xnorm
+    }
+  }
 
   // Groups gb + wave, gb + wave + WAVES, ... with the next group's loads in
   // flight while the current one is computed.  The scheduling barriers keep
@@ -377,6 +431,18 @@ constexpr int kGroupsPerWave = 8;
 template <int MT, int GROUP, bool STREAM>
 hipError_t launch_mts(const GemvArgs& a, const StreamPlan& p, hipStream_t stream) {
   dim3 grid(p.strips, p.splits, p.mblocks);
+  if (a.norm_w != nullptr) {
+    // The fused-RMSNorm form: one row block of at most 8 rows, 4 waves
+    // (validated on the host), the block's normalised rows in dynamic LDS.
+    if constexpr (MT <= 8) {
+      if (p.waves != 4 || p.mblocks != 1) return hipErrorInvalidValue;
+      const size_t lds = static_cast<size_t>(MT) * a.K * sizeof(_Float16);
+      gemv_mfma_kernel<MT, GROUP, 4, STREAM, true><<<grid, 256, lds, stream>>>(a);
+      return hipGetLastError();
+    } else {
+      return hipErrorInvalidValue;
+    }
+  }
   switch (p.waves) {
     case 1: gemv_mfma_kernel<MT, GROUP, 1, STREAM><<<grid, 64, 0, stream>>>(a); break;
     case 2: gemv_mfma_kernel<MT, GROUP, 2, STREAM><<<grid, 128, 0, stream>>>(a); break;
@@ -471,7 +537,7 @@ bool stream_supported(const void* X, const void* Wq, const void* S, const void* 
 int launch_stream(const void* X, const void* Wq, const void* S, void* Y, int64_t M, int64_t K,
                   int64_t N, int64_t G, const StreamPlan& p, void* workspace,
                   size_t workspace_bytes, hipStream_t stream, const char* who, int epilogue,
-                  const void* bias) {
+                  const void* bias, const void* norm_w, float norm_eps) {
   if (p.workspace_bytes > 0) {
     if (workspace == nullptr || workspace_bytes < p.workspace_bytes)
       return fail(NIBBLE_ERR_WORKSPACE, "%s needs %zu bytes of workspace, got %zu", who,
@@ -495,6 +561,8 @@ int launch_stream(const void* X, const void* Wq, const void* S, void* Y, int64_t
   a.splits = p.splits;
   a.epilogue = epilogue;
   a.bias = static_cast<const _Float16*>(bias);
+  a.norm_w = static_cast<const _Float16*>(norm_w);
+  a.norm_eps = norm_eps;
   hipError_t e = G == 128 ? launch_group<128>(a, p, stream) : launch_group<64>(a, p, stream);
   if (e != hipSuccess) return hip_fail(e, who);
   return NIBBLE_OK;
@@ -664,7 +732,8 @@ extern "C" int nibble_gemv_w4a16(const void* X, int64_t x_rows, int64_t x_cols, 
 namespace {
 int validate_fused(const void* X, int64_t x_rows, int64_t x_cols, const void* Wq, int64_t wq_rows,
                    int64_t wq_cols, const void* S, int64_t s_rows, int64_t s_cols,
-                   int64_t group_size, int64_t epilogue, const void* bias, const void* Y) {
+                   int64_t group_size, int64_t epilogue, const void* bias, const void* norm_w,
+                   float norm_eps, const void* Y) {
   NIBBLE_CHECK(x_rows >= 0 && x_cols > 0 && wq_rows >= 0 && wq_cols > 0 && s_rows >= 0 && s_cols >= 0,
                "bad dimension (K and N must be positive)");
   const int64_t M = x_rows, K = x_cols, N = wq_cols;
@@ -682,6 +751,18 @@ int validate_fused(const void* X, int64_t x_rows, int64_t x_cols, const void* Wq
                "swiglu needs N (gate|up interleaved in 32-column blocks) to be a multiple of 64");
   NIBBLE_CHECK(epilogue != kEpilogueBias || M == 0 || bias != nullptr, "null bias");
   NIBBLE_CHECK(epilogue != kEpilogueBias || aligned(bias, 2), "misaligned bias");
+  if (norm_w != nullptr) {
+    NIBBLE_CHECK(M <= kNormMaxM, "the fused RMSNorm supports M <= %d, got %lld", kNormMaxM,
+                 (long long)M);
+    NIBBLE_CHECK(K <= kNormMaxK, "the fused RMSNorm supports K <= %d, got %lld", kNormMaxK,
+                 (long long)K);
+    // The block's normalised rows live in LDS: mt x K fp16 within 64 KiB.
+    NIBBLE_CHECK(M == 0 || mt_for(M) * K * 2 <= 65536,
+                 "the fused RMSNorm needs %lld rows x K=%lld fp16 of LDS, above 64 KiB",
+                 (long long)mt_for(M), (long long)K);
+    NIBBLE_CHECK(aligned(norm_w, 16), "norm weight must be 16-byte aligned");
+    NIBBLE_CHECK(std::isfinite(norm_eps) && norm_eps >= 0.0f, "norm eps must be finite and >= 0");
+  }
   if (M == 0) return NIBBLE_OK;
   NIBBLE_CHECK(X != nullptr && Wq != nullptr && S != nullptr && Y != nullptr, "null pointer");
   NIBBLE_CHECK(stream_supported(X, Wq, S, Y, M, K, N, group_size),
@@ -714,10 +795,10 @@ extern "C" int nibble_matmul_w4a16_fused(const void* X, int64_t x_rows, int64_t 
                                          const void* Wq, int64_t wq_rows, int64_t wq_cols,
                                          const void* S, int64_t s_rows, int64_t s_cols,
                                          int64_t group_size, int64_t epilogue, const void* bias,
-                                         void* Y, void* workspace, size_t workspace_bytes,
-                                         void* stream_) {
+                                         const void* norm_weight, float norm_eps, void* Y,
+                                         void* workspace, size_t workspace_bytes, void* stream_) {
   int rc = validate_fused(X, x_rows, x_cols, Wq, wq_rows, wq_cols, S, s_rows, s_cols, group_size,
-                          epilogue, bias, Y);
+                          epilogue, bias, norm_weight, norm_eps, Y);
   if (rc != NIBBLE_OK) return rc;
   const int64_t M = x_rows, K = x_cols, N = wq_cols;
   if (M == 0) return ok();
@@ -729,6 +810,7 @@ extern "C" int nibble_matmul_w4a16_fused(const void* X, int64_t x_rows, int64_t 
   int dev = 0;
   NIBBLE_HIP(guard.enter(stream, &dev));
   rc = launch_stream(X, Wq, S, Y, M, K, N, group_size, p, workspace, workspace_bytes, stream,
-                     "fused matmul kernel launch", static_cast<int>(epilogue), bias);
+                     "fused matmul kernel launch", static_cast<int>(epilogue), bias, norm_weight,
+                     norm_eps);
   return rc == NIBBLE_OK ? ok() : rc;
 }

@@ -17,6 +17,7 @@
 
 #include "nibble_common.h"
 #include "nibble_decode.h"
+#include "nibble_reduce.h"
 
 namespace nibble {
 
@@ -26,55 +27,9 @@ constexpr int kHeadDim = 128;
 constexpr int kRopeHalf = kHeadDim / 2;
 constexpr int kChunk = 128;  // cached tokens per attention workgroup
 constexpr int kGlueThreads = 256;
-constexpr int kRmsMaxCols = kGlueThreads * 8 * 8;
+constexpr int kRmsMaxCols = kRmsThreads * 8 * 8;
 constexpr int kAttnMaxSeq = 1 << 16;
 constexpr int kAttnMaxChunks = kAttnMaxSeq / kChunk;
-
-// Cross-lane reductions on DPP moves (VALU latency, no LDS round trip).
-// Within each 16-lane row: partners lane ^ 1, lane ^ 2 (quad permutes), then
-// the mirrored lane of the 8-lane half and of the row, so after four steps
-// every lane of the row holds the row's total -- the same bits in every lane,
-// since each step adds the same two values in either lane.  A wave's total
-// adds its four row totals in row order (readlane).
-template <int CTRL>
-__device__ __forceinline__ float dpp(float v) {
-  return __builtin_bit_cast(
-      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
-constexpr int kDppXor1 = 0xB1;         // quad_perm [1, 0, 3, 2]
-constexpr int kDppXor2 = 0x4E;         // quad_perm [2, 3, 0, 1]
-constexpr int kDppHalfMirror = 0x141;  // lane i <-> 7 - i within each 8 lanes
-constexpr int kDppMirror = 0x140;      // lane i <-> 15 - i within each 16 lanes
-
-__device__ __forceinline__ float row16_sum(float v) {
-  v += dpp<kDppXor1>(v);
-  v += dpp<kDppXor2>(v);
-  v += dpp<kDppHalfMirror>(v);
-  v += dpp<kDppMirror>(v);
-  return v;
-}
-
-__device__ __forceinline__ float row16_max(float v) {
-  v = fmaxf(v, dpp<kDppXor1>(v));
-  v = fmaxf(v, dpp<kDppXor2>(v));
-  v = fmaxf(v, dpp<kDppHalfMirror>(v));
-  v = fmaxf(v, dpp<kDppMirror>(v));
-  return v;
-}
-
-__device__ __forceinline__ float lane_value(float v, int lane) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
-}
-
-__device__ __forceinline__ float wave_sum(float v) {
-  v = row16_sum(v);
-  return ((lane_value(v, 0) + lane_value(v, 16)) + lane_value(v, 32)) + lane_value(v, 48);
-}
-
-__device__ __forceinline__ float wave_max(float v) {
-  v = row16_max(v);
-  return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
-}
 
 // y = fp16(x * r * w) with r = 1 / sqrt(mean(x^2) + eps), in fp32 (the
 // transformers LlamaRMSNorm computes the same in fp32 and rounds x * r to
@@ -83,43 +38,27 @@ __device__ __forceinline__ float wave_max(float v) {
 // per wave (DPP rows, then rows in order) and across waves in wave order:
 // deterministic.
 template <int CH>
-__global__ __launch_bounds__(kGlueThreads) void rmsnorm_kernel(const _Float16* __restrict__ X,
-                                                               const _Float16* __restrict__ W,
-                                                               _Float16* __restrict__ Y, int cols,
-                                                               float eps) {
-  __shared__ float part[kGlueThreads / 64];
+__global__ __launch_bounds__(kRmsThreads) void rmsnorm_kernel(const _Float16* __restrict__ X,
+                                                              const _Float16* __restrict__ W,
+                                                              _Float16* __restrict__ Y, int cols,
+                                                              float eps) {
+  __shared__ float part[kRmsThreads / 64];
   const int tid = threadIdx.x;
   const size_t base = static_cast<size_t>(blockIdx.x) * cols;
   h8_t v[CH], w[CH];
   float ss = 0.0f;
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
-    const int col = (c * kGlueThreads + tid) * 8;
+    const int col = (c * kRmsThreads + tid) * 8;
     v[c] = col < cols ? *reinterpret_cast<const h8_t*>(X + base + col) : h8_t{};
     w[c] = col < cols ? *reinterpret_cast<const h8_t*>(W + col) : h8_t{};  // before the reduction
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float f = static_cast<float>(v[c][i]);
-      ss = __builtin_fmaf(f, f, ss);
-    }
+    ss = sumsq_chunk(v[c], ss);
   }
-  ss = wave_sum(ss);
-  if ((tid & 63) == 0) part[tid >> 6] = ss;
-  __syncthreads();
-  float tot = 0.0f;
-#pragma unroll
-  for (int w = 0; w < kGlueThreads / 64; ++w) tot += part[w];
-  const float r = 1.0f / sqrtf(tot / static_cast<float>(cols) + eps);
+  const float r = rms_scale(block256_sum(ss, part), cols, eps);
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
-    const int col = (c * kGlueThreads + tid) * 8;
-    if (col < cols) {
-      h8_t y;
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        y[i] = static_cast<_Float16>(static_cast<float>(v[c][i]) * r * static_cast<float>(w[c][i]));
-      *reinterpret_cast<h8_t*>(Y + base + col) = y;
-    }
+    const int col = (c * kRmsThreads + tid) * 8;
+    if (col < cols) *reinterpret_cast<h8_t*>(Y + base + col) = rms_apply(v[c], w[c], r);
   }
 }
 

@@ -37,10 +37,17 @@ bool stream_supported(const void* X, const void* Wq, const void* S, const void* 
 // Checks the workspace against the plan and launches on `stream` (whose
 // device must be current).  `epilogue` 0 writes X W; 1 adds `bias` ([N]
 // fp16) in fp16; 2 reads W as gate|up interleaved in 32-column blocks and
-// writes silu(gate) * up ([M, N/2]).  Returns a NIBBLE_* status.
+// writes silu(gate) * up ([M, N/2]).  A non-null `norm_w` ([K] fp16)
+// multiplies by the RMSNorm rows of X instead of X (M <= 8, K <= 16384, the
+// default 4-wave plan).  Returns a NIBBLE_* status.
 int launch_stream(const void* X, const void* Wq, const void* S, void* Y, int64_t M, int64_t K,
                   int64_t N, int64_t G, const StreamPlan& p, void* workspace,
                   size_t workspace_bytes, hipStream_t stream, const char* who, int epilogue = 0,
-                  const void* bias = nullptr);
+                  const void* bias = nullptr, const void* norm_w = nullptr,
+                  float norm_eps = 0.0f);
+
+// Largest K the fused-RMSNorm prologue takes (8 chunks of 256 x 8 columns).
+constexpr int kNormMaxK = 16384;
+constexpr int kNormMaxM = 8;
 
 }  // namespace nibble

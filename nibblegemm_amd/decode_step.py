@@ -28,8 +28,10 @@ activations); it only removes launches.
 layer RMSNorm, the q|k|v projection, rotary embedding and grouped-query
 attention over a KV cache of ``pos`` tokens, the o projection with the
 residual add in its epilogue, RMSNorm, gate|up through the SwiGLU epilogue
-and the down projection with the second residual add -- 7 launches per
-layer, every one a kernel of this library.  This is the per-token forward of
+and the down projection with the second residual add, every one a kernel of
+this library.  Each RMSNorm runs as the prologue of the projection after it
+(:func:`~nibblegemm_amd.ops.rmsnorm_matmul`, the same bits as the separate
+launch), so a layer is 5 launches.  This is the per-token forward of
 the reference's model decode (bench/bench_model.py:177-188) without the
 embedding lookup and the fp16 lm_head, which are not W4A16.
 
@@ -46,7 +48,7 @@ import torch
 
 from . import harness as H
 from .glue import attention_bytes, attention_decode, rmsnorm, rope_tables
-from .ops import matmul, matmul_bias, matmul_swiglu
+from .ops import matmul, matmul_bias, matmul_swiglu, rmsnorm_matmul
 from .quant import QuantizedWeight, concat_columns, interleave_swiglu, quantize_device
 
 LLAMA3_8B = {"hidden": 4096, "kv": 1024, "intermediate": 14336, "layers": 32,
@@ -126,8 +128,8 @@ class GlueDecodeStep:
     """
 
     def __init__(self, layers: List[Dict[str, QuantizedWeight]], pos: int = 1023,
-                 max_seq: int = 0, cfg=LLAMA3_8B, rope: bool = True, device="cuda",
-                 seed: int = 2):
+                 max_seq: int = 0, cfg=LLAMA3_8B, rope: bool = True, fuse_norm: bool = True,
+                 device="cuda", seed: int = 2):
         gen = torch.Generator(device=device).manual_seed(seed)
         h, kvh = cfg["hidden"], cfg["kv_heads"]
         self.pos = int(pos)
@@ -148,22 +150,27 @@ class GlueDecodeStep:
             self.caches.append((kc, vc))
         self.rope = rope_tables(self.max_seq, device=device) if rope else None
         self.kv_heads = kvh
+        self.fuse_norm = fuse_norm
 
     def __call__(self, _i: int = 0) -> torch.Tensor:
         hs = self.x
         for layer, (w_attn, w_ffn), (kc, vc) in zip(self.layers, self.norms, self.caches):
-            a = rmsnorm(hs, w_attn, self.eps)
-            qkv = matmul(a, layer["qkv"])
+            if self.fuse_norm:
+                qkv = rmsnorm_matmul(hs, w_attn, layer["qkv"], self.eps)
+            else:
+                qkv = matmul(rmsnorm(hs, w_attn, self.eps), layer["qkv"])
             att = attention_decode(qkv, kc, vc, self.pos, self.rope)
             h1 = matmul_bias(att, layer["o"], hs.view(-1))
-            b = rmsnorm(h1, w_ffn, self.eps)
-            g = matmul_swiglu(b, layer["gate_up_swiglu"])
+            if self.fuse_norm:
+                g = rmsnorm_matmul(h1, w_ffn, layer["gate_up_swiglu"], self.eps, swiglu=True)
+            else:
+                g = matmul_swiglu(rmsnorm(h1, w_ffn, self.eps), layer["gate_up_swiglu"])
             hs = matmul_bias(g, layer["down"], h1.view(-1))
         return hs
 
     @property
     def launches(self) -> int:
-        return 7 * len(self.layers)
+        return (5 if self.fuse_norm else 7) * len(self.layers)
 
     def step_bytes(self) -> int:
         """Weights, caches and norm weights one step reads (activations aside)."""

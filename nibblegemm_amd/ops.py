@@ -290,7 +290,7 @@ def _fusable(X: torch.Tensor, qw: QuantizedWeight) -> bool:
 
 
 def _fused(X: torch.Tensor, qw: QuantizedWeight, epilogue: int, bias: Optional[torch.Tensor],
-           n_out: int) -> torch.Tensor:
+           n_out: int, norm: Optional[Tuple[torch.Tensor, float]] = None) -> torch.Tensor:
     ext = _bind()
     Wq, S = qw.qweight, qw.scales
     _check_matmul_inputs(X, Wq, S)
@@ -302,7 +302,9 @@ def _fused(X: torch.Tensor, qw: QuantizedWeight, epilogue: int, bias: Optional[t
     ws, ws_bytes = _fused_workspace(ext, dev, stream, M, K, N, qw.group_size)
     rc = ext.matmul_fused(X.data_ptr(), M, K, Wq.data_ptr(), Wq.shape[0], N, S.data_ptr(),
                           S.shape[0], S.shape[1], qw.group_size, epilogue,
-                          bias.data_ptr() if bias is not None else None, Y.data_ptr(),
+                          bias.data_ptr() if bias is not None else None,
+                          norm[0].data_ptr() if norm is not None else None,
+                          float(norm[1]) if norm is not None else 0.0, Y.data_ptr(),
                           ws.data_ptr() if ws is not None else None, ws_bytes, stream)
     if rc:
         _raise(rc, ext)
@@ -340,6 +342,44 @@ def matmul_swiglu(X: torch.Tensor, qw: QuantizedWeight) -> torch.Tensor:
         return _fused(X, qw, 2, None, qw.N // 2)
     gate, up = split_swiglu(matmul(X, qw))
     return torch.nn.functional.silu(gate) * up
+
+
+NORM_FUSED_MAX_M = 8
+NORM_FUSED_MAX_K = 16384
+
+
+def rmsnorm_matmul(X: torch.Tensor, norm_weight: torch.Tensor, qw: QuantizedWeight,
+                   eps: float = 1e-5, *, bias: Optional[torch.Tensor] = None,
+                   swiglu: bool = False) -> torch.Tensor:
+    """``matmul(rmsnorm(X, norm_weight, eps), qw)``, optionally through the
+    bias or SwiGLU epilogue (:func:`matmul_bias`, :func:`matmul_swiglu`).
+
+    For M <= 8 and K <= 16384 (the normalised rows fitting 64 KiB) this is one
+    launch: the streaming kernel normalises the rows itself, with the
+    RMSNorm kernel's arithmetic, so the result has the bits of the two-step
+    composition, which runs otherwise."""
+    _check_2d(X, qw)
+    if bias is not None and swiglu:
+        raise ValueError("bias and swiglu epilogues are exclusive")
+    if swiglu and qw.N % (2 * SWIGLU_BLOCK):
+        raise ValueError(f"N={qw.N} is not an interleaved gate|up weight (multiple of 64)")
+    M, K = X.shape
+    mt = 1 if M <= 1 else 2 if M <= 2 else 4 if M <= 4 else 8
+    if (_fusable(X, qw) and M <= NORM_FUSED_MAX_M and K <= NORM_FUSED_MAX_K and mt * K * 2 <= 65536
+            and norm_weight.dtype == torch.float16 and norm_weight.is_contiguous()
+            and norm_weight.device == X.device and norm_weight.numel() == K
+            and norm_weight.data_ptr() % 16 == 0 and X.dtype == torch.float16
+            and (bias is None or (bias.dtype == torch.float16 and bias.dim() == 1
+                                  and bias.numel() == qw.N and bias.is_contiguous()
+                                  and bias.device == X.device))):
+        if swiglu:
+            return _fused(X, qw, 2, None, qw.N // 2, (norm_weight, eps))
+        return _fused(X, qw, 1 if bias is not None else 0, bias, qw.N, (norm_weight, eps))
+    from .glue import rmsnorm  # noqa: PLC0415  (glue imports this module)
+    a = rmsnorm(X, norm_weight, eps)
+    if swiglu:
+        return matmul_swiglu(a, qw)
+    return matmul_bias(a, qw, bias) if bias is not None else matmul(a, qw)
 
 
 class QuantLinear(torch.nn.Module):

@@ -246,12 +246,13 @@ def test_extension_exposes_the_reference_module_functions():
         ext.dequant_w4(qw.qweight, qw.scales, 128)
 
 
-def fused(ext, M, K, N, g=128, epilogue=1, bias=P, wq_rows=None, s_rows=None, s_cols=None, ptr=P):
+def fused(ext, M, K, N, g=128, epilogue=1, bias=P, wq_rows=None, s_rows=None, s_cols=None, ptr=P,
+          norm=None, eps=1e-5):
     wq_rows = K // 8 if wq_rows is None else wq_rows
     s_rows = K // g if s_rows is None else s_rows
     s_cols = N if s_cols is None else s_cols
-    return ext.matmul_fused(ptr, M, K, ptr, wq_rows, N, ptr, s_rows, s_cols, g, epilogue, bias, ptr,
-                            None, 0, None)
+    return ext.matmul_fused(ptr, M, K, ptr, wq_rows, N, ptr, s_rows, s_cols, g, epilogue, bias, norm,
+                            eps, ptr, None, 0, None)
 
 
 @pytest.mark.parametrize("kwargs,needle", [
@@ -264,6 +265,11 @@ def fused(ext, M, K, N, g=128, epilogue=1, bias=P, wq_rows=None, s_rows=None, s_
     (dict(M=4, K=256, N=128, s_cols=132), "scale columns"),
     (dict(M=4, K=0, N=128), "K and N must be positive"),
     (dict(M=4, K=256, N=128, ptr=P + 8), "aligned"),
+    (dict(M=9, K=256, N=128, norm=P), "fused RMSNorm supports M <= 8"),
+    (dict(M=1, K=16384 + 128, N=128, norm=P), "K <= 16384"),
+    (dict(M=8, K=8192, N=128, norm=P), "above 64 KiB"),
+    (dict(M=1, K=256, N=128, norm=P + 8), "norm weight must be 16-byte aligned"),
+    (dict(M=1, K=256, N=128, norm=P, eps=-1.0), "norm eps"),
 ])
 def test_fused_rejections(kwargs, needle):
     ext = ng.extension()

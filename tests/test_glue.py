@@ -284,9 +284,57 @@ def test_glue_step_matches_fp32(n_layers, pos):
     layers = [D.fuse(layer, swiglu=True) for layer in D.build_layers(n_layers, seed=11)]
     step = D.GlueDecodeStep(layers, pos=pos, max_seq=pos + 8)
     y = step()  # writes cache row pos only; the reference reads rows < pos
-    assert step.launches == 7 * n_layers
+    assert step.launches == 5 * n_layers
     ref = ref_step(step, layers)
     assert err_rms(y, ref) <= 1e-2, err_rms(y, ref)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,K,N", [(1, 4096, 6144), (1, 4096, 4096), (2, 16384, 512),
+                                   (3, 1024, 1024), (8, 4096, 2048), (1, 128, 64)])
+@pytest.mark.parametrize("epi", ["none", "bias", "swiglu"])
+def test_rmsnorm_matmul_fused_is_the_two_step_bits(M, K, N, epi):
+    """The streaming kernel's RMSNorm prologue reproduces the RMSNorm
+    kernel's row scale and rounding, so the fused launch gives exactly the
+    bits of rmsnorm followed by the matmul (and its epilogue)."""
+    from nibblegemm_amd import ops
+    g = torch.Generator().manual_seed(M * 131 + K + N)
+    qw = ng.quantize((torch.randn((K, N), generator=g) * 0.02), 128).to(dev)
+    x = (torch.randn((M, K), generator=g) * 2).half().to(dev)
+    w = (1 + 0.1 * torch.randn(K, generator=g)).half().to(dev)
+    bias = torch.randn(N, generator=g).half().to(dev) if epi == "bias" else None
+    fused = ops.rmsnorm_matmul(x, w, qw, 1e-5, bias=bias, swiglu=epi == "swiglu")
+    a = glue.rmsnorm(x, w, 1e-5)
+    if epi == "swiglu":
+        ref = ops.matmul_swiglu(a, qw)
+    elif epi == "bias":
+        ref = ops.matmul_bias(a, qw, bias)
+    else:
+        ref = ops.matmul(a, qw)
+    assert torch.equal(fused, ref)
+    W = ng.dequant(qw).float()
+    if epi == "none":
+        assert err_rms(fused, (a.float() @ W).half()) <= 1e-2
+
+
+@pytest.mark.gpu
+def test_rmsnorm_matmul_beyond_the_fused_limits_composes():
+    from nibblegemm_amd import ops
+    g = torch.Generator().manual_seed(4)
+    qw = ng.quantize(torch.randn((1024, 256), generator=g) * 0.02, 128).to(dev)
+    x = torch.randn((12, 1024), generator=g).half().to(dev)  # M > 8: two launches
+    w = (1 + 0.1 * torch.randn(1024, generator=g)).half().to(dev)
+    assert torch.equal(ops.rmsnorm_matmul(x, w, qw), ops.matmul(glue.rmsnorm(x, w), qw))
+
+
+@pytest.mark.gpu
+def test_glue_step_fused_norms_are_the_separate_launches():
+    from nibblegemm_amd import decode_step as D
+    layers = [D.fuse(layer, swiglu=True) for layer in D.build_layers(2, seed=13)]
+    fused = D.GlueDecodeStep(layers, pos=150, fuse_norm=True)
+    plain = D.GlueDecodeStep(layers, pos=150, fuse_norm=False)
+    assert fused.launches == 10 and plain.launches == 14
+    assert torch.equal(fused(), plain())
 
 
 @pytest.mark.gpu
