@@ -257,7 +257,12 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs a) {
     }
   };
 
+  Stage s0, s1;
+  int g = gb + wave;
   if constexpr (NORM) {
+    // The first group's weights do not depend on the activations: their
+    // loads go out before the prologue, which their latency then covers.
+    if (g < ge) load(s0, g, true);
     // Rows of this block, normalised into LDS.  Thread t holds chunks
     // (256 c + t) * 8 of a row (K <= 16384: at most 8), x and the weight
     // loaded before the reduction, as in the RMSNorm kernel.
@@ -289,10 +294,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs a) {
   // flight while the current one is computed.  The scheduling barriers keep
   // the compiler from sinking the prefetch below the compute it is meant to
   // overlap.
-  Stage s0, s1;
-  int g = gb + wave;
   if (g < ge) {
-    load(s0, g, true);
+    if constexpr (!NORM) load(s0, g, true);
     while (true) {
       const int g1 = g + WAVES;
       load(s1, g1, g1 < ge);

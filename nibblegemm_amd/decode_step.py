@@ -214,19 +214,28 @@ def measure(layers: List[Dict[str, QuantizedWeight]], trials: int = 10, warmup: 
     }
 
 
-def run(n_layers: int = 32, group_size: int = 128, trials: int = 10, glue_pos: int = 1023) -> dict:
+VARIANTS = ("projections", "fused", "fused_swiglu", "glue")
+
+
+def run(n_layers: int = 32, group_size: int = 128, trials: int = 10, glue_pos: int = 1023,
+        variants=VARIANTS) -> dict:
     layers = build_layers(n_layers, group_size=group_size)
     nbytes = weight_bytes(layers)
     res = {"config": f"Llama-3-8B shapes, {n_layers} distinct layers, g={group_size}, M=1",
            "roofline_tok_s": round(H.HBM_PEAK_GBPS * 1e9 / nbytes, 1)}
-    res["projections"] = measure(layers, trials)
-    fused = [fuse(layer) for layer in layers]
-    res["fused"] = measure(fused, trials)
-    del fused
-    swiglu = [fuse(layer, swiglu=True) for layer in layers]
-    res["fused_swiglu"] = measure(swiglu, trials)
-    if glue_pos >= 0:
-        res["glue"] = measure_glue(swiglu, glue_pos, trials)
+    if "projections" in variants:
+        res["projections"] = measure(layers, trials)
+    if "fused" in variants:
+        fused = [fuse(layer) for layer in layers]
+        res["fused"] = measure(fused, trials)
+        del fused
+    if "fused_swiglu" in variants or "glue" in variants:
+        swiglu = [fuse(layer, swiglu=True) for layer in layers]
+        del layers
+        if "fused_swiglu" in variants:
+            res["fused_swiglu"] = measure(swiglu, trials)
+        if "glue" in variants and glue_pos >= 0:
+            res["glue"] = measure_glue(swiglu, glue_pos, trials)
     return res
 
 
@@ -237,11 +246,17 @@ def main(argv=None) -> int:
     ap.add_argument("--trials", type=int, default=10)
     ap.add_argument("--glue-pos", type=int, default=1023,
                     help="position of the full-step (glue) variant's token; -1 skips it")
+    ap.add_argument("--variants", default=",".join(VARIANTS),
+                    help="comma-separated subset of " + ", ".join(VARIANTS))
     args = ap.parse_args(argv)
+    variants = tuple(v for v in args.variants.split(",") if v)
+    if not set(variants) <= set(VARIANTS):
+        ap.error(f"unknown variant in {args.variants!r}")
     if not torch.cuda.is_available():
         print("decode_step needs a GPU", file=sys.stderr)
         return 1
-    print(json.dumps(run(args.layers, args.group_size, args.trials, args.glue_pos)), flush=True)
+    print(json.dumps(run(args.layers, args.group_size, args.trials, args.glue_pos, variants)),
+          flush=True)
     return 0
 
 
