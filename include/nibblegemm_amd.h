@@ -50,7 +50,7 @@
 extern "C" {
 #endif
 
-#define NIBBLE_ABI_VERSION 5
+#define NIBBLE_ABI_VERSION 6
 
 #if defined(__GNUC__) || defined(__clang__)
 #define NIBBLE_API __attribute__((visibility("default")))
@@ -216,6 +216,21 @@ NIBBLE_API size_t nibble_attention_decode_workspace_bytes(int64_t n_heads, int64
 NIBBLE_API size_t nibble_attention_decode_counter_bytes(int64_t n_heads, int64_t n_kv_heads,
                                                         int64_t head_dim, int64_t max_seq,
                                                         int64_t pos, void* stream);
+
+/*
+ * GPTQ's column loop over one quantisation group (replaces the per-channel
+ * PyTorch loop of gptq_quantize, python/nibblegemm/gptq.py:103-122).
+ * W: fp32 rows of the group's G input channels for N output rows (row n at
+ * W + n * ldw; the [out, in] orientation GPTQ works in).  U: the group's
+ * G x G block of the upper Cholesky factor of H^-1 (row stride ldu).
+ * Writes, per row n: Q[n * ldq + i] = q + 8 (uint8, 0..15), E[n * G + i] =
+ * the compensation residual err_i, and scales[n] (fp32).  W and U are only
+ * read.  G must be 64 or 128.  Arithmetic as the reference's ops, each
+ * rounded on its own; see nibblegemm_amd/csrc/gptq.hip.
+ */
+NIBBLE_API int nibble_gptq_group_f32(const void* W, int64_t ldw, int64_t N, int64_t G,
+                                     const void* U, int64_t ldu, void* Q, int64_t ldq, void* E,
+                                     void* scales, void* stream);
 
 #ifdef __cplusplus
 }

@@ -12,7 +12,7 @@ of this package.  Symmetric GPTQ / AWQ 4-bit checkpoints are ingested by
 :mod:`nibblegemm_amd.convert`.
 """
 
-from . import convert
+from . import convert, gptq
 from .ops import (DECODE_MAX_M, QuantLinear, dequant, extension, gemm, gemv, matmul, matmul_bias,
                   matmul_swiglu, rmsnorm_matmul)
 from .quant import (
@@ -33,6 +33,7 @@ __all__ = [
     "QuantizedWeight",
     "concat_columns",
     "convert",
+    "gptq",
     "dequant",
     "dequantize",
     "extension",

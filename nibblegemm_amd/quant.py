@@ -114,14 +114,22 @@ def quantize_device(W: torch.Tensor, group_size: int = 128) -> QuantizedWeight:
     # from the true division the host path performs.
     scale = (amax / torch.full_like(amax, float(QMAX))).clamp(min=1e-8)
     q = torch.round(groups / scale.unsqueeze(1)).clamp(QMIN, QMAX)
-    qu = (q + ZERO_POINT).to(torch.int64).reshape(K // PACK_FACTOR, PACK_FACTOR, N)
-    packed = torch.zeros((K // PACK_FACTOR, N), dtype=torch.int64, device=W.device)
+    packed = pack_nibbles_device((q + ZERO_POINT).reshape(K, N))
+    return QuantizedWeight(packed, scale.to(torch.float16).contiguous(), group_size, K, N)
+
+
+def pack_nibbles_device(qu: torch.Tensor) -> torch.Tensor:
+    """:func:`pack_nibbles` on a torch tensor, on its device: [K, N] values in
+    [0, 15] (any integer or float dtype holding integers) -> int32 [K/8, N]."""
+    K, N = qu.shape
+    if K % PACK_FACTOR:
+        raise ValueError(f"K={K} must be divisible by {PACK_FACTOR}")
+    q = qu.to(torch.int64).reshape(K // PACK_FACTOR, PACK_FACTOR, N)
+    packed = torch.zeros((K // PACK_FACTOR, N), dtype=torch.int64, device=qu.device)
     for k_off in range(PACK_FACTOR):
-        packed |= qu[:, k_off, :] << (4 * int(SLOT_FOR_K[k_off]))
+        packed |= q[:, k_off, :] << (4 * int(SLOT_FOR_K[k_off]))
     # Words with the top bit set are the negative int32 of the same bit pattern.
-    packed = torch.where(packed >= 1 << 31, packed - (1 << 32), packed).to(torch.int32)
-    return QuantizedWeight(packed.contiguous(), scale.to(torch.float16).contiguous(),
-                           group_size, K, N)
+    return torch.where(packed >= 1 << 31, packed - (1 << 32), packed).to(torch.int32).contiguous()
 
 
 def concat_columns(*qws: QuantizedWeight) -> QuantizedWeight:
