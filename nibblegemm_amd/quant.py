@@ -59,15 +59,47 @@ class QuantizedWeight:
         return self.qweight.numel() * 4 + self.scales.numel() * 2
 
 
+# Clipping ratios the scale search tries, largest first (reference quant.py:57).
+CLIP_RATIOS = torch.linspace(1.0, 0.55, 19)
+
+
+def _search_scale(groups: torch.Tensor, n_chunk: int = 4096) -> torch.Tensor:
+    """Per-group scale minimising the group's squared quantisation error over
+    the clipping ratios ``CLIP_RATIOS`` (reference quant.py:81-124): for each
+    ratio r, ``scale = max(amax * r / 7, 1e-8)``, the group rounded with it,
+    and the sum of squared errors; a later ratio replaces the best so far only
+    when strictly better.  The reference keeps it as a documented negative
+    result (lower weight error, worse model quality); it is off by default.
+
+    groups: float32 ``[K/G, G, N]`` -> scales ``[K/G, N]``, on groups' device,
+    processed ``n_chunk`` columns at a time."""
+    n_groups, _, N = groups.shape
+    out = torch.empty((n_groups, N), dtype=groups.dtype, device=groups.device)
+    ratios = CLIP_RATIOS.to(groups.device, groups.dtype)
+    for c0 in range(0, N, n_chunk):
+        blk = groups[:, :, c0:c0 + n_chunk]
+        amax = blk.abs().amax(dim=1)
+        best = (amax / QMAX).clamp(min=1e-8)
+        best_err = torch.full_like(amax, float("inf"))
+        for r in ratios:
+            s = (amax * r / QMAX).clamp(min=1e-8)
+            q = torch.round(blk / s.unsqueeze(1)).clamp(QMIN, QMAX)
+            err = (q * s.unsqueeze(1) - blk).pow(2).sum(dim=1)
+            take = err < best_err
+            best_err = torch.where(take, err, best_err)
+            best = torch.where(take, s, best)
+        out[:, c0:c0 + n_chunk] = best
+    return out
+
+
 def quantize(W: torch.Tensor, group_size: int = 128, clip_search: bool = False) -> QuantizedWeight:
     """Round-to-nearest quantise a ``[K, N]`` weight to packed group-wise INT4.
 
-    Reference quant.py:127-161.  ``clip_search`` (the reference's MSE clipping
-    search, off by default there and documented as lowering model quality) is
-    not provided; asking for it raises ``NotImplementedError``.
+    Reference quant.py:127-161.  ``clip_search`` picks each group's scale by
+    :func:`_search_scale` instead of max-abs (off by default, as in the
+    reference, which documents it as lowering model quality).  The work runs
+    on W's device; the result is on the host.
     """
-    if clip_search:
-        raise NotImplementedError("clip_search is not provided by nibblegemm_amd")
     if W.ndim != 2:
         raise ValueError(f"expected a 2-D weight, got shape {tuple(W.shape)}")
     K, N = W.shape
@@ -78,8 +110,11 @@ def quantize(W: torch.Tensor, group_size: int = 128, clip_search: bool = False) 
 
     w = W.detach().float()
     groups = w.reshape(K // group_size, group_size, N)
-    # Clamp away exact zeros so all-zero groups stay finite.
-    scale = (groups.abs().amax(dim=1) / QMAX).clamp(min=1e-8)
+    if clip_search:
+        scale = _search_scale(groups)
+    else:
+        # Clamp away exact zeros so all-zero groups stay finite.
+        scale = (groups.abs().amax(dim=1) / QMAX).clamp(min=1e-8)
     q = torch.round(groups / scale.unsqueeze(1)).clamp(QMIN, QMAX)
     qu = (q + ZERO_POINT).reshape(K, N).to(torch.uint8).cpu().numpy()
 

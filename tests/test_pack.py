@@ -9,7 +9,8 @@ import pytest
 import torch
 
 import nibblegemm_amd as ng
-from nibblegemm_amd.quant import PACK_FACTOR, SLOT_FOR_K
+from nibblegemm_amd import quant
+from nibblegemm_amd.quant import PACK_FACTOR, SLOT_FOR_K, dequantize, quantize
 
 EXPECTED_SLOT_FOR_K = [0, 4, 1, 5, 2, 6, 3, 7]
 
@@ -101,3 +102,60 @@ def test_interleave_swiglu_column_order():
     assert torch.equal(qw.qweight[:, 64:96], gq[:, 32:]) and torch.equal(qw.scales[:, 96:], us[:, 32:])
     g_back, u_back = split_swiglu(qw.qweight)
     assert torch.equal(g_back, gq) and torch.equal(u_back, uq)
+
+
+# ---------------------------------------------------------------------------
+# quantize(clip_search=True): the reference's MSE scale search (quant.py:81-124)
+# ---------------------------------------------------------------------------
+def _clip_case(K=256, N=96, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    W = torch.randn(K, N, generator=g) * 0.02
+    W[torch.rand(K, N, generator=g) < 0.01] *= 8  # outliers: clipping pays for some groups
+    return W
+
+
+def _group_sse(W, scales, G):
+    """Squared quantisation error per (group, column) in float64."""
+    K, N = W.shape
+    g = W.double().reshape(K // G, G, N)
+    s = scales.double().unsqueeze(1)
+    q = torch.round(g / s).clamp(-8, 7)
+    return (q * s - g).pow(2).sum(dim=1)
+
+
+def test_clip_search_scale_is_a_candidate_and_never_worse():
+    """The chosen scale is one of the 19 clipped max-abs scales, and its
+    squared error is no larger than max-abs's (ratio 1 is the first candidate
+    and is replaced only by a strictly better one)."""
+    W, G = _clip_case(), 128
+    groups = W.float().reshape(-1, G, W.shape[1])
+    chosen = quant._search_scale(groups)
+    amax = groups.abs().amax(dim=1)
+    cands = torch.stack([(amax * r / 7).clamp(min=1e-8) for r in quant.CLIP_RATIOS])
+    assert bool((cands == chosen.unsqueeze(0)).any(dim=0).all())
+    plain = (amax / 7).clamp(min=1e-8)
+    assert bool((_group_sse(W, chosen, G) <= _group_sse(W, plain, G) * (1 + 1e-6)).all())
+    assert bool((chosen < plain).any())  # the outliers make clipping win somewhere
+
+
+def test_clip_search_picks_the_minimum_error_ratio():
+    """Brute force in float64 over the same candidates agrees with the search
+    (float32 sums may order near-equal candidates differently: allow a few)."""
+    W, G = _clip_case(seed=1), 64
+    groups = W.float().reshape(-1, G, W.shape[1])
+    chosen = quant._search_scale(groups)
+    amax = groups.abs().amax(dim=1)
+    cands = torch.stack([(amax * r / 7).clamp(min=1e-8) for r in quant.CLIP_RATIOS])
+    sse = torch.stack([_group_sse(W, c, G) for c in cands])
+    best = cands.gather(0, sse.argmin(dim=0, keepdim=True))[0]
+    assert (best != chosen).float().mean().item() < 0.02
+
+
+def test_quantize_with_clip_search_uses_the_searched_scales():
+    W, G = _clip_case(seed=2), 128
+    qw = quantize(W, G, clip_search=True)
+    scales = quant._search_scale(W.float().reshape(-1, G, W.shape[1]))
+    assert torch.equal(qw.scales, scales.half())
+    deq = dequantize(qw).float()
+    rtn = dequantize(quantize(W, G)).float()
+    assert (deq - W).pow(2).mean() < (rtn - W).pow(2).mean()
