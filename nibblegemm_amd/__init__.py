@@ -13,6 +13,7 @@ of this package.  Symmetric GPTQ / AWQ 4-bit checkpoints are ingested by
 """
 
 from . import convert, gptq
+from .gptq import HessianAccumulator, find_decoder_blocks, gptq_quantize, quantize_model_gptq
 from .ops import (DECODE_MAX_M, QuantLinear, dequant, extension, gemm, gemv, matmul, matmul_bias,
                   matmul_swiglu, rmsnorm_matmul)
 from .quant import (
@@ -29,14 +30,17 @@ from .quant import (
 
 __all__ = [
     "DECODE_MAX_M",
+    "HessianAccumulator",
     "QuantLinear",
     "QuantizedWeight",
     "concat_columns",
     "convert",
     "gptq",
+    "gptq_quantize",
     "dequant",
     "dequantize",
     "extension",
+    "find_decoder_blocks",
     "gemm",
     "gemv",
     "interleave_swiglu",
@@ -46,6 +50,7 @@ __all__ = [
     "pack_nibbles",
     "quantize",
     "quantize_device",
+    "quantize_model_gptq",
     "reference_matmul",
     "rmsnorm_matmul",
     "unpack_nibbles",

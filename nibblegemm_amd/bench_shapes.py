@@ -1,11 +1,13 @@
 """Shape sweeps of the W4A16 kernels against their baselines on one GPU (the
-roles of the reference's bench/bench_decode.py, bench/bench_prefill.py and
-bench/autotune.py, for the BASELINE configs).
+roles of the reference's bench/bench_decode.py, bench/bench_prefill.py,
+bench/launch_overhead.py and bench/autotune.py, for the BASELINE configs).
 
     python3 -m nibblegemm_amd.bench_shapes decode      # configs 1-3: M <= 8 GEMV
     python3 -m nibblegemm_amd.bench_shapes prefill     # configs 3-4: M = 16 .. 2048
     python3 -m nibblegemm_amd.bench_shapes dequant     # standalone dequant
     python3 -m nibblegemm_amd.bench_shapes crossover   # gemv vs gemm over M
+    python3 -m nibblegemm_amd.bench_shapes launch      # eager vs graph-replayed matmul
+    python3 -m nibblegemm_amd.bench_shapes autotune    # gemv splits x block_threads
 
 Every timing is a HIP-graph replay of many calls; a kernel and its hipBLASLt
 baseline are timed with interleaved trials (the same clock state for both).  Each call streams its
@@ -158,9 +160,68 @@ def crossover(args, rows):
         _emit(rows, row)
 
 
+LAUNCH_SHAPES = [(4096, 4096), (4096, 14336), (14336, 4096), (8192, 8192)]
+
+
+def launch(args, rows):
+    """What launching costs: the same ``matmul`` calls eager and replayed from
+    a HIP graph (reference bench/launch_overhead.py:32-58); the difference is
+    per-call host work, which a captured decode step does not pay."""
+    for K, N in LAUNCH_SHAPES:
+        qws, gen = _weights(K, N, args.group_size, seed=K + N)
+        for M in args.M or [1]:
+            X = torch.randn((M, K), generator=gen).to(torch.float16).cuda()
+            _check(ops.matmul(X, qws[0]), X, qws[0], f"matmul {M}x{K}x{N}")
+            e = H.bench(lambda i: ops.matmul(X, qws[i]), reps=64, trials=args.trials)
+            g = H.bench_graph(lambda i: ops.matmul(X, qws[i]), reps=64, trials=args.trials)
+            nb = H.total_bytes(M, K, N, args.group_size, 4)
+            _emit(rows, {"bench": "launch", "M": M, "K": K, "N": N,
+                         "eager_us": round(e.median_ms * 1e3, 2),
+                         "graph_us": round(g.median_ms * 1e3, 2),
+                         "launch_us": round((e.median_ms - g.median_ms) * 1e3, 2),
+                         "eager_GB/s": round(H.achieved_gbps(nb, e.median_ms)),
+                         "graph_GB/s": round(H.achieved_gbps(nb, g.median_ms))})
+        del qws
+        torch.cuda.empty_cache()
+
+
+def autotune(args, rows):
+    """The GEMV's launch geometry swept over K splits x workgroup size, each
+    point checked first, against the built-in plan (reference
+    bench/autotune.py:30-72).  ``vs_plan`` > 1 means the point beats the plan."""
+    for K, N in LAUNCH_SHAPES + [(4096, 1024)]:
+        qws, gen = _weights(K, N, args.group_size, seed=K + N)
+        groups = K // args.group_size
+        for M in args.M or [1]:
+            X = torch.randn((M, K), generator=gen).to(torch.float16).cuda()
+            plan = H.bench_graph(lambda i: ops.gemv(X, qws[i]), reps=32, trials=args.trials)
+            for threads in (64, 128, 256, 512, 1024):
+                for splits in (1, 2, 4, 8, 16):
+                    if splits > groups:
+                        continue
+                    try:
+                        y = ops.gemv(X, qws[0], 4, splits, threads)
+                    except RuntimeError:  # geometry the kernel does not take at this M
+                        continue
+                    err = _check(y, X, qws[0], f"gemv {M}x{K}x{N} s={splits} t={threads}")
+                    t = H.bench_graph(lambda i: ops.gemv(X, qws[i], 4, splits, threads),
+                                      reps=32, trials=args.trials)
+                    nb = H.total_bytes(M, K, N, args.group_size, 4)
+                    _emit(rows, {"bench": "autotune", "M": M, "K": K, "N": N,
+                                 "threads": threads, "splits": splits,
+                                 "us": round(t.median_ms * 1e3, 2),
+                                 "GB/s": round(H.achieved_gbps(nb, t.median_ms)),
+                                 "plan_us": round(plan.median_ms * 1e3, 2),
+                                 "vs_plan": round(plan.median_ms / t.median_ms, 2),
+                                 "max_err_rms": float(f"{err:.2e}")})
+        del qws
+        torch.cuda.empty_cache()
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
-    ap.add_argument("what", choices=["decode", "prefill", "dequant", "crossover"])
+    ap.add_argument("what", choices=["decode", "prefill", "dequant", "crossover", "launch",
+                                     "autotune"])
     ap.add_argument("--M", type=int, nargs="*", help="batch sizes (default: the BASELINE configs)")
     ap.add_argument("--group-size", type=int, default=128)
     ap.add_argument("--trials", type=int, default=10)
@@ -173,8 +234,8 @@ def main(argv=None) -> int:
     torch.backends.cuda.matmul.allow_tf32 = False
     print(f"# {H.device_summary()}", file=sys.stderr, flush=True)
     rows = []
-    {"decode": decode, "prefill": prefill, "dequant": dequant, "crossover": crossover}[args.what](
-        args, rows)
+    {"decode": decode, "prefill": prefill, "dequant": dequant, "crossover": crossover,
+     "launch": launch, "autotune": autotune}[args.what](args, rows)
     if args.markdown and rows:
         cols = [k for k in rows[0] if k != "bench"]
         print(H.markdown_table(rows, cols), file=sys.stderr)
