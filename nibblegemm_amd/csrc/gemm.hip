@@ -605,6 +605,186 @@ hipError_t launch_pc64(const TileArgs& a, int64_t G, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// Large-tile form for big batches: 256 x 256 output tiles, four waves (one
+// per SIMD), each wave a (BM/2) x (BN/2) block of 32 x 32 MFMA tiles held in
+// registers (256 accumulators per lane).  Every wave loads, decodes, stores
+// and multiplies, like the tile kernel, but an operand read from LDS now
+// feeds four MFMAs instead of two, halving the LDS traffic per FLOP of the
+// 128 x 128 producer/consumer kernel.  64-k steps, LDS double buffered
+// (2 x 64 KiB), global loads two steps ahead in registers, one barrier per
+// step.  The template also builds 256 x 128 and 128 x 256 tiles; measured on
+// MI355X they lost to the 128 x 128 producer/consumer kernel wherever they
+// were the largest tile to fill the chip (14336 x 4096, M = 2048: 267 and
+// 250 us against 242 us), so the planner does not use them.
+//
+// Loads per thread and step: BM / 32 16-byte A chunks (rows tid / 8 + 32 it,
+// unit tid % 8) and BN / 128 dwordx4 of packed B (columns 4 q .. 4 q + 3,
+// q = tid % (BN / 4), packed rows tid / (BN / 4) apart by 256 / (BN / 4))
+// with their four scales.
+template <int BM, int BN, int GROUP>
+__global__ __launch_bounds__(kGemmThreads) void gemm_big_kernel(TileArgs args) {
+  constexpr int PBK = 64;
+  constexpr int TM = BM / 64, TN = BN / 64;                   // 32 x 32 tiles per wave
+  constexpr int A_IT = BM * (PBK / 8) / kGemmThreads;          // 16-byte A chunks per thread
+  constexpr int QUADS = BN / 4;                                // column quads per packed row
+  constexpr int B_IT = (PBK / 8) * QUADS / kGemmThreads;       // packed quads per thread
+  constexpr int PR_STEP = kGemmThreads / QUADS;                // packed rows apart
+  static_assert(GROUP % PBK == 0, "one scale per column per step");
+  static_assert(B_IT >= 1 && A_IT >= 1, "tile too small for the loaders");
+  __shared__ __attribute__((aligned(16))) _Float16 As[2][BM * PBK];
+  __shared__ __attribute__((aligned(16))) _Float16 Bs[2][BN * PBK];
+  __shared__ int s_last;
+  const int M = args.M, K = args.K, N = args.N;
+  const int tid = static_cast<int>(threadIdx.x);
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int m0 = blockIdx.y * BM;
+  const int n0 = blockIdx.x * BN;
+  const int step0 = blockIdx.z * args.steps_per_split;
+  const int ntiles = min(args.steps_per_split, K / PBK - step0);
+  const int wm = (wave >> 1) * (BM / 2);
+  const int wn = (wave & 1) * (BN / 2);
+  const int r32 = lane & 31;
+
+  struct Stage {
+    h8_t a[A_IT];
+    u4_t b[B_IT];
+    h4_t s;
+  };
+  const uint32_t row_bytes = static_cast<uint32_t>(N) * 4u;
+  const __amdgpu_buffer_rsrc_t rx =
+      make_rsrc(args.X, static_cast<uint32_t>(M) * static_cast<uint32_t>(K) * 2u);
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(args.Wq, static_cast<uint32_t>(K / 8) * row_bytes);
+  const __amdgpu_buffer_rsrc_t rsc =
+      make_rsrc(args.S, static_cast<uint32_t>(K / GROUP) * static_cast<uint32_t>(N) * 2u);
+  uint32_t voff_a[A_IT];
+  int a_st[A_IT];
+#pragma unroll
+  for (int it = 0; it < A_IT; ++it) {
+    const int row = (tid >> 3) + 32 * it;
+    const int gm = m0 + row;
+    voff_a[it] = gm < M ? (static_cast<uint32_t>(gm) * K + (tid & 7) * 8) * 2u : kOutOfRange;
+    a_st[it] = lds_unit64(row, tid & 7) * 8;
+  }
+  const int quad = tid % QUADS;
+  const int b_col = n0 + 4 * quad;
+  const bool b_ok = b_col < N;  // N % 4 == 0: the quad is wholly inside or outside
+  uint32_t voff_b[B_IT];
+  int b_st[B_IT][4];
+#pragma unroll
+  for (int it = 0; it < B_IT; ++it) {
+    const int pr = tid / QUADS + PR_STEP * it;
+    voff_b[it] = b_ok ? pr * row_bytes + static_cast<uint32_t>(b_col) * 4u : kOutOfRange;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) b_st[it][j] = lds_unit64(4 * quad + j, pr) * 8;
+  }
+  const uint32_t voff_s = b_ok ? static_cast<uint32_t>(b_col) * 2u : kOutOfRange;
+
+  auto load_step = [&](Stage& st, int step) {
+    const uint32_t k0 = static_cast<uint32_t>((step0 + min(step, ntiles - 1)) * PBK);
+#pragma unroll
+    for (int it = 0; it < A_IT; ++it)
+      st.a[it] = __builtin_bit_cast(
+          h8_t, __builtin_amdgcn_raw_buffer_load_b128(rx, voff_a[it], k0 * 2u, 0));
+#pragma unroll
+    for (int it = 0; it < B_IT; ++it)
+      st.b[it] = __builtin_bit_cast(
+          u4_t, __builtin_amdgcn_raw_buffer_load_b128(rw, voff_b[it], (k0 / 8) * row_bytes, 0));
+    st.s = __builtin_bit_cast(
+        h4_t, __builtin_amdgcn_raw_buffer_load_b64(
+                  rsc, voff_s, (k0 / GROUP) * static_cast<uint32_t>(N) * 2u, 0));
+  };
+  auto store_step = [&](const Stage& st, int buf) {
+#pragma unroll
+    for (int it = 0; it < A_IT; ++it) *reinterpret_cast<h8_t*>(&As[buf][a_st[it]]) = st.a[it];
+#pragma unroll
+    for (int it = 0; it < B_IT; ++it)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        h2_t w[4];
+        const h2_t s2 = {st.s[j], st.s[j]};
+        decode8_scaled(st.b[it][j], s2, w);
+        const h8_t v = {w[0][0], w[0][1], w[1][0], w[1][1], w[2][0], w[2][1], w[3][0], w[3][1]};
+        *reinterpret_cast<h8_t*>(&Bs[buf][b_st[it][j]]) = v;
+      }
+  };
+
+  f16_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  int rda[TM][PBK / 16], rdb[TN][PBK / 16];
+#pragma unroll
+  for (int ks = 0; ks < PBK / 16; ++ks) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i) rda[i][ks] = lds_unit64(wm + 32 * i + r32, 2 * ks + (lane >> 5)) * 8;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) rdb[j][ks] = lds_unit64(wn + 32 * j + r32, 2 * ks + (lane >> 5)) * 8;
+  }
+  auto compute_step = [&](int buf) {
+    h8_t a[2][TM], b[2][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) a[0][i] = *reinterpret_cast<const h8_t*>(&As[buf][rda[i][0]]);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) b[0][j] = *reinterpret_cast<const h8_t*>(&Bs[buf][rdb[j][0]]);
+#pragma unroll
+    for (int ks = 0; ks < PBK / 16; ++ks) {
+      const int cur = ks & 1;
+      if (ks + 1 < PBK / 16) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+          a[cur ^ 1][i] = *reinterpret_cast<const h8_t*>(&As[buf][rda[i][ks + 1]]);
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          b[cur ^ 1][j] = *reinterpret_cast<const h8_t*>(&Bs[buf][rdb[j][ks + 1]]);
+      }
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma32(a[cur][i], b[cur][j], acc[i][j]);
+    }
+  };
+
+  Stage R0, R1;
+  load_step(R0, 0);
+  load_step(R1, 1);
+  store_step(R0, 0);
+  load_step(R0, 2);
+  __syncthreads();
+  int t = 0;
+  for (; t + 2 <= ntiles; t += 2) {
+    compute_step(0);
+    store_step(R1, 1);
+    load_step(R1, t + 3);
+    __syncthreads();
+    compute_step(1);
+    store_step(R0, 0);
+    load_step(R0, t + 4);
+    __syncthreads();
+  }
+  if (t < ntiles) {
+    compute_step(0);
+    __syncthreads();
+  }
+  pc_epilogue<TM, TN>(acc, args, false, m0 + wm, n0 + wn, s_last);
+}
+
+template <int BM, int BN>
+hipError_t launch_big(const TileArgs& a, int64_t G, hipStream_t stream) {
+  if (a.splits != 1) return hipErrorInvalidValue;  // the kernel sums all of K
+  dim3 grid(static_cast<unsigned>(ceil_div(a.N, BN)), static_cast<unsigned>(ceil_div(a.M, BM)),
+            static_cast<unsigned>(a.splits));
+  if (G == 128)
+    gemm_big_kernel<BM, BN, 128><<<grid, kGemmThreads, 0, stream>>>(a);
+  else
+    gemm_big_kernel<BM, BN, 64><<<grid, kGemmThreads, 0, stream>>>(a);
+  return hipGetLastError();
+}
+
 
 template <int BM, int BN>
 hipError_t launch_tile(const TileArgs& a, int64_t G, hipStream_t stream) {
@@ -619,15 +799,19 @@ hipError_t launch_tile(const TileArgs& a, int64_t G, hipStream_t stream) {
 
 struct TileChoice {
   int bm, bn;
-  bool pc = false;  // the producer/consumer kernel (BN = 128, 64-k steps)
+  bool pc = false;   // the producer/consumer kernel (BN = 128, 64-k steps)
+  bool big = false;  // the 256 x 256 large-tile kernel (64-k steps)
 };
+
+// Batches from this many rows up may run the large-tile kernel (version 6).
+constexpr int64_t kBigMinM = 1024;
 
 // The widest B vector aligned operands of this N allow (the plan the
 // workspace query assumes).
 int nominal_bn_max(int64_t N) { return N % 4 == 0 ? 256 : N % 2 == 0 ? 128 : 64; }
 
 // k per pipeline step of the kernel a choice runs.
-int step_k(TileChoice t) { return t.pc ? 64 : BK; }
+int step_k(TileChoice t) { return t.pc || t.big ? 64 : BK; }
 
 // Widest B vector (BN / 64 packed words per thread) the operands allow.
 int max_bn(int64_t N, const void* w, const void* s) {
@@ -640,13 +824,14 @@ int max_bn(int64_t N, const void* w, const void* s) {
 // count keeps the workspace query pure host code and equal to the launch.
 constexpr int kPlanCUs = 256;
 
-// Tile choice, measured on MI355X over M = 64..2048 at 4096 x 14336 and
+// Tile choice of the tile kernel (the shapes the producer/consumer kernel
+// does not take), measured on MI355X over M = 64..2048 at 4096 x 14336 and
 // 14336 x 4096: 128 x 128 (2 waves per SIMD, so one workgroup's barrier
 // wait overlaps another's MFMAs) is fastest whenever its grid gives every CU
 // a workgroup; otherwise 64 x 128, whose doubled grid wins (e.g. 126 us vs
-// 165 us at M = 512, 14336 x 4096).  256-wide tiles, one workgroup per CU,
-// were slower at every shape.  Narrower B vectors serve N not a multiple of
-// 2 or operands without 8-byte alignment.
+// 165 us at M = 512, 14336 x 4096).  256-wide tiles of this kernel, one
+// workgroup per CU, were slower at every shape.  Narrower B vectors serve N
+// not a multiple of 2 or operands without 8-byte alignment.
 TileChoice choose_tile(int64_t M, int64_t N, int bn_max) {
   const int bn = std::min(128, bn_max);
   if (ceil_div(M, 128) * ceil_div(N, bn) >= kPlanCUs) return {128, bn};
@@ -671,7 +856,19 @@ TilePlan plan_tile(int64_t M, int64_t K, int64_t N, int64_t version, int bn_max)
   TilePlan p;
   int64_t tiles = 0;
   int splits = 1;
-  if (K % 64 == 0 && bn_max >= 256) {
+  // 256 x 256 tiles when their last wave over the CUs is at least 7/8 full;
+  // never split over K.  Measured on MI355X against the 128 x 128
+  // producer/consumer kernel: 4096 x 14336 at M = 1024 (224 tiles) 131 vs
+  // 137 us, M = 2048 / 3072 / 4096 (448 / 672 / 896) 244 / 357 / 472 vs
+  // 247 / 372 / 483 us; 14336 x 4096 at M = 4096 (256) 423 vs 472 us; but at
+  // M = 3072 (192 tiles, a quarter of the CUs idle) 365 vs 359 us.
+  const int64_t t256 = ceil_div(M, 256) * ceil_div(N, 256);
+  const bool big = version == 6 && M >= kBigMinM && K % 64 == 0 && bn_max >= 256 &&
+                   8 * t256 >= 7 * ceil_div(t256, kPlanCUs) * kPlanCUs;
+  if (big) {
+    p.t = TileChoice{256, 256, false, true};
+    tiles = t256;
+  } else if (K % 64 == 0 && bn_max >= 256) {
     // The producer/consumer kernel wherever it applies (whole 64-k steps,
     // 16-byte packed-word loads).  Measured on MI355X over M = 160..2048 at
     // 4096 x 14336 and 14336 x 4096: 128-row tiles win once the launch has
@@ -701,6 +898,9 @@ TilePlan plan_tile(int64_t M, int64_t K, int64_t N, int64_t version, int bn_max)
 }
 
 hipError_t launch_choice(TileChoice t, const TileArgs& a, int64_t G, hipStream_t stream) {
+  if (t.big) {
+    return launch_big<256, 256>(a, G, stream);
+  }
   if (t.pc) return t.bm == 128 ? launch_pc64<128>(a, G, stream) : launch_pc64<64>(a, G, stream);
   if (t.bm == 128 && t.bn == 128) return launch_tile<128, 128>(a, G, stream);
   if (t.bm == 64 && t.bn == 128) return launch_tile<64, 128>(a, G, stream);
@@ -839,7 +1039,8 @@ extern "C" int nibble_gemm_w4a16(const void* X, int64_t x_rows, int64_t x_cols, 
   // another kernel than that plan's, the call runs without a split, as do
   // row-blocked tall launches.
   const TilePlan nominal = plan_tile(M, K, N, version, nominal_bn_max(N));
-  if (M > rows_max || p.t.pc != nominal.t.pc || p.t.bm != nominal.t.bm || p.t.bn != nominal.t.bn)
+  if (M > rows_max || p.t.pc != nominal.t.pc || p.t.big != nominal.t.big ||
+      p.t.bm != nominal.t.bm || p.t.bn != nominal.t.bn)
     p.splits = 1;
   if (p.splits > 1) {
     if (workspace == nullptr || workspace_bytes < p.workspace_bytes)
