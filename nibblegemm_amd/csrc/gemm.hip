@@ -856,15 +856,17 @@ TilePlan plan_tile(int64_t M, int64_t K, int64_t N, int64_t version, int bn_max)
   TilePlan p;
   int64_t tiles = 0;
   int splits = 1;
-  // 256 x 256 tiles when their last wave over the CUs is at least 7/8 full;
-  // never split over K.  Measured on MI355X against the 128 x 128
-  // producer/consumer kernel: 4096 x 14336 at M = 1024 (224 tiles) 131 vs
-  // 137 us, M = 2048 / 3072 / 4096 (448 / 672 / 896) 244 / 357 / 472 vs
-  // 247 / 372 / 483 us; 14336 x 4096 at M = 4096 (256) 423 vs 472 us; but at
-  // M = 3072 (192 tiles, a quarter of the CUs idle) 365 vs 359 us.
+  // 256 x 256 tiles when the grid is one round over the CUs, at least 7/8
+  // full; never split over K.  Measured on MI355X against the 128 x 128
+  // producer/consumer kernel, graph replays interleaved with each other and
+  // with hipBLASLt: 1024 x 4096 x 14336 (224 tiles) 128 vs 133 us,
+  // 4096 x 14336 x 4096 (256 tiles) 414 vs 464 us.  Grids of several rounds
+  // (one workgroup per CU: nothing overlaps a tile's prologue and epilogue
+  // with another's MFMAs) lost under that load: 2048 and 4096 x 4096 x 14336
+  // (448 and 896 tiles) 254 vs 242 and 495 vs 474 us.
   const int64_t t256 = ceil_div(M, 256) * ceil_div(N, 256);
   const bool big = version == 6 && M >= kBigMinM && K % 64 == 0 && bn_max >= 256 &&
-                   8 * t256 >= 7 * ceil_div(t256, kPlanCUs) * kPlanCUs;
+                   8 * t256 >= 7 * kPlanCUs && t256 <= kPlanCUs;
   if (big) {
     p.t = TileChoice{256, 256, false, true};
     tiles = t256;

@@ -169,14 +169,15 @@ def test_producer_consumer_kernel_edges(M, K_, N, g):
 
 
 @pytest.mark.parametrize("M,K_,N,g", [(1024, 256, 14336, 128), (4096, 512, 4096, 64),
-                                      (1900, 384, 14208, 128), (3072, 256, 4096, 128),
-                                      (1024, 320, 14336, 64)])
+                                      (1100, 384, 12000, 128), (2048, 256, 14336, 128),
+                                      (1024, 320, 14336, 64), (4000, 256, 4000, 64)])
 def test_large_tile_kernel(M, K_, N, g):
-    """Version 6 runs 256 x 256 tiles from M = 1024 where their grid fills the
-    CUs: 224 tiles at 1024 x 14336, 256 at 4096 x 4096, and row and column
-    tails at 1900 x 14208 (448 tiles); 3072 x 4096 (192 tiles) keeps the
-    128 x 128 kernel.  Both kernels sum each output over k in the same
-    order, so version 6 and version 7 (128 x 128) agree to the bit."""
+    """Version 6 runs 256 x 256 tiles from M = 1024 when the grid is one round
+    over the CUs, at least 7/8 full: 224 tiles at 1024 x 14336, 256 at
+    4096 x 4096, and with row and column tails 235 at 1100 x 12000 and 256
+    at 4000 x 4000; 2048 x 14336 (448 tiles) keeps the 128 x 128 kernel.
+    Both kernels sum each output over k in the same order, so version 6 and
+    version 7 (128 x 128) agree to the bit."""
     X, packed, scales, Xd, qw = synthetic(M, K_, N, g, seed=M + K_ + N)
     y6 = ng.gemm(Xd, qw, version=6)
     y7 = ng.gemm(Xd, qw, version=7)
