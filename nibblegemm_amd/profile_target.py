@@ -6,6 +6,7 @@ holds only that kernel (plus setup copies).
     python3 -m nibblegemm_amd.profile_target gemv --K 4096 --N 14336 --M 1 --calls 50
     python3 -m nibblegemm_amd.profile_target dequant --K 4096 --N 14336 --calls 20
     python3 -m nibblegemm_amd.profile_target gemm --M 2048 --K 4096 --N 14336 --calls 10
+    python3 -m nibblegemm_amd.profile_target gemm --M 4096 --K 14336 --N 4096 --version 7
     python3 -m nibblegemm_amd.profile_target copy --mib 256 --calls 20
 
 ``copy`` is the calibration kernel for the HBM byte counters: a device copy
@@ -45,6 +46,7 @@ def main(argv=None) -> int:
     ap.add_argument("--G", type=int, default=128)
     ap.add_argument("--calls", type=int, default=50)
     ap.add_argument("--mib", type=int, default=256)
+    ap.add_argument("--version", type=int, default=6, choices=[6, 7], help="gemm version")
     args = ap.parse_args(argv)
     if not torch.cuda.is_available():
         print("profile_target needs a GPU", file=sys.stderr)
@@ -62,7 +64,7 @@ def main(argv=None) -> int:
         qws, gen = _weights(args.K, args.N, args.G, dev)
         X = torch.randn((args.M, args.K), generator=gen).to(torch.float16).to(dev)
         fn = {"gemv": lambda i: ops.gemv(X, qws[i]),
-              "gemm": lambda i: ops.gemm(X, qws[i]),
+              "gemm": lambda i: ops.gemm(X, qws[i], version=args.version),
               "dequant": lambda i: ops.dequant(qws[i])}[args.kernel]
         torch.cuda.synchronize()
         for i in range(args.calls):
