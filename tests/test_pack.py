@@ -20,6 +20,14 @@ def test_slot_table_is_the_documented_permutation():
     assert list(ng.quant.K_FOR_SLOT) == [0, 2, 4, 6, 1, 3, 5, 7]
 
 
+def test_slot_table_matches_the_cuda_scalar_decode():
+    """The reference's scalar decode computes the slot instead of looking it
+    up (csrc/dequant.cuh:96: odd k in the high half of the word); the formula
+    gives the documented table."""
+    slot = [(4 + (k >> 1)) if (k & 1) else (k >> 1) for k in range(PACK_FACTOR)]
+    assert slot == EXPECTED_SLOT_FOR_K
+
+
 def test_nibble_slot_assignment_is_pinned():
     qu = np.arange(PACK_FACTOR, dtype=np.uint8).reshape(PACK_FACTOR, 1)
     word = int(ng.pack_nibbles(qu).view(np.uint32)[0, 0])
