@@ -861,9 +861,10 @@ TilePlan plan_tile(int64_t M, int64_t K, int64_t N, int64_t version, int bn_max)
   // producer/consumer kernel, graph replays interleaved with each other and
   // with hipBLASLt: 1024 x 4096 x 14336 (224 tiles) 128 vs 133 us,
   // 4096 x 14336 x 4096 (256 tiles) 414 vs 464 us.  Grids of several rounds
-  // (one workgroup per CU: nothing overlaps a tile's prologue and epilogue
-  // with another's MFMAs) lost under that load: 2048 and 4096 x 4096 x 14336
-  // (448 and 896 tiles) 254 vs 242 and 495 vs 474 us.
+  // lost under that load: 2048 and 4096 x 4096 x 14336 (448 and 896 tiles,
+  // 1.75 and 3.5 rounds) 254 vs 242 and 495 vs 474 us.  Their last round is
+  // part-empty, and with one workgroup per CU no other workgroup's MFMAs
+  // overlap a tile's prologue and epilogue.
   const int64_t t256 = ceil_div(M, 256) * ceil_div(N, 256);
   const bool big = version == 6 && M >= kBigMinM && K % 64 == 0 && bn_max >= 256 &&
                    8 * t256 >= 7 * kPlanCUs && t256 <= kPlanCUs;
