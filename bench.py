@@ -77,9 +77,9 @@ def main() -> int:
     ap.add_argument("--skip-extras", action="store_true",
                     help="skip the copy-bandwidth, hipBLASLt and eager side measurements")
     ap.add_argument("--skip-decode-step", action="store_true",
-                    help="skip the 8B-shaped decode step (BASELINE config 5)")
+                    help="skip the Llama-3-8B-shaped decode step")
     ap.add_argument("--skip-prefill", action="store_true",
-                    help="skip the M=2048 prefill GEMM points (BASELINE config 4)")
+                    help="skip the M=2048 prefill GEMM points")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))

@@ -1,6 +1,6 @@
 """Shape sweeps of the W4A16 kernels against their baselines on one GPU (the
 roles of the reference's bench/bench_decode.py, bench/bench_prefill.py,
-bench/launch_overhead.py and bench/autotune.py, for the BASELINE configs).
+bench/launch_overhead.py and bench/autotune.py, at the benchmark shapes).
 
     python3 -m nibblegemm_amd.bench_shapes decode      # configs 1-3: M <= 8 GEMV
     python3 -m nibblegemm_amd.bench_shapes prefill     # configs 3-4: M = 16 .. 2048
@@ -12,7 +12,7 @@ bench/launch_overhead.py and bench/autotune.py, for the BASELINE configs).
 Every timing is a HIP-graph replay of many calls; a kernel and its hipBLASLt
 baseline are timed with interleaved trials (the same clock state for both).  Each call streams its
 weights from HBM: copies of the weights rotate through at least 1 GiB, more
-than the 256 MiB Infinity Cache.  Inputs follow BASELINE's synthetic
+than the 256 MiB Infinity Cache.  Inputs are synthetic, with the benchmark
 distributions: nibbles U{0..15}, scales U(0.002, 0.02), activations N(0, 1).
 Every measured configuration is first checked against a torch fp32
 reference, on the GPU, of the same weights (the bit-exact dequant kernel's
@@ -222,7 +222,7 @@ def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("what", choices=["decode", "prefill", "dequant", "crossover", "launch",
                                      "autotune"])
-    ap.add_argument("--M", type=int, nargs="*", help="batch sizes (default: the BASELINE configs)")
+    ap.add_argument("--M", type=int, nargs="*", help="batch sizes (default: the benchmark shapes)")
     ap.add_argument("--group-size", type=int, default=128)
     ap.add_argument("--trials", type=int, default=10)
     ap.add_argument("--markdown", action="store_true")

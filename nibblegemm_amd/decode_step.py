@@ -1,5 +1,5 @@
 """Llama-3-8B-shaped batch-1 decode step: every W4A16 projection of 32
-layers, replayed from a HIP graph (the reference's
+layers, replayed from a HIP graph (the decode-step benchmark; the reference's
 ``bench/bench_model.py`` layers mode, :43-125).
 
 Like the reference, a step is the projections only: q, k, v, o, gate, up and

@@ -253,7 +253,7 @@ def rms_err(y, ref) -> float:
 
 
 # --------------------------------------------------------------------------
-# seeded synthetic inputs (restating the BASELINE configs)
+# seeded synthetic inputs (the benchmark distributions)
 # --------------------------------------------------------------------------
 def synthetic_case(M: int, K: int, N: int, group_size: int = 128, seed: int = 0):
     """Nibbles U{0..15}, scales fp16(U(0.002, 0.02)), X fp16(N(0,1)).

@@ -11,7 +11,7 @@ import torch
 import nibblegemm_amd as ng
 import oracle as O
 
-#: The decode configs of BASELINE.json (configs 1-2): M = 1, g = 128.
+#: The decode benchmark shapes: M = 1, g = 128.
 DECODE_SHAPES = [(4096, 4096), (4096, 14336), (14336, 4096), (8192, 8192), (4096, 1024)]
 
 
@@ -24,7 +24,7 @@ def to_dev_qw(packed: np.ndarray, scales: np.ndarray, K: int, N: int, g: int,
 
 
 def synthetic(M: int, K: int, N: int, g: int = 128, seed: int = 0):
-    """BASELINE distributions: returns (X_np fp16, packed, scales fp16, X_dev, qw_dev)."""
+    """The benchmark distributions: returns (X_np fp16, packed, scales fp16, X_dev, qw_dev)."""
     X, packed, scales = O.synthetic_case(M, K, N, g, seed)
     Xd = torch.from_numpy(X.copy()).to("cuda")
     return X, packed, scales, Xd, to_dev_qw(packed, scales, K, N, g)

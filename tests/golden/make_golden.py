@@ -6,7 +6,7 @@ seeded inputs and the reference path's outputs -- dequantized weights
 (bit-exact) and fp32-accumulated matmul results -- so GPU tests can compare
 against stored data and CPU tests can detect any drift in the oracle.
 
-Inputs follow the BASELINE synthetic distributions: nibbles uniform in
+Inputs follow the benchmark's synthetic distributions: nibbles uniform in
 [0, 15], scales fp16(U(0.002, 0.02)), activations fp16(N(0, 1)); plus the
 reference's dequant sweep (tests/test_dequant.py:27-44 in arvindcr4/nibblegemm):
 every value in every slot on a 0xF background, all slots equal, random words.

@@ -138,7 +138,7 @@ def test_gemv_workspace_formula():
     # a single split needs no workspace
     assert ext.gemv_workspace_bytes(1, 1024, 256, 64, 4, 1, 0, None) == (0, 0)
     assert ext.gemv_workspace_bytes(1, 1024, 256, 64, 3, 0, 0, None) == (0, 0)
-    # default plan at the BASELINE decode shapes (pure host arithmetic):
+    # default plan at the benchmark decode shapes (pure host arithmetic):
     # one split up to 32 quant groups, then ~8 groups per wave of 4
     assert ext.gemv_workspace_bytes(1, 4096, 14336, 128, 4, 0, 0, None) == (0, 0)
     assert ext.gemv_workspace_bytes(1, 4096, 4096, 128, 4, 0, 0, None) == (0, 0)

@@ -127,7 +127,7 @@ def test_golden_sweep_vectors():
 
 
 def test_full_size_gate_up_bit_exact(oracle):
-    """The headline shape 4096 x 14336 at BASELINE's distributions."""
+    """The headline shape 4096 x 14336 at the benchmark distributions."""
     K, N, g = 4096, 14336, 128
     _, packed, scales = oracle.synthetic_case(1, K, N, g, seed=21)
     qw = to_dev_qw(packed, scales, K, N, g)

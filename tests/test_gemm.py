@@ -1,7 +1,7 @@
 """Parity of the MFMA prefill GEMM with the reference path.
 
 Edge cases follow the reference's tests/test_gemm.py (M on, just past and far
-past tile boundaries; N with masked columns), then the BASELINE prefill and
+past tile boundaries; N with masked columns), then the benchmark prefill and
 handover configs at full size -- checked on sampled rows, since the CPU oracle
 cannot do 2048 x 4096 x 14336 in seconds.
 
@@ -69,7 +69,8 @@ def test_versions_agree():
 
 @pytest.mark.parametrize("M", [16, 32])
 def test_small_batch_config_gemm_leg(M):
-    """BASELINE config 3 at M > 8 (the GEMM side of the handover), full size."""
+    """The small-batch config (M = 16, 32 at 4096 x 14336) above M = 8, the GEMM side
+    of the handover, at full size."""
     X, packed, scales, Xd, qw = synthetic(M, 4096, 14336, 128, seed=200 + M)
     y = host(ng.matmul(Xd, qw))
     assert rms_err(y, oracle_y(X, packed, scales, 4096, 128)) <= RMS_TOL
@@ -78,8 +79,9 @@ def test_small_batch_config_gemm_leg(M):
 @pytest.mark.parametrize("M", [128, 512, 2048])
 @pytest.mark.parametrize("K_,N", [(4096, 14336), (14336, 4096)])
 def test_prefill_configs_sampled_rows(M, K_, N):
-    """BASELINE config 4 at full size; the oracle checks 12 sampled rows
-    (first, last, both sides of every 128-row tile edge it hits, random)."""
+    """The prefill config (M = 128, 512, 2048 at 4096 x 14336 and 14336 x 4096)
+    at full size; the oracle checks 12 sampled rows (first, last, both sides
+    of every 128-row tile edge it hits, random)."""
     X, packed, scales, Xd, qw = synthetic(M, K_, N, 128, seed=300 + M + N)
     y = host(ng.gemm(Xd, qw))
     rng = np.random.default_rng(M)

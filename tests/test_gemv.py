@@ -56,7 +56,7 @@ def test_gemv_synthetic_distributions(M, K, N):
 
 @pytest.mark.parametrize("K,N", DECODE_SHAPES)
 def test_decode_configs_full_size(K, N):
-    """BASELINE configs 1-2 (M = 1, g = 128) at their real shapes."""
+    """The decode configs (M = 1, g = 128) at their real shapes."""
     X, packed, scales, Xd, qw = synthetic(1, K, N, 128, seed=K + N)
     y = host(ng.gemv(Xd, qw))
     ref = oracle_y(X, packed, scales, K, 128)
@@ -66,7 +66,7 @@ def test_decode_configs_full_size(K, N):
 
 @pytest.mark.parametrize("M", [2, 4, 8])
 def test_small_batch_config_gemv_leg(M):
-    """BASELINE config 3 at M <= 8 (the GEMV side of the handover)."""
+    """The small-batch config at M <= 8 (the GEMV side of the handover)."""
     X, packed, scales, Xd, qw = synthetic(M, 4096, 14336, 128, seed=100 + M)
     y = host(ng.matmul(Xd, qw))
     assert rms_err(y, oracle_y(X, packed, scales, 4096, 128)) <= RMS_TOL
