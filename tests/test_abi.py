@@ -293,3 +293,61 @@ def test_fused_workspace_matches_streaming_plan():
     assert ext.matmul_fused_workspace_bytes(1, 14336, 4096, 128, None) == \
         ext.gemv_workspace_bytes(1, 14336, 4096, 128, 4, 0, 0, None)
     assert ext.matmul_fused_workspace_bytes(129, 4096, 4096, 128, None) == (0, 0)
+
+
+def test_last_error_is_per_thread():
+    """nibble_last_error() is thread-local: a failure on one thread does not
+    overwrite the message another thread is about to read."""
+    import threading
+
+    ext = ng.extension()
+    first_failed, second_failed = threading.Event(), threading.Event()
+    seen = {}
+
+    def first():
+        assert gemv(ext, 1, 256, 128, version=9) == INVALID
+        first_failed.set()
+        second_failed.wait(10)
+        seen["first"] = ext.last_error()
+
+    def second():
+        first_failed.wait(10)
+        assert ext.dequant(P, 32, 128, P, 2, 128, 100, 1, P, None) == INVALID
+        seen["second"] = ext.last_error()
+        second_failed.set()
+
+    threads = [threading.Thread(target=first), threading.Thread(target=second)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(20)
+    assert "version" in seen["first"] and "group_size" not in seen["first"]
+    assert "group_size" in seen["second"]
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_workspace_plans_are_self_consistent(seed):
+    """Over random shapes: counters are 256-byte padded, a workspace exists
+    exactly when there are counters, and what follows the counters is whole
+    fp32 [splits, M, N] partials with 2 to 16 (streaming plans: gemv, and
+    gemm up to 128 rows) or 2 to 4 (tiled gemm) splits."""
+    import random
+
+    rng = random.Random(seed)
+    ext = ng.extension()
+    for _ in range(200):
+        g = rng.choice([64, 128])
+        K = g * rng.randint(1, 256)
+        N = 4 * rng.randint(1, 8192)
+        for M, kind in ((rng.randint(1, 8), "gemv"), (rng.randint(9, 4096), "gemm")):
+            if kind == "gemv":
+                ws, cb = ext.gemv_workspace_bytes(M, K, N, g, 4, 0, 0, None)
+                max_splits = 16
+            else:
+                ws, cb = ext.gemm_workspace_bytes(M, K, N, g, rng.choice([6, 7]), None)
+                max_splits = 16 if M <= 128 else 4  # M <= 128 streams, as gemv
+            assert cb % 256 == 0 and (ws == 0) == (cb == 0), (kind, M, K, N, g, ws, cb)
+            if ws:
+                body = ws - cb
+                assert body % (4 * M * N) == 0, (kind, M, K, N, g, ws, cb)
+                assert 2 <= body // (4 * M * N) <= max_splits, (kind, M, K, N, g, ws, cb)
