@@ -82,3 +82,45 @@ def test_dequant_random_shapes(K, N, g):
     for fast in (True, False):
         got = ng.dequant(qw, fast=fast).cpu().numpy()
         assert got.dtype == np.float16 and np.array_equal(got.view(np.uint16), expect.view(np.uint16))
+
+
+def _glue_cases(seed: int, n: int):
+    rng = random.Random(seed)
+    out = []
+    for _ in range(n):
+        n_kv = rng.choice([1, 2, 8])
+        n_heads = n_kv * rng.choice([1, 2, 4, 8])
+        max_seq = rng.randint(1, 3000)
+        out.append((n_heads, n_kv, rng.randrange(max_seq), max_seq))
+    return out
+
+
+@pytest.mark.parametrize("n_heads,n_kv,pos,max_seq", _glue_cases(505, 16))
+def test_attention_random_positions(n_heads, n_kv, pos, max_seq):
+    """Grouped-query attention at random positions, head ratios and cache
+    sizes (one chunk to two dozen), against the float32 reference, to one
+    fp16 rounding of the output; a repeat gives the same bits."""
+    from test_glue import _attn_case, err_rms, ref_attention, ulp_excess
+
+    from nibblegemm_amd import glue
+
+    qkv, kc, vc = _attn_case(n_heads, n_kv, pos, max_seq, seed=pos + 17 * n_heads + max_seq)
+    rope = glue.rope_tables(max_seq)
+    ref, _, _ = ref_attention(qkv, kc, vc, pos, n_heads, n_kv, rope)
+    a = glue.attention_decode(qkv, kc, vc, pos, rope)
+    assert err_rms(a, ref) <= 1e-2
+    assert ulp_excess(a, ref) <= 1.0, ulp_excess(a, ref)
+    assert torch.equal(glue.attention_decode(qkv, kc, vc, pos, rope), a)
+
+
+@pytest.mark.parametrize("M,K,N,g", [(m % 8 + 1, k, n, g) for m, k, n, g in _shapes(606, 16, 8, 4)])
+def test_rmsnorm_matmul_random_shapes(M, K, N, g):
+    """The RMSNorm prologue gives the bits of the RMSNorm launch followed by
+    the matmul, at random shapes (K a multiple of 8 up to 16384 columns)."""
+    from nibblegemm_amd import glue, ops
+
+    gen = torch.Generator().manual_seed(M + K + N)
+    qw = ng.quantize(torch.randn((K, N), generator=gen) * 0.02, g).to("cuda")
+    x = (torch.randn((M, K), generator=gen) * 2).half().to("cuda")
+    w = (1 + 0.1 * torch.randn(K, generator=gen)).half().to("cuda")
+    assert torch.equal(ops.rmsnorm_matmul(x, w, qw, 1e-5), ops.matmul(glue.rmsnorm(x, w, 1e-5), qw))
