@@ -61,13 +61,16 @@ struct GemvArgs {
   const _Float16* bias;   // [N] for kEpilogueBias
   const _Float16* norm_w; // [K]: the activations are RMSNorm(X) * norm_w (fused prologue), or null
   float norm_eps;
+  int strips;             // strip kernel: column strips of the launch
+  int strips_per_xcd;     // strip kernel: strips run by each XCD's workgroups
 };
 
 // Output epilogues of the streaming kernel (fused forms of what a caller
 // would otherwise run as separate elementwise kernels on the fp16 result).
 constexpr int kEpilogueNone = 0;
 constexpr int kEpilogueBias = 1;    // Y = fp16(fp16(X W) + bias)
-constexpr int kEpilogueSwiglu = 2;  // W = [gate | up] in 32-column blocks; Y = silu(G) * U
+constexpr int kEpilogueSwiglu = 2;  // W = [gate | up] in 16-column blocks; Y = silu(G) * U
+constexpr int kSwigluBlock = 16;    // columns of one gate or up block of that layout
 
 // The fp16 arithmetic of the unfused composition, step by step: the two
 // products rounded to fp16, silu(g) = g / (1 + e^-g) evaluated in fp32 and
@@ -85,26 +88,34 @@ __device__ __forceinline__ f4_t mfma16(h8_t a, h8_t b, f4_t c) {
 }
 
 // Writes a strip's outputs from `total(r, qq)`, the fp32 sums of column quad
-// qq of row r, through the launch's epilogue.
-template <int MT, int THREADS, typename Total>
+// qq of row r, through the launch's epilogue.  SW is the strip width in
+// columns; the SwiGLU epilogue needs strips of whole gate|up block pairs.
+template <int MT, int THREADS, int SW = kStripCols, typename Total>
 __device__ __forceinline__ void emit_outputs(const GemvArgs& a, int strip, int m_base, int mrows,
                                              Total total) {
-  if (a.epilogue == kEpilogueSwiglu) {
-    const int nout = a.N / 2;
-    for (int e = threadIdx.x; e < MT * 8; e += THREADS) {
-      const int r = e >> 3, qq = e & 7;
-      const int ocol = strip * (kStripCols / 2) + 4 * qq;
-      if (r >= mrows || ocol >= nout) continue;
-      const f4_t g = total(r, qq), u = total(r, qq + 8);
-      const h4_t y = {(_Float16)silu_mul(g[0], u[0]), (_Float16)silu_mul(g[1], u[1]),
-                      (_Float16)silu_mul(g[2], u[2]), (_Float16)silu_mul(g[3], u[3])};
-      *reinterpret_cast<h4_t*>(a.Y + static_cast<size_t>(m_base + r) * nout + ocol) = y;
+  constexpr int QUADS = SW / 4;
+  if constexpr (SW >= 2 * kSwigluBlock) {
+    if (a.epilogue == kEpilogueSwiglu) {
+      // The strip holds SW / 32 pairs of 16 gate columns and the matching 16
+      // up columns; output quad o reads gate quad 8 (o / 4) + o % 4 and the
+      // up quad 4 columns later.
+      const int nout = a.N / 2;
+      for (int e = threadIdx.x; e < MT * (QUADS / 2); e += THREADS) {
+        const int r = e / (QUADS / 2), o = e % (QUADS / 2);
+        const int gq = 8 * (o / 4) + o % 4;
+        const int ocol = strip * (SW / 2) + 4 * o;
+        if (r >= mrows || ocol >= nout) continue;
+        const f4_t g = total(r, gq), u = total(r, gq + 4);
+        const h4_t y = {(_Float16)silu_mul(g[0], u[0]), (_Float16)silu_mul(g[1], u[1]),
+                        (_Float16)silu_mul(g[2], u[2]), (_Float16)silu_mul(g[3], u[3])};
+        *reinterpret_cast<h4_t*>(a.Y + static_cast<size_t>(m_base + r) * nout + ocol) = y;
+      }
+      return;
     }
-    return;
   }
-  for (int e = threadIdx.x; e < MT * 16; e += THREADS) {
-    const int r = e >> 4, qq = e & 15;
-    const int ocol = strip * kStripCols + 4 * qq;
+  for (int e = threadIdx.x; e < MT * QUADS; e += THREADS) {
+    const int r = e / QUADS, qq = e % QUADS;
+    const int ocol = strip * SW + 4 * qq;
     if (r >= mrows || ocol >= a.N) continue;
     const f4_t sum = total(r, qq);
     h4_t y = {(_Float16)sum[0], (_Float16)sum[1], (_Float16)sum[2], (_Float16)sum[3]};
@@ -114,6 +125,50 @@ __device__ __forceinline__ void emit_outputs(const GemvArgs& a, int strip, int m
         y[c] = (_Float16)(static_cast<float>(y[c]) + static_cast<float>(a.bias[ocol + c]));
     }
     *reinterpret_cast<h4_t*>(a.Y + static_cast<size_t>(m_base + r) * a.N + ocol) = y;
+  }
+}
+
+// The fused-RMSNorm prologue: rows [m_base, m_base + mrows) of X, normalised
+// into `xnorm` ([rows][K] fp16 in LDS) as fp16(x * r * norm_w), with r
+// computed exactly as the RMSNorm kernel does -- the first 256 threads hold
+// chunks (256 c + t) * 8 of the row (K <= 16384: at most 8), x and the weight
+// loaded before the reduction, the squares reduced in the same fixed order --
+// so the fused launch has the two-step composition's bits.  Threads past the
+// first 256 only pass the same barriers.
+template <int THREADS>
+__device__ __forceinline__ void norm_rows_to_lds(const GemvArgs& a, int m_base, int mrows,
+                                                 _Float16* xnorm) {
+  static_assert(THREADS % kRmsThreads == 0, "the RMSNorm prologue runs on 256-thread multiples");
+  __shared__ float part[kRmsThreads / 64];
+  constexpr int kMaxChunks = kNormMaxK / (kRmsThreads * 8);
+  const int tid = threadIdx.x;
+  const bool active = THREADS == kRmsThreads || tid < kRmsThreads;
+  for (int r = 0; r < mrows; ++r) {
+    const _Float16* xr = a.X + static_cast<size_t>(m_base + r) * a.K;
+    h8_t v[kMaxChunks], w[kMaxChunks];
+    float ss = 0.0f;
+    if (active) {
+#pragma unroll
+      for (int c = 0; c < kMaxChunks; ++c) {
+        const int col = (c * kRmsThreads + tid) * 8;
+        v[c] = col < a.K ? *reinterpret_cast<const h8_t*>(xr + col) : h8_t{};
+        w[c] = col < a.K ? *reinterpret_cast<const h8_t*>(a.norm_w + col) : h8_t{};
+        ss = sumsq_chunk(v[c], ss);
+      }
+      ss = wave_sum(ss);
+      if ((tid & 63) == 0) part[tid >> 6] = ss;
+    }
+    __syncthreads();
+    const float total = ((part[0] + part[1]) + part[2]) + part[3];
+    if (active) {
+      const float rr = rms_scale(total, a.K, a.norm_eps);
+#pragma unroll
+      for (int c = 0; c < kMaxChunks; ++c) {
+        const int col = (c * kRmsThreads + tid) * 8;
+        if (col < a.K) *reinterpret_cast<h8_t*>(&xnorm[r * a.K + col]) = rms_apply(v[c], w[c], rr);
+      }
+    }
+    __syncthreads();  // before `part` is written again, and before the loop reads xnorm
   }
 }
 
@@ -263,31 +318,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs a) {
     // The first group's weights do not depend on the activations: their
     // loads go out before the prologue, which their latency then covers.
     if (g < ge) load(s0, g, true);
-    // Rows of this block, normalised into LDS.  Thread t holds chunks
-    // (256 c + t) * 8 of a row (K <= 16384: at most 8), x and the weight
-    // loaded before the reduction, as in the RMSNorm kernel.
-    __shared__ float part[kRmsThreads / 64];
-    constexpr int kMaxChunks = 8;
-    const int tid = threadIdx.x;
-    for (int r = 0; r < mrows; ++r) {
-      const _Float16* xr = a.X + static_cast<size_t>(m_base + r) * a.K;
-      h8_t v[kMaxChunks], w[kMaxChunks];
-      float ss = 0.0f;
-#pragma unroll
-      for (int c = 0; c < kMaxChunks; ++c) {
-        const int col = (c * kRmsThreads + tid) * 8;
-        v[c] = col < a.K ? *reinterpret_cast<const h8_t*>(xr + col) : h8_t{};
-        w[c] = col < a.K ? *reinterpret_cast<const h8_t*>(a.norm_w + col) : h8_t{};
-        ss = sumsq_chunk(v[c], ss);
-      }
-      const float rr = rms_scale(block256_sum(ss, part), a.K, a.norm_eps);
-#pragma unroll
-      for (int c = 0; c < kMaxChunks; ++c) {
-        const int col = (c * kRmsThreads + tid) * 8;
-        if (col < a.K) *reinterpret_cast<h8_t*>(&xnorm[r * a.K + col]) = rms_apply(v[c], w[c], rr);
-      }
-      __syncthreads();  // before `part` is written again, and before the loop reads xnorm
-    }
+    norm_rows_to_lds<THREADS>(a, m_base, mrows, xnorm);
   }
 
   // Groups gb + wave, gb + wave + WAVES, ... with the next group's loads in
@@ -383,6 +414,320 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs a) {
   emit_outputs<MT, THREADS>(a, strip, m_base, mrows, split_sum);
   if (threadIdx.x == 0)
     __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Column-strip decode kernel (M <= 8, one launch, no cross-workgroup
+// exchange).  A workgroup owns SW columns (16, 32 or 64) over the whole of K;
+// its WAVES waves take contiguous ranges of quant groups, and every wave
+// keeps the weight loads of DEPTH groups in flight (a register ring; ONEPASS
+// when no wave has more groups than that, so every load is issued before
+// the first wait).  Workgroups are numbered so that each XCD (workgroup id %
+// 8 on a multi-XCD part) runs a contiguous run of strips.
+//
+// MFMA mapping.  A wave load is one dwordx4 per lane: lane l reads columns
+// 4 c .. 4 c + 3 (c = l % LPR, LPR = SW / 4 lanes per packed row) of packed
+// row r = l / LPR, so one load covers RPL = 64 / LPR packed rows (8 RPL k).
+// In v_mfma_f32_16x16x32_f16 terms lane l supplies B column slot n = l % 16
+// and k block b = l / 16, i.e. column 4 (n % LPR) + j of packed row
+// P b + n / LPR, with P = RPL / 4 phases.  Column slots of different phases
+// read different packed rows, so the A operand is laid out block-diagonally:
+// A row m' = RPT p + mm (RPT = 16 / P rows per phase) holds activation row mm
+// at the packed rows of phase p, and only the C entries with m' / RPT ==
+// n / LPR are kept.  For SW = 64 (one phase) this is the plain mapping of
+// gemv_mfma_kernel.  Phase-major rows put activation row mm of every phase in
+// accumulator element mm % 4 of a lane, so at M = 1 each lane carries one
+// live element per column word and the per-group scaling touches only that.
+// A 16-row A tile holds RPT activation rows, so M <= 8 takes one tile for
+// SW >= 32 and two for SW = 16.  The per-lane decode, the pre-scaled
+// activations and the correction MFMA are those of gemv_mfma_kernel; waves
+// and phases are summed in LDS in a fixed order.
+//
+// STAGED: the activation rows ([MT][K] fp16) and the strip's scales
+// ([K / GROUP][SW] fp16) are copied into LDS once per workgroup by LDS-DMA
+// buffer loads issued ahead of the weights, and the MFMA operands are read
+// from there.  Per group a wave then issues only its weight loads: a
+// per-lane activation load would cost a whole 64-lane address-unit pass for
+// the few lanes that hold real rows at M <= 8, and a per-lane scale load the
+// same for 8-byte scale quads.  NORM (RMSNorm prologue) fills the activation
+// rows itself and implies STAGED.
+template <int MT, int GROUP, int SW, int WAVES, int DEPTH, bool NORM, bool ONEPASS, bool STAGED>
+__global__ __launch_bounds__(WAVES * 64) void gemv_strip_kernel(GemvArgs a) {
+  constexpr int LPR = SW / 4;            // lanes per packed row
+  constexpr int RPL = 64 / LPR;          // packed rows per wave load
+  constexpr int P = RPL / 4;             // phases
+  constexpr int KPL = 8 * RPL;           // k per wave load
+  constexpr int CPG = GROUP / KPL;       // wave loads per quant group
+  constexpr int RPT = 16 / P;            // activation rows per 16-row A tile
+  constexpr int TILES = (MT + RPT - 1) / RPT;
+  // Accumulator elements that can hold a real row: element i of row block q
+  // is A row 4 q + i, activation row (4 q + i) % RPT < MT.
+  constexpr int LANE_ROWS = MT < 4 ? MT : 4;
+  constexpr int THREADS = WAVES * 64;
+  static_assert(SW == 16 || SW == 32 || SW == 64, "strip width");
+  static_assert(CPG >= 1 && GROUP % KPL == 0, "a wave load must not straddle quant groups");
+  static_assert(!NORM || STAGED, "the RMSNorm prologue leaves the activations in LDS");
+  static_assert(DEPTH >= 2, "the ring prepares the next stage while computing this one");
+  constexpr int kWPolicy = 2;            // non-temporal: the launch reads each weight once
+  __shared__ __attribute__((aligned(16))) float red[WAVES][P][MT][SW];
+  // STAGED: [MT][K] activation rows, then [K / GROUP][SW] scales.
+  extern __shared__ __attribute__((aligned(16))) _Float16 xnorm[];
+
+  // The grid is rounded up to whole XCD runs; a workgroup past the last
+  // strip finds every column out of range (its loads read zeros, its stores
+  // are skipped).  It does not return early: that test would need the
+  // strip count before the operand pointers, two dependent kernel-argument
+  // fetches ahead of the first weight load instead of one.
+  // Unsigned index arithmetic throughout (divisions by powers of two become
+  // shifts); every kernel argument the weight loads need is read up front.
+  const uint32_t K = static_cast<uint32_t>(a.K), N = static_cast<uint32_t>(a.N);
+  const uint32_t strip = (blockIdx.x & 7u) * static_cast<uint32_t>(a.strips_per_xcd) + (blockIdx.x >> 3);
+  const uint32_t lane = threadIdx.x & 63u;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int mrows = min(MT, a.M);
+  const uint32_t total_groups = K / GROUP;
+
+  // B side: lane (c, r).
+  const uint32_t c = lane % LPR, r = lane / LPR;
+  const uint32_t col = strip * SW + 4 * c;
+  const bool col_ok = strip < static_cast<uint32_t>(a.strips) && col < N;
+  const uint32_t row_bytes = N * 4u;
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.Wq, (K / 8) * row_bytes);
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.X, static_cast<uint32_t>(a.M) * K * 2u);
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.S, total_groups * N * 2u);
+  const uint32_t voff_w = col_ok ? r * row_bytes + col * 4u : kOutOfRange;
+  const uint32_t voff_s = col_ok ? col * 2u : kOutOfRange;
+  // A side: lane (m', kb) holds row m' = RPT p + mm of each tile at k block
+  // kb, i.e. the 8 k of packed row P kb + p of a wave load.
+  const uint32_t mq = lane & 15u, kb = lane >> 4;
+  const uint32_t ph = mq / RPT, mm = mq % RPT;
+  const uint32_t kx_lane = (kb * P + ph) * 8u;
+  uint32_t voff_x[TILES];
+#pragma unroll
+  for (int t = 0; t < TILES; ++t) {
+    const uint32_t m = t * RPT + mm;
+    voff_x[t] = m < static_cast<uint32_t>(mrows) ? (m * K + kx_lane) * 2u : kOutOfRange;
+  }
+  _Float16* const s_lds = xnorm + MT * K;  // STAGED scales
+
+  // STAGED: LDS-DMA copies of the activation rows and the strip's scales,
+  // 16 bytes per lane, block i of a region landing at byte 1024 i; lanes
+  // past the end are masked off.
+  auto stage_to_lds = [&]() {
+    using lds_ptr = __attribute__((address_space(3))) void*;
+    if constexpr (!NORM) {
+      const uint32_t chunks = static_cast<uint32_t>(mrows) * K / 8;
+      for (uint32_t blk = wave; blk * 64 < chunks; blk += WAVES) {
+        const uint32_t ch = blk * 64 + lane;
+        if (ch < chunks)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr)(xnorm + blk * 512), 16, ch * 16u,
+                                                   0, 0, 0);
+      }
+    }
+    // Scales: row g of the strip is SW / 8 chunks of 8 columns.
+    constexpr uint32_t kRowChunks = SW / 8;
+    const uint32_t chunks = total_groups * kRowChunks;
+    for (uint32_t blk = wave; blk * 64 < chunks; blk += WAVES) {
+      const uint32_t ch = blk * 64 + lane;
+      const uint32_t g = ch / kRowChunks, part = ch % kRowChunks;
+      const uint32_t scol = strip * SW + 8 * part;
+      if (ch < chunks)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rs, (lds_ptr)(s_lds + blk * 512), 16,
+            strip < static_cast<uint32_t>(a.strips) && scol < N ? (g * N + scol) * 2u : kOutOfRange,
+            0, 0, 0);
+    }
+    // Rows past M read as zeros from LDS (no masking in the loop).
+    for (uint32_t e = threadIdx.x; e < static_cast<uint32_t>(MT - mrows) * K / 8; e += THREADS)
+      *reinterpret_cast<h8_t*>(xnorm + mrows * K + 8 * e) = h8_t{};
+  };
+
+  // This wave's quant groups [g0, g0 + n).
+  const int g0 = static_cast<int>((wave * total_groups) / WAVES);
+  const int n = static_cast<int>(((wave + 1) * total_groups) / WAVES) - g0;
+
+  struct Stage {
+    h8_t x[TILES][CPG];  // unstaged: loaded with the weights; staged: read from LDS by prep
+    u4_t w[CPG];
+    h4_t s;
+    f4_t corr[TILES];
+    int g;
+  };
+  // Loads of the wave's i-th group; past the range every lane takes the
+  // out-of-range offset (zeros, no memory access), so the load sequence is
+  // the same on every path and the compiler's wait counts stay exact.
+  auto load = [&](Stage& st, int i) {
+    const bool in = i < n;
+    const int g = in ? g0 + i : g0;
+    const uint32_t vw = in ? voff_w : kOutOfRange;
+    st.g = g;
+    if constexpr (!STAGED) {
+      const uint32_t kx = static_cast<uint32_t>(g) * GROUP * 2u;
+#pragma unroll
+      for (int t = 0; t < TILES; ++t)
+#pragma unroll
+        for (int cc = 0; cc < CPG; ++cc)
+          st.x[t][cc] = __builtin_bit_cast(
+              h8_t, __builtin_amdgcn_raw_buffer_load_b128(rx, in ? voff_x[t] : kOutOfRange,
+                                                          kx + cc * KPL * 2, 0));
+    }
+    const uint32_t kw = static_cast<uint32_t>(g) * (GROUP / 8) * row_bytes;
+#pragma unroll
+    for (int cc = 0; cc < CPG; ++cc)
+      st.w[cc] = __builtin_bit_cast(
+          u4_t, __builtin_amdgcn_raw_buffer_load_b128(rw, vw, kw + cc * RPL * row_bytes, kWPolicy));
+    if constexpr (!STAGED)
+      st.s = __builtin_bit_cast(
+          h4_t, __builtin_amdgcn_raw_buffer_load_b64(rs, in ? voff_s : kOutOfRange,
+                                                     static_cast<uint32_t>(g) * N * 2u, kWPolicy));
+  };
+
+  f4_t tot[TILES][4];
+#pragma unroll
+  for (int t = 0; t < TILES; ++t)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) tot[t][j] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+  const DecodeConsts dk = decode_consts();
+  const h8_t xscale = biased_x_scale();
+  const h8_t bcorr = biased_correction();
+  // The activations of a group (pre-scaled) and its correction term
+  // sum_k x~ * correction, which does not depend on the weights: staged
+  // launches compute it ahead of the weight MFMAs, off their dependency
+  // chain.
+  auto prep = [&](Stage& st) {
+#pragma unroll
+    for (int t = 0; t < TILES; ++t) {
+      f4_t corr = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int cc = 0; cc < CPG; ++cc) {
+        if constexpr (STAGED)
+          st.x[t][cc] = *reinterpret_cast<const h8_t*>(
+              &xnorm[(t * RPT + mm) * K + st.g * GROUP + cc * KPL + kx_lane]);
+        st.x[t][cc] = st.x[t][cc] * xscale;
+        corr = mfma16(st.x[t][cc], bcorr, corr);
+      }
+      st.corr[t] = corr;
+    }
+  };
+  auto compute = [&](const Stage& st) {
+    f4_t acc[TILES][4];
+#pragma unroll
+    for (int t = 0; t < TILES; ++t)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[t][j] = st.corr[t];
+#pragma unroll
+    for (int cc = 0; cc < CPG; ++cc)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const h8_t b = decode8_biased(st.w[cc][j], dk);
+#pragma unroll
+        for (int t = 0; t < TILES; ++t) acc[t][j] = mfma16(st.x[t][cc], b, acc[t][j]);
+      }
+    h4_t sc;
+    if constexpr (STAGED)
+      sc = *reinterpret_cast<const h4_t*>(&s_lds[st.g * SW + 4 * c]);
+    else
+      sc = st.s;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float sj = static_cast<float>(sc[j]);
+#pragma unroll
+      for (int t = 0; t < TILES; ++t)
+#pragma unroll
+        for (int i = 0; i < LANE_ROWS; ++i)
+          tot[t][j][i] = __builtin_fmaf(sj, acc[t][j][i], tot[t][j][i]);
+    }
+  };
+
+  // The prologue's loads are issued stage by stage, in the order the loop
+  // body issues them: with the scheduler free to interleave them, the wait
+  // counts at the loop head could not be matched across the back edge and
+  // the compiler drained every load there.
+  // The LDS-DMA copies go first: the barrier before the first compute then
+  // waits for them alone (wait counts are in issue order), not for every
+  // weight load in flight.
+  if constexpr (STAGED) {
+    stage_to_lds();
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  Stage st[DEPTH];
+#pragma unroll
+  for (int d = 0; d < DEPTH; ++d) {
+    load(st[d], d);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if constexpr (NORM) norm_rows_to_lds<THREADS>(a, 0, mrows, xnorm);
+  // Every wave's LDS-DMA copies have landed (each waits for its own, the
+  // barrier for the others').
+  if constexpr (STAGED && !NORM) __syncthreads();
+  if constexpr (ONEPASS) {
+    // Every group of the wave is already in flight (n <= DEPTH).
+    if constexpr (STAGED) {
+#pragma unroll
+      for (int d = 0; d < DEPTH; ++d)
+        if (d < n) prep(st[d]);
+    }
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (d < n) {
+        if constexpr (!STAGED) prep(st[d]);
+        compute(st[d]);
+      }
+    }
+  } else {
+    if constexpr (STAGED) prep(st[0]);
+    for (int i0 = 0; i0 < n; i0 += DEPTH) {
+#pragma unroll
+      for (int d = 0; d < DEPTH; ++d) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (i0 + d < n) {
+          if constexpr (STAGED) {
+            // the next group's activations and correction, then this group
+            if (i0 + d + 1 < n) prep(st[(d + 1) % DEPTH]);
+          } else {
+            prep(st[d]);
+          }
+          compute(st[d]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        load(st[d], i0 + d + DEPTH);
+      }
+    }
+  }
+
+  // Lane (n = lane % 16, row block lane / 16) holds C rows 4 (lane / 16) + i
+  // of each tile; it keeps the entries of its own phase.
+  const int nslot = lane & 15;
+  const int my_phase = nslot / LPR;
+  const int ccol = 4 * (nslot % LPR);
+#pragma unroll
+  for (int t = 0; t < TILES; ++t)
+#pragma unroll
+    for (int i = 0; i < LANE_ROWS; ++i) {
+      const int mp = 4 * (lane >> 4) + i;
+      const int m = t * RPT + mp % RPT;
+      if (mp / RPT == my_phase && m < MT) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) red[wave][my_phase][m][ccol + j] = tot[t][j][i];
+      }
+    }
+  __syncthreads();
+  auto strip_sum = [&](int row, int qq) {
+    f4_t sum = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w)
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+        const f4_t v = *reinterpret_cast<const f4_t*>(&red[w][p][row][4 * qq]);
+        sum[0] += v[0];
+        sum[1] += v[1];
+        sum[2] += v[2];
+        sum[3] += v[3];
+      }
+    return sum;
+  };
+  emit_outputs<MT, THREADS, SW>(a, strip, 0, mrows, strip_sum);
 }
 
 // Versions 0 and 1: one thread per (m, n), scalar decode, fp32 weights
@@ -487,17 +832,78 @@ hipError_t launch_group(const GemvArgs& a, const StreamPlan& p, hipStream_t stre
   }
 }
 
-}  // namespace
+// The strip kernel at one geometry.  The grid is rounded up to a whole
+// number of XCD runs (8 workgroups per strip-per-XCD).
+template <int MT, int GROUP, int SW, int WAVES, int DEPTH>
+hipError_t launch_strip_geometry(const GemvArgs& a, hipStream_t stream) {
+  if constexpr (SW == 16 && GROUP != 128) {
+    return hipErrorInvalidValue;  // a 16-column wave load spans 128 k
+  } else if constexpr (MT > 8) {
+    return hipErrorInvalidValue;
+  } else {
+    const dim3 grid(8 * a.strips_per_xcd);
+    // One pass when no wave has more groups than the ring holds; activations
+    // and scales staged in LDS when the rows fit 64 KiB (the RMSNorm prologue
+    // always stages, and is only planned when they fit).
+    const bool onepass = (a.K / GROUP + WAVES - 1) / WAVES <= DEPTH;
+    const size_t xbytes = static_cast<size_t>(MT) * a.K * sizeof(_Float16);
+    const size_t lds = xbytes + static_cast<size_t>(a.K / GROUP) * SW * sizeof(_Float16);
+    const bool staged = a.norm_w != nullptr || xbytes <= 65536;
+    if (a.norm_w != nullptr) {
+      if (onepass)
+        gemv_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, true, true, true><<<grid, WAVES * 64, lds, stream>>>(a);
+      else
+        gemv_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, true, false, true><<<grid, WAVES * 64, lds, stream>>>(a);
+    } else if (staged) {
+      if (onepass)
+        gemv_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, false, true, true><<<grid, WAVES * 64, lds, stream>>>(a);
+      else
+        gemv_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, false, false, true><<<grid, WAVES * 64, lds, stream>>>(a);
+    } else {
+      if (onepass)
+        gemv_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, false, true, false><<<grid, WAVES * 64, 0, stream>>>(a);
+      else
+        gemv_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, false, false, false><<<grid, WAVES * 64, 0, stream>>>(a);
+    }
+    return hipGetLastError();
+  }
+}
+
+// The strip geometries compiled into the library; plan_strip only picks
+// these.
+template <int MT, int GROUP>
+hipError_t launch_strip_mt(const GemvArgs& a, const StreamPlan& p, hipStream_t stream) {
+  const int key = p.strip_cols * 10000 + p.waves * 100 + p.depth;
+  switch (key) {
+    case 32 * 10000 + 8 * 100 + 2: return launch_strip_geometry<MT, GROUP, 32, 8, 2>(a, stream);
+    case 32 * 10000 + 16 * 100 + 2: return launch_strip_geometry<MT, GROUP, 32, 16, 2>(a, stream);
+    case 64 * 10000 + 4 * 100 + 2: return launch_strip_geometry<MT, GROUP, 64, 4, 2>(a, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <int GROUP>
+hipError_t launch_strip_group(const GemvArgs& a, const StreamPlan& p, hipStream_t stream) {
+  switch (p.mt) {
+    case 1: return launch_strip_mt<1, GROUP>(a, p, stream);
+    case 2: return launch_strip_mt<2, GROUP>(a, p, stream);
+    case 4: return launch_strip_mt<4, GROUP>(a, p, stream);
+    case 8: return launch_strip_mt<8, GROUP>(a, p, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
 
 // Split heuristic: whole K in one workgroup per 64-column strip unless a wave
 // would have to stream more than kGroupsPerWave groups, in which case K is
 // split evenly.  Overrides follow the reference: splits are floor-then-trimmed
 // (csrc/gemv_w4a16.cu:398-401).
-int plan_stream(int64_t M, int64_t K, int64_t N, int64_t G, bool split_k, int64_t splits_override,
-                int64_t threads_override, StreamPlan* p) {
+int plan_split_kernel(int64_t M, int64_t K, int64_t N, int64_t G, bool split_k,
+                      int64_t splits_override, int64_t threads_override, StreamPlan* p) {
   if (M < 1 || M > kStreamMaxM || K <= 0 || N <= 0 || (G != 64 && G != 128) || K % G != 0)
     return fail(NIBBLE_ERR_INVALID_ARGUMENT, "no streaming plan for M=%lld K=%lld N=%lld G=%lld",
                 (long long)M, (long long)K, (long long)N, (long long)G);
+  *p = StreamPlan();
+  p->kernel = kSplitKernel;
   p->mt = mt_for(std::min<int64_t>(M, 32));
   p->mblocks = static_cast<int>(ceil_div(M, p->mt));
   // A 32-thread block (accepted by the reference, csrc/gemv_w4a16.cu:384-385)
@@ -528,6 +934,58 @@ int plan_stream(int64_t M, int64_t K, int64_t N, int64_t G, bool split_k, int64_
     p->workspace_bytes = 0;
   }
   return NIBBLE_OK;
+}
+
+}  // namespace
+
+// The strip kernel serves M <= 8 up to K = 8192.  Its geometry depends on
+// (M, K, N) only -- never on the epilogue or the RMSNorm prologue -- so the
+// fused and unfused launches of one shape sum every output in the same order
+// and give the same bits.  Measured on MI355X (graph replay, weights streamed
+// from HBM, M = 1, against the split kernel's plan):
+//  * N >= 12288: 64-column strips, 4 waves -- 4096 x 14336 7.6 us (7.8;
+//    32-column strips 9.0), 4096 x 28672 13.3 us (14.0);
+//  * narrower: 32-column strips, 8 waves (16 at K = 8192) -- 4096 x 1024
+//    4.4 us (5.5), 4096 x 4096 4.7 (5.8), 4096 x 6144 5.5 (6.7), 8192 x 8192
+//    9.2 (9.4); 16-column strips were no faster and 64-column ones slower;
+//  * two groups of loads in flight per wave (deeper rings measured slower);
+//  * longer K keeps the split kernel: 14336 x 4096 9.5 us there, 10.0 us at
+//    the best strip geometry.
+constexpr int64_t kStripMaxK = 8192;
+constexpr int64_t kStripWideN = 12288;
+
+bool plan_strip(int64_t M, int64_t K, int64_t N, int64_t G, StreamFusion fusion, StreamPlan* p) {
+  (void)fusion;
+  if (M < 1 || M > 8 || K <= 0 || K > kStripMaxK || N <= 0 || (G != 64 && G != 128) ||
+      K % G != 0)
+    return false;
+  StreamPlan q;
+  q.kernel = kStripKernel;
+  q.mt = mt_for(M);
+  q.mblocks = 1;
+  q.splits = 1;
+  q.groups_per_split = static_cast<int>(K / G);
+  q.depth = 2;
+  if (N >= kStripWideN) {
+    q.strip_cols = 64;
+    q.waves = 4;
+  } else {
+    q.strip_cols = 32;
+    q.waves = K <= 4096 ? 8 : 16;
+  }
+  q.strips = static_cast<int>(ceil_div(N, q.strip_cols));
+  q.counter_bytes = 0;
+  q.workspace_bytes = 0;
+  *p = q;
+  return true;
+}
+
+int plan_stream(int64_t M, int64_t K, int64_t N, int64_t G, bool split_k, int64_t splits_override,
+                int64_t threads_override, StreamPlan* p, StreamFusion fusion) {
+  if (split_k && splits_override == 0 && threads_override == 0 &&
+      plan_strip(M, K, N, G, fusion, p))
+    return NIBBLE_OK;
+  return plan_split_kernel(M, K, N, G, split_k, splits_override, threads_override, p);
 }
 
 bool stream_supported(const void* X, const void* Wq, const void* S, const void* Y, int64_t M,
@@ -566,13 +1024,17 @@ int launch_stream(const void* X, const void* Wq, const void* S, void* Y, int64_t
   a.bias = static_cast<const _Float16*>(bias);
   a.norm_w = static_cast<const _Float16*>(norm_w);
   a.norm_eps = norm_eps;
-  hipError_t e = G == 128 ? launch_group<128>(a, p, stream) : launch_group<64>(a, p, stream);
+  hipError_t e;
+  if (p.kernel == kStripKernel) {
+    a.strips = p.strips;
+    a.strips_per_xcd = static_cast<int>(ceil_div(p.strips, 8));
+    e = G == 128 ? launch_strip_group<128>(a, p, stream) : launch_strip_group<64>(a, p, stream);
+  } else {
+    e = G == 128 ? launch_group<128>(a, p, stream) : launch_group<64>(a, p, stream);
+  }
   if (e != hipSuccess) return hip_fail(e, who);
   return NIBBLE_OK;
 }
-
-namespace {
-}  // namespace
 
 // Mirrors check_inputs (csrc/gemv_w4a16.cu:251-265) on shapes; pure host code.
 int validate_gemv(const void* X, int64_t x_rows, int64_t x_cols, const void* Wq, int64_t wq_rows,
@@ -750,8 +1212,8 @@ int validate_fused(const void* X, int64_t x_rows, int64_t x_cols, const void* Wq
   NIBBLE_CHECK(epilogue == kEpilogueNone || epilogue == kEpilogueBias ||
                    epilogue == kEpilogueSwiglu,
                "epilogue must be 0 (none), 1 (bias) or 2 (swiglu), got %lld", (long long)epilogue);
-  NIBBLE_CHECK(epilogue != kEpilogueSwiglu || N % kStripCols == 0,
-               "swiglu needs N (gate|up interleaved in 32-column blocks) to be a multiple of 64");
+  NIBBLE_CHECK(epilogue != kEpilogueSwiglu || N % (2 * kSwigluBlock) == 0,
+               "swiglu needs N (gate|up interleaved in 16-column blocks) to be a multiple of 32");
   NIBBLE_CHECK(epilogue != kEpilogueBias || M == 0 || bias != nullptr, "null bias");
   NIBBLE_CHECK(epilogue != kEpilogueBias || aligned(bias, 2), "misaligned bias");
   if (norm_w != nullptr) {
@@ -774,12 +1236,16 @@ int validate_fused(const void* X, int64_t x_rows, int64_t x_cols, const void* Wq
 }
 }  // namespace
 
+// The workspace a fused launch may need does not depend on its epilogue: the
+// query answers for the split kernel, the larger of the two plans (the strip
+// kernel needs none), so one buffer serves every epilogue and prologue.
 extern "C" size_t nibble_matmul_fused_workspace_bytes(int64_t M, int64_t K, int64_t N,
                                                       int64_t group_size, void* stream) {
   (void)stream;
   StreamPlan p;
   if (M < 1 || M > kStreamMaxM || K <= 0 || N <= 0 || (group_size != 64 && group_size != 128) ||
-      K % group_size != 0 || plan_stream(M, K, N, group_size, true, 0, 0, &p) != NIBBLE_OK)
+      K % group_size != 0 ||
+      plan_split_kernel(M, K, N, group_size, true, 0, 0, &p) != NIBBLE_OK)
     return 0;
   return p.workspace_bytes;
 }
@@ -789,7 +1255,8 @@ extern "C" size_t nibble_matmul_fused_counter_bytes(int64_t M, int64_t K, int64_
   (void)stream;
   StreamPlan p;
   if (M < 1 || M > kStreamMaxM || K <= 0 || N <= 0 || (group_size != 64 && group_size != 128) ||
-      K % group_size != 0 || plan_stream(M, K, N, group_size, true, 0, 0, &p) != NIBBLE_OK)
+      K % group_size != 0 ||
+      plan_split_kernel(M, K, N, group_size, true, 0, 0, &p) != NIBBLE_OK)
     return 0;
   return p.counter_bytes;
 }
@@ -805,8 +1272,11 @@ extern "C" int nibble_matmul_w4a16_fused(const void* X, int64_t x_rows, int64_t 
   if (rc != NIBBLE_OK) return rc;
   const int64_t M = x_rows, K = x_cols, N = wq_cols;
   if (M == 0) return ok();
+  StreamFusion fusion;
+  fusion.epilogue = static_cast<int>(epilogue);
+  fusion.norm = norm_weight != nullptr;
   StreamPlan p;
-  rc = plan_stream(M, K, N, group_size, true, 0, 0, &p);
+  rc = plan_stream(M, K, N, group_size, true, 0, 0, &p, fusion);
   if (rc != NIBBLE_OK) return rc;
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   DeviceGuard guard;

@@ -10,24 +10,49 @@ namespace nibble {
 
 constexpr int kStreamMaxM = 128;
 
-// Launch geometry.  The split-K workspace (splits > 1) is `counter_bytes` of
-// uint32 counters, one per (row block, strip), zero on entry and left zero,
-// followed by fp32 partials [splits, M, N]; `workspace_bytes` is the total.
+// Two kernels serve the plan.  kSplitKernel: 64-column strips, K split
+// across workgroups when a wave would stream too many groups, partials
+// reduced by the last workgroup of a strip (any M up to kStreamMaxM).
+// kStripKernel (M <= 8): `strip_cols`-column strips over the whole of K,
+// `waves` waves per workgroup on contiguous group ranges with `depth` groups
+// of loads in flight per wave; no workspace.
+constexpr int kSplitKernel = 0;
+constexpr int kStripKernel = 1;
+
+// Launch geometry.  The split-K workspace (split kernel, splits > 1) is
+// `counter_bytes` of uint32 counters, one per (row block, strip), zero on
+// entry and left zero, followed by fp32 partials [splits, M, N];
+// `workspace_bytes` is the total.
 struct StreamPlan {
+  int kernel = kSplitKernel;
   int mt = 1;      // compiled row count: 1, 2, 4, 8, 16 or 32
   int mblocks = 1; // blocks of mt rows (grid.z); more than one only above 32 rows
   int waves = 4;   // wave64s per workgroup
-  int strips = 0;  // 64-column strips (grid.x)
+  int strips = 0;  // column strips (grid.x for the split kernel)
   int splits = 1;  // K splits (grid.y)
   int groups_per_split = 0;
+  int strip_cols = 64;  // strip kernel: 16, 32 or 64
+  int depth = 2;        // strip kernel: groups in flight per wave
   size_t counter_bytes = 0;
   size_t workspace_bytes = 0;
 };
 
-// Pure host arithmetic.  split_k = false forces one split (gemv versions 2
-// and 3); splits_override / threads_override of 0 mean "heuristic".
+// What a launch asks of the kernel besides the matmul: the output epilogue
+// (0 none, 1 bias, 2 SwiGLU) and whether the RMSNorm prologue is fused.
+struct StreamFusion {
+  int epilogue = 0;
+  bool norm = false;
+};
+
+// Pure host arithmetic.  split_k = false forces one split of the split
+// kernel (gemv versions 2 and 3); splits_override / threads_override of 0
+// mean "heuristic", and only the heuristic path may choose the strip kernel.
 int plan_stream(int64_t M, int64_t K, int64_t N, int64_t G, bool split_k, int64_t splits_override,
-                int64_t threads_override, StreamPlan* p);
+                int64_t threads_override, StreamPlan* p, StreamFusion fusion = StreamFusion());
+
+// The strip kernel's plan for these operands, if it serves them (M <= 8,
+// and the fusion it supports); returns false otherwise.  Pure host arithmetic.
+bool plan_strip(int64_t M, int64_t K, int64_t N, int64_t G, StreamFusion fusion, StreamPlan* p);
 
 // Whether the streaming kernel can take these operands: N a multiple of 4,
 // 16-byte X and Wq, 8-byte S and Y, offsets within 31 bits.

@@ -11,12 +11,17 @@ instead of a pybind11 torch extension:
   as the reference allocated them in C++;
 * kernels launch on torch's current stream of that device, so calls compose
   with torch ops and can be recorded into CUDA/HIP graphs;
-* the split-K workspace of ``gemv`` comes from a cache of zeroed buffers keyed
-  by (device, stream, graph capture, counter-region size): the kernel returns its counter region to
-  zero at the end of every call, so a buffer is zeroed once and then reused.
-  Inside a graph capture the first call allocates and zeroes a buffer for that
-  capture, so the zeroing is part of the graph and every replay starts from
-  zero; that buffer stays cached (one per capture) for the life of the process.
+* the split-K workspace of the split kernel comes from a cache of zeroed
+  buffers keyed by (device, stream, graph capture, counter-region size): the
+  kernel returns its counter region to zero at the end of every call, so a
+  buffer is zeroed once and then reused.  Inside a graph capture the first call
+  allocates and zeroes a buffer for that capture from the graph's private
+  memory pool, so the zeroing is part of the graph and every replay starts
+  from zero.  The cache holds a capture's buffers only while that capture is
+  in progress: the first call from another capture, or outside any, drops
+  them, and the graph's pool keeps their memory until the graph is destroyed.
+  (Graphs that share one memory pool must not be replayed concurrently with
+  each other -- PyTorch's own condition for sharing a pool.)
 """
 from __future__ import annotations
 
@@ -35,6 +40,7 @@ DECODE_MAX_M = 8
 
 _lock = threading.Lock()
 _workspaces: Dict[Tuple[int, int, int, int], torch.Tensor] = {}
+_capture_entries = 0  # cached buffers that belong to a graph capture
 _ws_plan: Dict[tuple, Tuple[int, int]] = {}
 
 _get_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
@@ -141,22 +147,52 @@ def _workspace(plan: Tuple[int, int], device: torch.device,
                stream: int) -> Tuple[Optional[torch.Tensor], int]:
     """A zeroed buffer of at least ``plan[0]`` bytes whose leading
     ``plan[1]`` bytes (split-K counters) are zero; None if no bytes needed."""
+    global _capture_entries
     nbytes, counter_bytes = plan
     if nbytes == 0:
         return None, 0
     # One buffer per counter-region size: a plan's fp32 partials start right
     # after its counters, so a plan with fewer counters would overwrite the
     # (zero) counters of a plan with more if they shared a buffer.
-    wkey = (device.index, stream, _capture_id(stream), counter_bytes)
+    capture = _capture_id(stream)
+    wkey = (device.index, stream, capture, counter_bytes)
     buf = _workspaces.get(wkey)
     if buf is None or buf.numel() < nbytes:
         with _lock:
+            _drop_ended_captures(capture)
             buf = _workspaces.get(wkey)
             if buf is None or buf.numel() < nbytes:
                 size = max(nbytes, 1 << 20)
                 buf = torch.zeros(size, dtype=torch.uint8, device=device)
                 _workspaces[wkey] = buf
+                if capture != 0:
+                    _capture_entries += 1
+    elif capture == 0 and _capture_entries:
+        with _lock:
+            _drop_ended_captures(0)
     return buf, buf.numel()
+
+
+def _drop_ended_captures(current: int) -> None:
+    """Forget the buffers of every capture other than ``current`` (called
+    under ``_lock``).  Calls are made from one capture at a time, so a call
+    from elsewhere means those captures have ended; their memory belongs to
+    their graphs' pools, which free it with the graphs."""
+    global _capture_entries
+    if not _capture_entries:
+        return
+    for key in [k for k in _workspaces if k[2] not in (0, current)]:
+        del _workspaces[key]
+    _capture_entries = sum(1 for k in _workspaces if k[2] != 0)
+
+
+def release_workspaces() -> None:
+    """Drop every cached split-K workspace (eager and capture buffers alike);
+    later calls allocate and zero fresh ones."""
+    global _capture_entries
+    with _lock:
+        _workspaces.clear()
+        _capture_entries = 0
 
 
 def _gemv_workspace(ext, device: torch.device, stream: int, M: int, K: int, N: int, g: int,
@@ -337,7 +373,7 @@ def matmul_swiglu(X: torch.Tensor, qw: QuantizedWeight) -> torch.Tensor:
     silu, then the product).  M <= 128 runs as one launch."""
     _check_2d(X, qw)
     if qw.N % (2 * SWIGLU_BLOCK):
-        raise ValueError(f"N={qw.N} is not an interleaved gate|up weight (multiple of 64)")
+        raise ValueError(f"N={qw.N} is not an interleaved gate|up weight (multiple of 32)")
     if _fusable(X, qw):
         return _fused(X, qw, 2, None, qw.N // 2)
     gate, up = split_swiglu(matmul(X, qw))
@@ -362,7 +398,7 @@ def rmsnorm_matmul(X: torch.Tensor, norm_weight: torch.Tensor, qw: QuantizedWeig
     if bias is not None and swiglu:
         raise ValueError("bias and swiglu epilogues are exclusive")
     if swiglu and qw.N % (2 * SWIGLU_BLOCK):
-        raise ValueError(f"N={qw.N} is not an interleaved gate|up weight (multiple of 64)")
+        raise ValueError(f"N={qw.N} is not an interleaved gate|up weight (multiple of 32)")
     M, K = X.shape
     mt = 1 if M <= 1 else 2 if M <= 2 else 4 if M <= 4 else 8
     if (_fusable(X, qw) and M <= NORM_FUSED_MAX_M and K <= NORM_FUSED_MAX_K and mt * K * 2 <= 65536
@@ -383,32 +419,38 @@ def rmsnorm_matmul(X: torch.Tensor, norm_weight: torch.Tensor, qw: QuantizedWeig
 
 
 class QuantLinear(torch.nn.Module):
-    """Drop-in replacement for ``nn.Linear`` with INT4 weights (reference
-    ops.py:107-135).  Buffers ``qweight``, ``scales`` and ``bias`` keep the
-    reference's names, so state dicts carry over unchanged."""
+    """An ``nn.Linear`` whose weight is packed INT4 (reference ops.py:107-135).
+
+    The module holds three buffers under the reference's names -- ``qweight``
+    (int32 ``[in/8, out]``), ``scales`` (fp16 ``[in/G, out]``) and ``bias``
+    (or None) -- so state dicts move between the two packages unchanged.
+    ``forward`` flattens leading dimensions, multiplies through
+    :func:`matmul` and adds the bias; an fp16 bias is added inside the
+    matmul's output stage where the kernel supports it (same bits as a
+    separate fp16 add)."""
 
     def __init__(self, qw: QuantizedWeight, bias: Optional[torch.Tensor] = None):
         super().__init__()
-        self.register_buffer("qweight", qw.qweight)
-        self.register_buffer("scales", qw.scales)
-        self.register_buffer("bias", bias if bias is not None else None)
-        self.group_size, self.K, self.N = qw.group_size, qw.K, qw.N
+        self.group_size = qw.group_size
+        self.K = qw.K
+        self.N = qw.N
+        for name, tensor in (("qweight", qw.qweight), ("scales", qw.scales), ("bias", bias)):
+            self.register_buffer(name, tensor)
 
     @classmethod
     def from_linear(cls, linear: torch.nn.Linear, group_size: int = 128) -> "QuantLinear":
-        # nn.Linear stores [out, in]; the kernels consume [in, out].
-        qw = quantize(linear.weight.data.t().contiguous(), group_size)
-        bias = linear.bias.data.clone() if linear.bias is not None else None
-        return cls(qw.to(linear.weight.device), bias)
+        """Quantise ``linear`` (RTN, group ``group_size``) onto its own device.
+        ``nn.Linear`` keeps ``[out_features, in_features]``; the packed format
+        is ``[K = in_features, N = out_features]``, hence the transpose."""
+        weight_kn = linear.weight.detach().transpose(0, 1).contiguous()
+        bias = None if linear.bias is None else linear.bias.detach().clone()
+        return cls(quantize(weight_kn, group_size).to(linear.weight.device), bias)
 
     def _qw(self) -> QuantizedWeight:
         return QuantizedWeight(self.qweight, self.scales, self.group_size, self.K, self.N)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        shape = x.shape
-        x2 = x.reshape(-1, shape[-1]).contiguous()
-        if self.bias is None:
-            y = matmul(x2, self._qw())
-        else:
-            y = matmul_bias(x2, self._qw(), self.bias)
-        return y.reshape(*shape[:-1], self.N)
+        lead = x.shape[:-1]
+        rows = x.reshape(-1, x.shape[-1]).contiguous()
+        y = matmul(rows, self._qw()) if self.bias is None else matmul_bias(rows, self._qw(), self.bias)
+        return y.reshape(*lead, self.N)

@@ -1,155 +1,149 @@
-"""Packed INT4 weight format: quantiser, packer and host-side decode.
+"""The packed INT4 weight format and its host-side tools.
 
-Drop-in for ``python/nibblegemm/quant.py`` of arvindcr4/nibblegemm: same names,
-same array shapes and dtypes, same errors.
+Drop-in for ``python/nibblegemm/quant.py`` of arvindcr4/nibblegemm: the public
+names, argument orders, dtypes and exceptions are that module's (callers and
+checkpoints move over unchanged); the code is this package's own.
 
-Format (reference quant.py:8-54)
---------------------------------
-``W`` is ``[K, N]`` and consumed as ``Y = X @ W`` (K is the reduction axis).
+Layout (the reference documents it at quant.py:8-54)
+----------------------------------------------------
+A weight ``W`` is ``[K, N]`` and is applied as ``Y = X @ W``.  Every run of
+``group_size`` consecutive k shares one fp16 scale per column (``scales`` is
+``[K / group_size, N]``).  A weight is stored as the 4-bit code
+``round_half_even(w / scale)`` clamped to ``[-8, 7]`` and offset by 8, so codes
+are ``0..15`` and the zero point is implicit.  The scale of a group column is
+its largest magnitude divided by 7 (never below 1e-8).
 
-* Groups of ``group_size`` rows along K share one fp16 scale per column.
-* Symmetric INT4: ``q = clamp(round_half_even(w / scale), -8, 7)``, stored as
-  ``q + 8`` in ``[0, 15]``; there is no zero-point tensor.
-* ``scale = max(max|w| / 7, 1e-8)`` per group and column (plain max-abs).
-* Eight nibbles along K share one 32-bit word: ``qweight`` is int32
-  ``[K // 8, N]``.  Logical offset ``k`` of a word lives in nibble slot
-  ``SLOT_FOR_K[k] = [0, 4, 1, 5, 2, 6, 3, 7]`` (even k in slots 0..3, odd k in
-  slots 4..7), the order in which the kernels' mask-and-or decode emits fp16
-  pairs in ascending k.
+Codes are packed eight to a 32-bit word along K (``qweight`` is int32
+``[K / 8, N]``).  Code k of a word occupies bits ``4 * SLOT_FOR_K[k]`` up: the
+even k take the low four nibbles and the odd k the high four, which is what
+lets the kernels turn two codes sixteen bits apart into one fp16 pair with a
+single mask-and-or.
 
-Host code only: packing happens at quantisation time, ``dequantize`` and
-``reference_matmul`` reproduce the reference's definitions for callers' own
-checks.  The kernel entry points in :mod:`nibblegemm_amd.ops` never call them.
+This module never launches a kernel; :mod:`nibblegemm_amd.ops` never calls its
+host decoders.
 """
 from __future__ import annotations
 
+import dataclasses
 from dataclasses import dataclass
 
 import numpy as np
 import torch
 
-#: ``SLOT_FOR_K[k]`` is the nibble slot that stores logical offset ``k`` (0..7).
+#: Nibble slot of each logical k within a packed word.
 SLOT_FOR_K = np.array([0, 4, 1, 5, 2, 6, 3, 7], dtype=np.int64)
-#: Inverse permutation: ``K_FOR_SLOT[s]`` is the logical offset held by slot ``s``.
+#: Logical k held by each nibble slot (the inverse permutation).
 K_FOR_SLOT = np.argsort(SLOT_FOR_K)
 
 QMIN, QMAX = -8, 7
 ZERO_POINT = 8
 PACK_FACTOR = 8
 
+_SHIFTS = (4 * SLOT_FOR_K).astype(np.uint32)  # bit offset of each k's nibble
+
 
 @dataclass(frozen=True)
 class QuantizedWeight:
-    """Packed INT4 weights plus their fp16 group scales (reference quant.py:60-78)."""
+    """One quantised ``[K, N]`` weight: the packed codes, the group scales and
+    the shape they describe (reference quant.py:60-78)."""
 
-    qweight: torch.Tensor  # int32 [K // 8, N], nibble-interleaved
-    scales: torch.Tensor  # fp16  [K // G, N]
+    qweight: torch.Tensor  # int32 [K // 8, N]
+    scales: torch.Tensor  # fp16  [K // group_size, N]
     group_size: int
     K: int
     N: int
 
     def to(self, device) -> "QuantizedWeight":
-        return QuantizedWeight(
-            self.qweight.to(device), self.scales.to(device), self.group_size, self.K, self.N
-        )
+        """The same weight with both tensors moved to ``device``."""
+        return dataclasses.replace(self, qweight=self.qweight.to(device),
+                                   scales=self.scales.to(device))
 
     @property
     def weight_bytes(self) -> int:
-        """Bytes of weight traffic a perfect kernel must read (packed + scales)."""
-        return self.qweight.numel() * 4 + self.scales.numel() * 2
+        """Bytes a matmul must read for this weight: packed codes and scales."""
+        return sum(t.numel() * t.element_size() for t in (self.qweight, self.scales))
 
 
-# Clipping ratios the scale search tries, largest first (reference quant.py:57).
+#: Clip ratios of the optional scale search, from 1.0 (plain max-abs) down.
 CLIP_RATIOS = torch.linspace(1.0, 0.55, 19)
 
 
-def _search_scale(groups: torch.Tensor, n_chunk: int = 4096) -> torch.Tensor:
-    """Per-group scale minimising the group's squared quantisation error over
-    the clipping ratios ``CLIP_RATIOS`` (reference quant.py:81-124): for each
-    ratio r, ``scale = max(amax * r / 7, 1e-8)``, the group rounded with it,
-    and the sum of squared errors; a later ratio replaces the best so far only
-    when strictly better.  The reference keeps it as a documented negative
-    result (lower weight error, worse model quality); it is off by default.
+def _check_quantize_args(W: torch.Tensor, group_size: int):
+    if W.ndim != 2:
+        raise ValueError(f"expected a 2-D weight, got shape {tuple(W.shape)}")
+    K, N = W.shape
+    if K % group_size:
+        raise ValueError(f"K={K} must be divisible by group_size={group_size}")
+    if group_size % PACK_FACTOR:
+        raise ValueError(f"group_size={group_size} must be divisible by {PACK_FACTOR}")
+    return K, N
 
-    groups: float32 ``[K/G, G, N]`` -> scales ``[K/G, N]``, on groups' device,
-    processed ``n_chunk`` columns at a time."""
+
+def _codes(groups: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """Offset 4-bit codes (0..15, float) of ``groups`` ``[K/G, G, N]`` at the
+    per-group-column ``scale`` ``[K/G, N]``: half-even rounding of the true
+    quotient, clamped to the signed range, plus the zero point."""
+    return torch.round(groups / scale[:, None, :]).clamp(QMIN, QMAX) + ZERO_POINT
+
+
+def _search_scale(groups: torch.Tensor, n_chunk: int = 4096) -> torch.Tensor:
+    """Scales chosen by squared quantisation error instead of max-abs
+    (reference quant.py:81-124, which keeps it, off by default, as a measured
+    negative result for model quality).
+
+    Each candidate is ``max(amax * r / 7, 1e-8)`` for the ratios r of
+    ``CLIP_RATIOS``; the error of a group column is the sum over the group of
+    ``(q * s - w)^2`` in float32.  The pick is the first candidate reaching the
+    smallest error, so ratio 1.0 (max-abs) wins every tie.  ``groups`` is
+    float32 ``[K/G, G, N]``; the result ``[K/G, N]`` is on its device, worked
+    out ``n_chunk`` columns at a time."""
     n_groups, _, N = groups.shape
-    out = torch.empty((n_groups, N), dtype=groups.dtype, device=groups.device)
     ratios = CLIP_RATIOS.to(groups.device, groups.dtype)
-    for c0 in range(0, N, n_chunk):
-        blk = groups[:, :, c0:c0 + n_chunk]
-        amax = blk.abs().amax(dim=1)
-        best = (amax / QMAX).clamp(min=1e-8)
-        best_err = torch.full_like(amax, float("inf"))
+    out = torch.empty((n_groups, N), dtype=groups.dtype, device=groups.device)
+    for lo in range(0, N, n_chunk):
+        w = groups[:, :, lo:lo + n_chunk]
+        amax = w.abs().amax(dim=1)
+        cands = []
+        errs = []
         for r in ratios:
             s = (amax * r / QMAX).clamp(min=1e-8)
-            q = torch.round(blk / s.unsqueeze(1)).clamp(QMIN, QMAX)
-            err = (q * s.unsqueeze(1) - blk).pow(2).sum(dim=1)
-            take = err < best_err
-            best_err = torch.where(take, err, best_err)
-            best = torch.where(take, s, best)
-        out[:, c0:c0 + n_chunk] = best
+            q = torch.round(w / s[:, None, :]).clamp(QMIN, QMAX)
+            errs.append((q * s[:, None, :] - w).pow(2).sum(dim=1))
+            cands.append(s)
+        pick = torch.stack(errs).argmin(dim=0, keepdim=True)  # first minimum
+        out[:, lo:lo + n_chunk] = torch.stack(cands).gather(0, pick)[0]
     return out
 
 
 def quantize(W: torch.Tensor, group_size: int = 128, clip_search: bool = False) -> QuantizedWeight:
-    """Round-to-nearest quantise a ``[K, N]`` weight to packed group-wise INT4.
-
-    Reference quant.py:127-161.  ``clip_search`` picks each group's scale by
-    :func:`_search_scale` instead of max-abs (off by default, as in the
-    reference, which documents it as lowering model quality).  The work runs
-    on W's device; the result is on the host.
-    """
-    if W.ndim != 2:
-        raise ValueError(f"expected a 2-D weight, got shape {tuple(W.shape)}")
-    K, N = W.shape
-    if K % group_size:
-        raise ValueError(f"K={K} must be divisible by group_size={group_size}")
-    if group_size % PACK_FACTOR:
-        raise ValueError(f"group_size={group_size} must be divisible by {PACK_FACTOR}")
-
-    w = W.detach().float()
-    groups = w.reshape(K // group_size, group_size, N)
+    """Round-to-nearest group-wise INT4 of a ``[K, N]`` weight (reference
+    quant.py:127-161).  The arithmetic runs on W's device, in float32, with the
+    reference's operations (the max-abs scale divides by the Python scalar 7);
+    the packed result is returned on the host.  ``clip_search`` takes the
+    scales from :func:`_search_scale` instead."""
+    K, N = _check_quantize_args(W, group_size)
+    groups = W.detach().float().reshape(K // group_size, group_size, N)
     if clip_search:
         scale = _search_scale(groups)
     else:
-        # Clamp away exact zeros so all-zero groups stay finite.
-        scale = (groups.abs().amax(dim=1) / QMAX).clamp(min=1e-8)
-    q = torch.round(groups / scale.unsqueeze(1)).clamp(QMIN, QMAX)
-    qu = (q + ZERO_POINT).reshape(K, N).to(torch.uint8).cpu().numpy()
-
-    return QuantizedWeight(
-        qweight=torch.from_numpy(pack_nibbles(qu)),
-        scales=scale.to(torch.float16).cpu().contiguous(),
-        group_size=group_size,
-        K=K,
-        N=N,
-    )
+        scale = (groups.abs().amax(dim=1) / QMAX).clamp(min=1e-8)  # all-zero groups stay finite
+    codes = _codes(groups, scale).reshape(K, N).to(torch.uint8).cpu().numpy()
+    return QuantizedWeight(torch.from_numpy(pack_nibbles(codes)),
+                           scale.to(torch.float16).cpu().contiguous(), group_size, K, N)
 
 
 def quantize_device(W: torch.Tensor, group_size: int = 128) -> QuantizedWeight:
-    """:func:`quantize` without leaving W's device: the same round-to-nearest
-    INT4 and the same packed layout, bit for bit, with ``qweight`` and
-    ``scales`` on W's device.  For building large weight stacks on the GPU
-    (the reference's ``quantize`` always returns host tensors,
-    python/nibblegemm/quant.py:154-161).
-    """
-    if W.ndim != 2:
-        raise ValueError(f"expected a 2-D weight, got shape {tuple(W.shape)}")
-    K, N = W.shape
-    if K % group_size:
-        raise ValueError(f"K={K} must be divisible by group_size={group_size}")
-    if group_size % PACK_FACTOR:
-        raise ValueError(f"group_size={group_size} must be divisible by {PACK_FACTOR}")
-
+    """:func:`quantize` kept on W's device: the same codes, scales and packed
+    layout, with ``qweight`` and ``scales`` left where W is (for building large
+    weight stacks on the GPU; the reference's ``quantize`` always returns host
+    tensors).  The max-abs scale divides by a tensor of 7s: a GPU divides by a
+    Python scalar as a multiply by its reciprocal, which can round differently
+    from the true division a host ``quantize`` performs."""
+    K, N = _check_quantize_args(W, group_size)
     groups = W.detach().float().reshape(K // group_size, group_size, N)
     amax = groups.abs().amax(dim=1)
-    # A tensor divisor, not the Python scalar 7: on the GPU a scalar divisor is
-    # applied as a multiply by its reciprocal, which can round differently
-    # from the true division the host path performs.
     scale = (amax / torch.full_like(amax, float(QMAX))).clamp(min=1e-8)
-    q = torch.round(groups / scale.unsqueeze(1)).clamp(QMIN, QMAX)
-    packed = pack_nibbles_device((q + ZERO_POINT).reshape(K, N))
+    packed = pack_nibbles_device(_codes(groups, scale).reshape(K, N))
     return QuantizedWeight(packed, scale.to(torch.float16).contiguous(), group_size, K, N)
 
 
@@ -184,14 +178,15 @@ def concat_columns(*qws: QuantizedWeight) -> QuantizedWeight:
                            g, K, sum(qw.N for qw in qws))
 
 
-#: Column block of :func:`interleave_swiglu` (half of the kernels' 64-column strip).
-SWIGLU_BLOCK = 32
+#: Column block of :func:`interleave_swiglu`: every 32-column strip of the
+#: kernels holds 16 gate columns and the matching 16 up columns.
+SWIGLU_BLOCK = 16
 
 
 def interleave_swiglu(gate: QuantizedWeight, up: QuantizedWeight) -> QuantizedWeight:
     """The gate and up projections of a SwiGLU MLP as one ``[K, 2N]`` weight
-    whose columns alternate in blocks of 32: gate 0..31, up 0..31, gate
-    32..63, ...  Every 64-column strip of the kernels then holds matching
+    whose columns alternate in blocks of 16: gate 0..15, up 0..15, gate
+    16..31, ...  Every 32- or 64-column strip of the kernels then holds matching
     gate and up columns, which lets one launch write ``silu(X Wg) * (X Wu)``
     (``ops.matmul_swiglu``).  Packing runs along K, so permuting packed and
     scale columns is exact."""
@@ -221,50 +216,46 @@ def split_swiglu(y: torch.Tensor):
 
 
 def pack_nibbles(qu: np.ndarray) -> np.ndarray:
-    """Pack ``uint8 [K, N]`` values in ``[0, 15]`` into ``int32 [K // 8, N]``.
-
-    Works in uint32 so the top nibble cannot trip signed overflow, then views
-    the result as int32 (the dtype the kernels take).  Reference quant.py:164-182.
-    """
+    """Codes ``[K, N]`` (values 0..15) to packed words ``int32 [K // 8, N]``
+    (reference quant.py:164-182).  Each code is shifted to its nibble slot and
+    the eight of a word are OR-ed in uint32 (no sign to overflow into); the
+    words are returned viewed as int32, the dtype the kernels take."""
     qu = np.asarray(qu)
     K, N = qu.shape
     if K % PACK_FACTOR:
         raise ValueError(f"K={K} must be divisible by {PACK_FACTOR}")
     if qu.max(initial=0) > 15:
         raise ValueError("quantised values must fit in 4 bits")
-
-    blocks = qu.reshape(K // PACK_FACTOR, PACK_FACTOR, N).astype(np.uint32)
-    packed = np.zeros((K // PACK_FACTOR, N), dtype=np.uint32)
-    for k_off in range(PACK_FACTOR):
-        packed |= (blocks[:, k_off, :] & np.uint32(0xF)) << np.uint32(4 * int(SLOT_FOR_K[k_off]))
-    return packed.view(np.int32)
+    codes = qu.reshape(K // PACK_FACTOR, PACK_FACTOR, N).astype(np.uint32)
+    words = np.bitwise_or.reduce(codes << _SHIFTS[None, :, None], axis=1)
+    return np.ascontiguousarray(words, dtype=np.uint32).view(np.int32)
 
 
 def unpack_nibbles(packed: np.ndarray, K: int) -> np.ndarray:
-    """Inverse of :func:`pack_nibbles`; returns ``uint8 [K, N]`` in ``[0, 15]``
-    (reference quant.py:185-196)."""
-    p = np.ascontiguousarray(packed).view(np.uint32)
-    rows, N = p.shape
+    """Packed words ``[K // 8, N]`` back to codes ``uint8 [K, N]`` (reference
+    quant.py:185-196)."""
+    words = np.ascontiguousarray(packed).view(np.uint32)
+    rows, N = words.shape
     if rows * PACK_FACTOR != K:
         raise ValueError(f"packed rows={rows} inconsistent with K={K}")
-    out = np.empty((rows, PACK_FACTOR, N), dtype=np.uint8)
-    for k_off in range(PACK_FACTOR):
-        out[:, k_off, :] = ((p >> np.uint32(4 * int(SLOT_FOR_K[k_off]))) & np.uint32(0xF)).astype(np.uint8)
-    return out.reshape(K, N)
+    codes = (words[:, None, :] >> _SHIFTS[None, :, None]) & np.uint32(0xF)
+    return codes.astype(np.uint8).reshape(K, N)
 
 
 def dequantize(qw: QuantizedWeight) -> torch.Tensor:
-    """The ``[K, N]`` fp16 weight the kernels model, on the host:
-    ``fp16((nibble - 8) * fp32(scale))`` (reference quant.py:199-204).
-    The device kernel for the same result is :func:`nibblegemm_amd.ops.dequant`."""
-    qu = unpack_nibbles(qw.qweight.cpu().numpy(), qw.K)
-    q = torch.from_numpy(qu.astype(np.int16)).float() - ZERO_POINT
-    scale = qw.scales.float().cpu().repeat_interleave(qw.group_size, dim=0)
-    return (q * scale).to(torch.float16)
+    """The fp16 ``[K, N]`` weight a packed weight stands for, on the host
+    (reference quant.py:199-204): ``(code - 8) * scale`` formed in float32 --
+    exact, since both factors fit in 11 bits -- and rounded once to fp16.  The
+    device kernel for the same bits is :func:`nibblegemm_amd.ops.dequant`."""
+    codes = unpack_nibbles(qw.qweight.cpu().numpy(), qw.K)
+    signed = codes.astype(np.float32) - np.float32(ZERO_POINT)
+    per_row = np.repeat(qw.scales.cpu().numpy().astype(np.float32), qw.group_size, axis=0)
+    return torch.from_numpy((signed * per_row).astype(np.float16))
 
 
 def reference_matmul(X: torch.Tensor, qw: QuantizedWeight) -> torch.Tensor:
-    """fp32-accumulated ``X @ dequantize(qw)`` rounded to fp16, on X's device
-    (reference quant.py:207-215)."""
-    W = dequantize(qw).to(X.device).float()
-    return (X.float() @ W).to(torch.float16)
+    """``X @ dequantize(qw)`` accumulated in float32 and rounded to fp16, on
+    X's device (reference quant.py:207-215): the yardstick the kernels are
+    tested against."""
+    W = dequantize(qw).to(device=X.device, dtype=torch.float32)
+    return torch.matmul(X.to(torch.float32), W).to(torch.float16)

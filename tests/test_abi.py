@@ -138,12 +138,15 @@ def test_gemv_workspace_formula():
     # a single split needs no workspace
     assert ext.gemv_workspace_bytes(1, 1024, 256, 64, 4, 1, 0, None) == (0, 0)
     assert ext.gemv_workspace_bytes(1, 1024, 256, 64, 3, 0, 0, None) == (0, 0)
-    # default plan at the benchmark decode shapes (pure host arithmetic):
-    # one split up to 32 quant groups, then ~8 groups per wave of 4
+    # default plan at the benchmark decode shapes (pure host arithmetic): the
+    # strip kernel (no workspace) up to K = 8192; beyond, the split kernel
+    # with ~8 groups per wave of 4
     assert ext.gemv_workspace_bytes(1, 4096, 14336, 128, 4, 0, 0, None) == (0, 0)
     assert ext.gemv_workspace_bytes(1, 4096, 4096, 128, 4, 0, 0, None) == (0, 0)
+    assert ext.gemv_workspace_bytes(1, 8192, 8192, 128, 4, 0, 0, None) == (0, 0)
     assert ext.gemv_workspace_bytes(1, 14336, 4096, 128, 4, 0, 0, None) == (256 + 4 * 4096 * 4, 256)
-    assert ext.gemv_workspace_bytes(1, 8192, 8192, 128, 4, 0, 0, None) == (512 + 2 * 8192 * 4, 512)
+    # an explicit split count always runs the split kernel
+    assert ext.gemv_workspace_bytes(1, 8192, 8192, 128, 4, 2, 0, None) == (512 + 2 * 8192 * 4, 512)
     # 14336 / 64 = 224 strips of counters need 896 bytes, padded to 1024
     assert ext.gemv_workspace_bytes(2, 16384, 14336, 128, 4, 0, 0, None) == (
         1024 + 4 * 2 * 14336 * 4, 1024)
@@ -263,7 +266,7 @@ def fused(ext, M, K, N, g=128, epilogue=1, bias=P, wq_rows=None, s_rows=None, s_
 @pytest.mark.parametrize("kwargs,needle", [
     (dict(M=129, K=256, N=128), "M <= 128"),
     (dict(M=4, K=256, N=128, epilogue=3), "epilogue"),
-    (dict(M=4, K=256, N=96, epilogue=2), "multiple of 64"),
+    (dict(M=4, K=256, N=80, epilogue=2), "multiple of 32"),
     (dict(M=4, K=256, N=130, epilogue=0), "multiple of 4"),
     (dict(M=4, K=256, N=128, bias=None), "null bias"),
     (dict(M=4, K=256, N=128, wq_rows=31), "packed weight rows"),

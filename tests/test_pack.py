@@ -1,6 +1,10 @@
-"""On-disk nibble format of the package (reference tests/test_pack.py intents).
+"""The packed nibble format, on the host: the layout every kernel decodes.
 
-CPU only: pins the layout every kernel decodes.
+CPU only.  The slot table and the word 0x75316420 are the reference's
+known-answer data (tests/test_pack.py:17, :42 there); the checks around them
+are this package's: every (slot, code) bit position, agreement with the C
+oracle's independent packer, both round trips, and the input validation of
+the drop-in functions (ValueError, as in python/nibblegemm/quant.py).
 """
 from __future__ import annotations
 
@@ -12,92 +16,88 @@ import nibblegemm_amd as ng
 from nibblegemm_amd import quant
 from nibblegemm_amd.quant import PACK_FACTOR, SLOT_FOR_K, dequantize, quantize
 
-EXPECTED_SLOT_FOR_K = [0, 4, 1, 5, 2, 6, 3, 7]
+SLOT_TABLE = (0, 4, 1, 5, 2, 6, 3, 7)  # known-answer data: slot of k = 0..7
+ASCENDING_WORD = 0x75316420  # known-answer data: codes k = 0..7 packed
 
 
-def test_slot_table_is_the_documented_permutation():
-    assert list(SLOT_FOR_K) == EXPECTED_SLOT_FOR_K
-    assert list(ng.quant.K_FOR_SLOT) == [0, 2, 4, 6, 1, 3, 5, 7]
+def test_format_constants():
+    assert tuple(SLOT_FOR_K) == SLOT_TABLE
+    assert (quant.QMIN, quant.QMAX, quant.ZERO_POINT, quant.PACK_FACTOR) == (-8, 7, 8, 8)
+    # K_FOR_SLOT inverts the table; even k live in slots 0..3, odd k in 4..7.
+    assert [int(quant.K_FOR_SLOT[SLOT_FOR_K[k]]) for k in range(8)] == list(range(8))
+    assert [SLOT_TABLE[k] // 4 for k in range(8)] == [k % 2 for k in range(8)]
 
 
-def test_slot_table_matches_the_cuda_scalar_decode():
-    """The reference's scalar decode computes the slot instead of looking it
-    up (csrc/dequant.cuh:96: odd k in the high half of the word); the formula
-    gives the documented table."""
-    slot = [(4 + (k >> 1)) if (k & 1) else (k >> 1) for k in range(PACK_FACTOR)]
-    assert slot == EXPECTED_SLOT_FOR_K
+def test_every_code_lands_in_its_slot():
+    """A column holding one nonzero code c at offset k packs to exactly
+    c << (4 * slot(k)): all 8 offsets x 15 codes."""
+    for k in range(8):
+        qu = np.zeros((8, 15), np.uint8)
+        qu[k, :] = np.arange(1, 16)
+        words = ng.pack_nibbles(qu).view(np.uint32)[0]
+        assert words.tolist() == [c << (4 * SLOT_TABLE[k]) for c in range(1, 16)]
 
 
-def test_nibble_slot_assignment_is_pinned():
-    qu = np.arange(PACK_FACTOR, dtype=np.uint8).reshape(PACK_FACTOR, 1)
-    word = int(ng.pack_nibbles(qu).view(np.uint32)[0, 0])
-    for k, slot in enumerate(EXPECTED_SLOT_FOR_K):
-        assert (word >> (4 * slot)) & 0xF == k
-    assert word == 0x75316420
+def test_ascending_codes_known_answer():
+    qu = np.arange(8, dtype=np.uint8)[:, None]
+    assert int(ng.pack_nibbles(qu).view(np.uint32)[0, 0]) == ASCENDING_WORD
+    # and read back, slot by slot
+    assert [(ASCENDING_WORD >> (4 * s)) & 0xF for s in SLOT_TABLE] == list(range(8))
 
 
-@pytest.mark.parametrize("shape", [(8, 1), (8, 4), (256, 64), (128, 130), (1024, 3), (2048, 1)])
-def test_pack_unpack_is_an_involution(shape):
-    K, N = shape
-    qu = np.random.default_rng(K * 31 + N).integers(0, 16, size=shape, dtype=np.uint8)
-    packed = ng.pack_nibbles(qu)
-    assert packed.dtype == np.int32
-    assert packed.shape == (K // PACK_FACTOR, N)
-    assert np.array_equal(ng.unpack_nibbles(packed, K), qu)
+@pytest.mark.parametrize("K,N,seed", [(8, 5, 0), (64, 33, 1), (512, 96, 2), (4096, 7, 3)])
+def test_packer_agrees_with_the_oracle_and_round_trips(oracle, K, N, seed):
+    rng = np.random.default_rng(seed)
+    codes = rng.integers(0, 16, size=(K, N), dtype=np.uint8)
+    packed = ng.pack_nibbles(codes)
+    assert packed.dtype == np.int32 and packed.shape == (K // 8, N)
+    assert np.array_equal(packed, oracle.pack_nibbles(codes))
+    assert np.array_equal(ng.unpack_nibbles(packed, K), codes)
+    # arbitrary words (negative int32 included) survive unpack -> pack
+    words = rng.integers(-(1 << 31), 1 << 31, size=(K // 8, N), dtype=np.int64).astype(np.int32)
+    assert np.array_equal(ng.pack_nibbles(ng.unpack_nibbles(words, K)), words)
 
 
-def test_top_nibble_sets_the_sign_bit():
-    qu = np.zeros((8, 1), np.uint8)
-    qu[7, 0] = 15  # k = 7 lives in slot 7, bits 28..31
-    assert int(ng.pack_nibbles(qu)[0, 0]) == -(1 << 31) + (7 << 28)
+def test_high_codes_at_k7_make_negative_words():
+    qu = np.zeros((8, 16), np.uint8)
+    qu[7, :] = np.arange(16)  # k = 7 sits in the top nibble
+    words = ng.pack_nibbles(qu)[0].astype(np.int64)
+    assert ((words < 0) == (np.arange(16) >= 8)).all()
+    assert words[15] == -(1 << 31) + (7 << 28)
 
 
-def test_pack_rejects_values_above_15():
-    qu = np.zeros((8, 4), dtype=np.uint8)
-    qu[5, 2] = 16
-    with pytest.raises(ValueError):
-        ng.pack_nibbles(qu)
+def _bad_pack_value():
+    qu = np.zeros((16, 3), np.uint8)
+    qu[9, 1] = 200
+    return lambda: ng.pack_nibbles(qu)
 
 
-def test_pack_rejects_k_not_divisible_by_8():
-    with pytest.raises(ValueError):
-        ng.pack_nibbles(np.zeros((12, 4), dtype=np.uint8))
+@pytest.mark.parametrize("call,needle", [
+    (lambda: ng.pack_nibbles(np.zeros((20, 2), np.uint8)), "divisible by 8"),
+    (_bad_pack_value(), "4 bits"),
+    (lambda: ng.unpack_nibbles(np.zeros((3, 2), np.int32), 32), "inconsistent"),
+    (lambda: quantize(torch.zeros(2, 3, 128)), "2-D"),
+    (lambda: quantize(torch.zeros(320, 4), group_size=128), "divisible by group_size"),
+    (lambda: quantize(torch.zeros(96, 4), group_size=12), "divisible by 8"),
+    (lambda: ng.quantize_device(torch.zeros(200, 4), group_size=64), "divisible by group_size"),
+])
+def test_invalid_inputs_raise_value_error(call, needle):
+    with pytest.raises(ValueError, match=needle):
+        call()
 
 
-def test_unpack_rejects_inconsistent_k():
-    packed = ng.pack_nibbles(np.zeros((16, 4), dtype=np.uint8))
-    with pytest.raises(ValueError):
-        ng.unpack_nibbles(packed, 24)
-
-
-@pytest.mark.parametrize("K,group_size", [(192, 128), (100, 64), (8, 128), (130, 128)])
-def test_quantize_rejects_k_not_divisible_by_group(K, group_size):
-    with pytest.raises(ValueError):
-        ng.quantize(torch.randn(K, 8), group_size=group_size)
-
-
-def test_quantize_rejects_non_2d_weight():
-    with pytest.raises(ValueError):
-        ng.quantize(torch.randn(4, 128, 8), group_size=128)
-
-
-def test_quantize_rejects_group_not_multiple_of_8():
-    with pytest.raises(ValueError):
-        ng.quantize(torch.randn(120, 8), group_size=12)
-
-
-def test_quantized_weight_bytes_and_to():
-    qw = ng.quantize(torch.randn(256, 16) * 0.02, group_size=128)
-    assert qw.qweight.shape == (32, 16) and qw.qweight.dtype == torch.int32
-    assert qw.scales.shape == (2, 16) and qw.scales.dtype == torch.float16
-    assert qw.weight_bytes == 32 * 16 * 4 + 2 * 16 * 2
-    qw2 = qw.to("cpu")
-    assert torch.equal(qw2.qweight, qw.qweight) and (qw2.K, qw2.N, qw2.group_size) == (256, 16, 128)
+def test_quantized_weight_accounting_and_move():
+    qw = quantize(torch.randn(384, 20) * 0.02, group_size=64)
+    assert qw.qweight.dtype == torch.int32 and tuple(qw.qweight.shape) == (48, 20)
+    assert qw.scales.dtype == torch.float16 and tuple(qw.scales.shape) == (6, 20)
+    assert qw.weight_bytes == 48 * 20 * 4 + 6 * 20 * 2
+    moved = qw.to("cpu")
+    assert (moved.K, moved.N, moved.group_size) == (384, 20, 64)
+    assert torch.equal(moved.qweight, qw.qweight) and torch.equal(moved.scales, qw.scales)
 
 
 def test_interleave_swiglu_column_order():
-    """Columns alternate gate/up in blocks of 32; split_swiglu inverts it."""
-    import torch
+    """Columns alternate gate/up in blocks of 16; split_swiglu inverts it."""
     from nibblegemm_amd.quant import QuantizedWeight, interleave_swiglu, split_swiglu
     K, N, g = 16, 64, 8
     gq = torch.arange(K // 8 * N, dtype=torch.int32).reshape(K // 8, N)
@@ -106,8 +106,10 @@ def test_interleave_swiglu_column_order():
     us = -gs
     qw = interleave_swiglu(QuantizedWeight(gq, gs, g, K, N), QuantizedWeight(uq, us, g, K, N))
     assert (qw.K, qw.N) == (K, 2 * N)
-    assert torch.equal(qw.qweight[:, :32], gq[:, :32]) and torch.equal(qw.qweight[:, 32:64], uq[:, :32])
-    assert torch.equal(qw.qweight[:, 64:96], gq[:, 32:]) and torch.equal(qw.scales[:, 96:], us[:, 32:])
+    for b in range(N // 16):
+        assert torch.equal(qw.qweight[:, 32 * b:32 * b + 16], gq[:, 16 * b:16 * b + 16])
+        assert torch.equal(qw.qweight[:, 32 * b + 16:32 * b + 32], uq[:, 16 * b:16 * b + 16])
+        assert torch.equal(qw.scales[:, 32 * b + 16:32 * b + 32], us[:, 16 * b:16 * b + 16])
     g_back, u_back = split_swiglu(qw.qweight)
     assert torch.equal(g_back, gq) and torch.equal(u_back, uq)
 
