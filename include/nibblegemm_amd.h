@@ -50,7 +50,7 @@
 extern "C" {
 #endif
 
-#define NIBBLE_ABI_VERSION 6
+#define NIBBLE_ABI_VERSION 7
 
 #if defined(__GNUC__) || defined(__clang__)
 #define NIBBLE_API __attribute__((visibility("default")))
@@ -80,8 +80,10 @@ NIBBLE_API const char* nibble_last_error(void);
  *                   2, 3 = the streaming kernel with one K split;
  *                   4 = the streaming kernel with split-K (default).
  * splits_override   0 = heuristic; else the number of K splits (version 4).
- * threads_override  0 = heuristic; else workgroup size in {64,128,256,512,1024}.
- * workspace         version 4 with more than one split needs
+ * threads_override  0 = heuristic; else workgroup size in {32,64,128,256,512,1024}
+ *                   (32, which the reference accepts, runs as one 64-lane wave).
+ * workspace         version 4 with more than one K split (K above 8192, or an
+ *                   explicit splits_override / threads_override) needs
  *                   nibble_gemv_workspace_bytes(...) bytes, 256-byte aligned.
  *                   Its first nibble_gemv_counter_bytes(...) bytes must be zero
  *                   before the first call; every call leaves them zero again.
@@ -94,6 +96,25 @@ NIBBLE_API int nibble_gemv_w4a16(const void* X, int64_t x_rows, int64_t x_cols,
                       int64_t group_size, int64_t version, int64_t splits_override,
                       int64_t threads_override, void* Y, void* workspace,
                       size_t workspace_bytes, void* stream);
+
+/*
+ * nibble_gemv_w4a16 that allocates nothing and takes no workspace.  No
+ * counterpart in the reference: it is for callers that cannot allocate (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Arguments, results and errors are nibble_gemv_w4a16's.  When
+ * the plan splits K across workgroups, the split counters and partials live
+ * in a static device array of the library (4 MiB per GPU, held until the
+ * process ends: 64 KiB of counters, zeroed when a GPU first uses it, then the
+ * fp32 partials [splits, M, N]); a request needing more than that fails with
+ * NIBBLE_ERR_UNSUPPORTED before anything is launched.  Every call on a GPU
+ * shares that GPU's array: calls that overlap on one GPU (other streams or
+ * threads) race and must be serialised by the caller.
+ */
+NIBBLE_API int nibble_gemv_w4a16_noalloc(const void* X, int64_t x_rows, int64_t x_cols,
+                      const void* Wq, int64_t wq_rows, int64_t wq_cols,
+                      const void* S, int64_t s_rows, int64_t s_cols,
+                      int64_t group_size, int64_t version, int64_t splits_override,
+                      int64_t threads_override, void* Y, void* stream);
 
 /* Bytes of workspace nibble_gemv_w4a16 needs for these arguments (0 if none,
  * and 0 for arguments the launcher would reject).  Pure host computation:
@@ -138,8 +159,8 @@ NIBBLE_API size_t nibble_gemm_counter_bytes(int64_t M, int64_t K, int64_t N, int
  *   epilogue 0  Y [M, N] = X @ W, as nibble_gemm_w4a16 writes it;
  *   epilogue 1  Y [M, N] = fp16(fp16(X @ W) + bias), bias fp16 [N] -- the
  *               same bits as the separate fp16 add;
- *   epilogue 2  W is [gate | up] interleaved in 32-column blocks (N a
- *               multiple of 64, nibblegemm_amd.quant.interleave_swiglu);
+ *   epilogue 2  W is [gate | up] interleaved in 16-column blocks (N a
+ *               multiple of 32, nibblegemm_amd.quant.interleave_swiglu);
  *               Y [M, N/2] = silu(G) * U with G, U and silu(G) rounded to
  *               fp16 as the unfused fp16 ops would.
  * A non-null `norm_weight` (fp16 [K], 16-byte aligned) fuses an RMSNorm

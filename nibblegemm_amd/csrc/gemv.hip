@@ -35,6 +35,7 @@
 // reference's v0/v1, :30-72): an on-device reference, not a fast path.
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 
 #include "nibble_common.h"
 #include "nibble_decode.h"
@@ -1006,15 +1007,24 @@ int launch_stream(const void* X, const void* Wq, const void* S, void* Y, int64_t
     if (!aligned(workspace, 256))
       return fail(NIBBLE_ERR_WORKSPACE, "workspace must be 256-byte aligned");
   }
+  void* counters = p.workspace_bytes > 0 ? workspace : nullptr;
+  void* partials =
+      p.workspace_bytes > 0 ? static_cast<char*>(workspace) + p.counter_bytes : nullptr;
+  return launch_stream_split(X, Wq, S, Y, M, K, N, G, p, counters, partials, stream, who,
+                             epilogue, bias, norm_w, norm_eps);
+}
+
+int launch_stream_split(const void* X, const void* Wq, const void* S, void* Y, int64_t M,
+                        int64_t K, int64_t N, int64_t G, const StreamPlan& p, void* counters,
+                        void* partials, hipStream_t stream, const char* who, int epilogue,
+                        const void* bias, const void* norm_w, float norm_eps) {
   GemvArgs a;
   a.X = static_cast<const _Float16*>(X);
   a.Wq = static_cast<const uint32_t*>(Wq);
   a.S = static_cast<const _Float16*>(S);
   a.Y = static_cast<_Float16*>(Y);
-  a.counters = p.splits > 1 ? static_cast<uint32_t*>(workspace) : nullptr;
-  a.partial = p.splits > 1
-                  ? reinterpret_cast<float*>(static_cast<char*>(workspace) + p.counter_bytes)
-                  : nullptr;
+  a.counters = p.splits > 1 ? static_cast<uint32_t*>(counters) : nullptr;
+  a.partial = p.splits > 1 ? static_cast<float*>(partials) : nullptr;
   a.M = static_cast<int>(M);
   a.K = static_cast<int>(K);
   a.N = static_cast<int>(N);
@@ -1285,5 +1295,99 @@ extern "C" int nibble_matmul_w4a16_fused(const void* X, int64_t x_rows, int64_t 
   rc = launch_stream(X, Wq, S, Y, M, K, N, group_size, p, workspace, workspace_bytes, stream,
                      "fused matmul kernel launch", static_cast<int>(epilogue), bias, norm_weight,
                      norm_eps);
+  return rc == NIBBLE_OK ? ok() : rc;
+}
+
+// ---------------------------------------------------------------------------
+// nibble_gemv_w4a16 without a caller workspace.  No counterpart in the
+// reference; for callers that cannot allocate (code under HIP graph capture,
+// tight serving loops, harnesses that forbid hipMalloc).  The split-K counters
+// and partials live in `scratch`, a file-scope device array: every GPU the
+// library runs on holds one copy until the process ends, and every call on a
+// GPU shares it, so calls that overlap on one GPU (concurrent streams or
+// threads) race.  The first kScratchCounterBytes are split counters: zeroed
+// by a fill kernel when a device first uses the array, and returned to zero
+// by every call; the fp32 partials follow them.  Requests whose plan needs
+// more are refused before anything is launched.
+
+namespace {
+constexpr size_t kScratchBytes = size_t(4) << 20;          // the whole array
+constexpr size_t kScratchCounterBytes = size_t(64) << 10;  // counter region at its start
+constexpr int kScratchDevices = 64;
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+std::mutex g_scratch_mutex;
+void* g_scratch_addr[kScratchDevices];  // this device's `scratch` (null until set up)
+
+__global__ void zero_words_kernel(uint32_t* __restrict__ p, uint32_t n) {
+  const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+// The device address of `scratch` on `device` (which must be current), set
+// up on the device's first use: the address comes from the runtime (in host
+// code the array's name only stands for the symbol), and the counter region
+// is cleared by a kernel on `stream`, ahead of the call that asked.
+int scratch_on(int device, hipStream_t stream, void** addr) {
+  if (device < 0 || device >= kScratchDevices)
+    return fail(NIBBLE_ERR_UNSUPPORTED, "no-alloc scratch: device %d out of range", device);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_addr[device] == nullptr) {
+    void* p = nullptr;
+    NIBBLE_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    const uint32_t words = static_cast<uint32_t>(kScratchCounterBytes / 4);
+    zero_words_kernel<<<(words + 255) / 256, 256, 0, stream>>>(static_cast<uint32_t*>(p), words);
+    NIBBLE_HIP(hipGetLastError());
+    g_scratch_addr[device] = p;
+  }
+  *addr = g_scratch_addr[device];
+  return NIBBLE_OK;
+}
+}  // namespace
+
+extern "C" int nibble_gemv_w4a16_noalloc(const void* X, int64_t x_rows, int64_t x_cols,
+                                         const void* Wq, int64_t wq_rows, int64_t wq_cols,
+                                         const void* S, int64_t s_rows, int64_t s_cols,
+                                         int64_t group_size, int64_t version,
+                                         int64_t splits_override, int64_t threads_override,
+                                         void* Y, void* stream_) {
+  int rc = validate_gemv(X, x_rows, x_cols, Wq, wq_rows, wq_cols, S, s_rows, s_cols, group_size,
+                         version, splits_override, threads_override, Y);
+  if (rc != NIBBLE_OK) return rc;
+  const int64_t M = x_rows, K = x_cols, N = wq_cols;
+  StreamPlan p;
+  const bool needs_workspace =
+      gemv_plannable(M, K, N, group_size, version) &&
+      gemv_plan(M, K, N, group_size, version, splits_override, threads_override, &p) ==
+          NIBBLE_OK &&
+      p.workspace_bytes > 0;
+  // Every other request (no split, or one the launcher rejects) is exactly
+  // nibble_gemv_w4a16 without a workspace.
+  if (!needs_workspace)
+    return nibble_gemv_w4a16(X, x_rows, x_cols, Wq, wq_rows, wq_cols, S, s_rows, s_cols,
+                             group_size, version, splits_override, threads_override, Y, nullptr,
+                             0, stream_);
+  const size_t partial_bytes = p.workspace_bytes - p.counter_bytes;
+  if (p.counter_bytes > kScratchCounterBytes ||
+      partial_bytes > kScratchBytes - kScratchCounterBytes)
+    return fail(NIBBLE_ERR_UNSUPPORTED,
+                "nibble_gemv_w4a16_noalloc: M=%lld K=%lld N=%lld splits into %d and needs %zu "
+                "bytes of split counters and %zu of partials; its static scratch holds %zu and "
+                "%zu (use nibble_gemv_w4a16 with a workspace)",
+                (long long)M, (long long)K, (long long)N, p.splits, p.counter_bytes,
+                partial_bytes, kScratchCounterBytes, kScratchBytes - kScratchCounterBytes);
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  DeviceGuard guard;
+  int dev = 0;
+  NIBBLE_HIP(guard.enter(stream, &dev));
+  void* base = nullptr;
+  rc = scratch_on(dev, stream, &base);
+  if (rc != NIBBLE_OK) return rc;
+  rc = launch_stream_split(X, Wq, S, Y, M, K, N, group_size, p, base,
+                           static_cast<char*>(base) + kScratchCounterBytes, stream,
+                           "gemv (no-alloc) kernel launch");
   return rc == NIBBLE_OK ? ok() : rc;
 }

@@ -71,6 +71,15 @@ int launch_stream(const void* X, const void* Wq, const void* S, void* Y, int64_t
                   const void* bias = nullptr, const void* norm_w = nullptr,
                   float norm_eps = 0.0f);
 
+// launch_stream with the split-K workspace given as its two parts: the
+// counter region (zero on entry, left zero) and the fp32 partials.  The plan
+// must fit whatever those point at; no checks are made here.
+int launch_stream_split(const void* X, const void* Wq, const void* S, void* Y, int64_t M,
+                        int64_t K, int64_t N, int64_t G, const StreamPlan& p, void* counters,
+                        void* partials, hipStream_t stream, const char* who, int epilogue = 0,
+                        const void* bias = nullptr, const void* norm_w = nullptr,
+                        float norm_eps = 0.0f);
+
 // Largest K the fused-RMSNorm prologue takes (8 chunks of 256 x 8 columns).
 constexpr int kNormMaxK = 16384;
 constexpr int kNormMaxM = 8;

@@ -194,6 +194,27 @@ def test_dequant_rejections(args, needle):
     assert needle in ext.last_error()
 
 
+def test_noalloc_gemv_rejects_plans_beyond_its_scratch():
+    """nibble_gemv_w4a16_noalloc refuses, before any HIP call, a split plan
+    whose partials exceed its static scratch (4 MiB less 64 KiB of counters),
+    with a message that names the limit; validation errors are
+    nibble_gemv_w4a16's."""
+    lib = ctypes.CDLL(_native.LIBRARY_PATH)
+    fn = lib.nibble_gemv_w4a16_noalloc
+    fn.restype = ctypes.c_int
+    fn.argtypes = ([ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64] * 3
+                   + [ctypes.c_int64] * 4 + [ctypes.c_void_p, ctypes.c_void_p])
+    lib.nibble_last_error.restype = ctypes.c_char_p
+    # 16 splits x 8 rows x 8192 columns of fp32 partials = 4 MiB
+    rc = fn(P, 8, 4096, P, 512, 8192, P, 32, 8192, 128, 4, 16, 0, P, None)
+    assert rc == 2 and b"static scratch" in lib.nibble_last_error()
+    # (a plan that fits would launch, which needs a GPU: tests/test_zz_no_alloc.py)
+    rc = fn(P, 9, 4096, P, 512, 8192, P, 32, 8192, 128, 4, 0, 0, P, None)
+    assert rc == 2 and b"M <= 8" in lib.nibble_last_error()
+    rc = fn(P, 1, 4096, P, 511, 8192, P, 32, 8192, 128, 4, 0, 0, P, None)
+    assert rc == INVALID and b"packed weight rows" in lib.nibble_last_error()
+
+
 def test_binding_rejects_wrong_arity():
     ext = ng.extension()
     with pytest.raises(TypeError):
