@@ -14,9 +14,14 @@ one ``nibblegemm_amd.gemv`` call (M=1) over one batch of synthetic inputs
   of the packed weights and scales from a rotation spanning >= 1 GiB, so no
   step is served from the 256 MiB Infinity Cache or the L2s.
 * ``--warmup W`` eager steps run untimed, then the K timed steps are captured
-  into one HIP graph (capture executes nothing), replayed once untimed, and
-  replayed once timed between events on the replay stream, bracketed by
-  ``torch.cuda.synchronize()``.  ``ms_per_step`` = elapsed / K.
+  into one HIP graph (capture executes nothing), replayed untimed for ~0.25 s
+  so the timed replay starts at the loaded shader clock, and replayed once
+  timed between events on the replay stream, bracketed by
+  ``torch.cuda.synchronize()``.  ``ms_per_step`` = elapsed / K.  The default
+  K = 5000 makes the timed region ~36 ms, long enough for the sysfs clock /
+  power sampler (10 ms period) to see it: ``clock`` holds the shader clock
+  at its start and end, min / mean / max over it, and the reference's
+  ``throttled`` test (the clock moving by more than 5%).
 * ``value`` = algorithmic bytes per step (K*N/2 + (K/128)*N*2 + 2K + 2N) /
   ms_per_step, in GB/s.  ``roofline`` prices the same figure against MI355X's
   8 TB/s; ``cpu_baseline`` times the CPU oracle (dequantize + fp32 matmul,
@@ -44,14 +49,29 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(target_s: float) -> dict:
-    """The reference's CPU path (dequantize + fp32 matmul), via the CPU oracle."""
+    """The reference's CPU path (dequantize + fp32 matmul), via the CPU oracle,
+    on this host's cores: as many threads as the job's CPU share allows (the
+    affinity mask, capped by OMP_NUM_THREADS where the box sets it)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O  # noqa: PLC0415  (cpu_baseline leg only)
 
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(os.cpu_count() or 1, 16)
+    affinity = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    omp = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    threads = min(affinity, omp) if omp > 0 else affinity
     one = O.time_reference_path(M, K, N, G, reps=1, threads=threads)
-    reps = int(max(3, min(60, target_s / max(one["total_s"], 1e-3))))
+    reps = int(max(5, min(60, target_s / max(one["total_s"], 1e-3))))
     r = O.time_reference_path(M, K, N, G, reps=reps, threads=threads)
     nbytes = K * N // 2 + (K // G) * N * 2 + M * K * 2 + M * N * 2
     return {
@@ -64,14 +84,21 @@ def cpu_baseline(target_s: float) -> dict:
                    f"{r['dequant_s'] * 1e3:.1f} ms + matmul {r['matmul_s'] * 1e3:.1f} ms "
                    f"= {r['total_s'] * 1e3:.1f} ms per step"),
         "ms_per_step": round(r["total_s"] * 1e3, 3),
+        "dequant_ms": round(r["dequant_s"] * 1e3, 3),
+        "matmul_ms": round(r["matmul_s"] * 1e3, 3),
+        "threads_used": r["threads"],
+        "host_cpu_count": os.cpu_count(),
+        "affinity_cores": affinity,
+        "omp_num_threads": omp or None,
+        "cpu_model": _cpu_model(),
     }
 
 
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=5000)
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--skip-extras", action="store_true",
@@ -122,17 +149,11 @@ def main() -> int:
     runner = H.GraphRunner(lambda i: ng.gemv(X, variants[i]), reps=steps, warmup=0)
     runner.graph.replay()  # untimed: first replay uploads the graph
     torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
+    ms_per_step, clocks = runner.time_once(warm_s=0.25)
     torch.cuda.synchronize()
-    start.record()
-    runner.graph.replay()
-    end.record()
-    torch.cuda.synchronize()
-    ms_per_step = start.elapsed_time(end) / steps
     gbps = H.achieved_gbps(nbytes, ms_per_step)
     log(f"gemv M=1 {K}x{N}: {ms_per_step * 1e3:.2f} us/step, {gbps:.0f} GB/s "
-        f"({100 * gbps / H.HBM_PEAK_GBPS:.1f}% of 8 TB/s)")
+        f"({100 * gbps / H.HBM_PEAK_GBPS:.1f}% of 8 TB/s); clock {clocks}")
 
     extras = {}
     if not args.skip_extras:
@@ -141,6 +162,9 @@ def main() -> int:
         copy = H.measured_copy_gbps()
         extras["copy_gbps"] = round(copy, 1)
         extras["pct_of_copy_bw"] = round(100 * gbps / copy, 1)
+        read = H.measured_read_gbps()
+        extras.update(read)
+        extras["pct_of_read_bw"] = round(100 * gbps / read["read_gbps"], 1)
         torch.backends.cuda.matmul.allow_tf32 = False
         w16 = (torch.randn((K, N), generator=gen) * 0.02).to(torch.float16).to(dev)
         rot16 = H.Rotation(w16)
@@ -150,8 +174,8 @@ def main() -> int:
         fp16_bytes = H.total_bytes(M, K, N, G, 16)
         extras["byte_ratio_ceiling"] = round(fp16_bytes / nbytes, 3)
         del rot16, w16
-        log(f"copy {copy:.0f} GB/s; hipBLASLt fp16 {fp16.median_ms * 1e3:.2f} us; "
-            f"eager {eager.median_ms * 1e3:.2f} us/call")
+        log(f"copy {copy:.0f} GB/s; 2 GiB read {read['read_gbps']:.0f} GB/s; hipBLASLt fp16 "
+            f"{fp16.median_ms * 1e3:.2f} us; eager {eager.median_ms * 1e3:.2f} us/call")
 
     decode = None
     if not args.skip_decode_step:
@@ -216,6 +240,7 @@ def main() -> int:
         "config": {"workload": f"gemv M={M} K={K} N={N} g={G} (BASELINE configs[1] headline shape)",
                    "M": M, "K": K, "N": N, "group_size": G},
         "gemv_us": round(ms_per_step * 1e3, 3),
+        "clock": clocks,
         "pct_hbm_peak": round(100 * gbps / H.HBM_PEAK_GBPS, 2),
         "roofline": roofline,
         "cpu_baseline": cpu,

@@ -253,6 +253,18 @@ NIBBLE_API int nibble_gptq_group_f32(const void* W, int64_t ldw, int64_t N, int6
                                      const void* U, int64_t ldu, void* Q, int64_t ldq, void* E,
                                      void* scales, void* stream);
 
+/*
+ * Measurement: a streaming read of `bytes` (a positive multiple of 16) from
+ * `src` (16-byte aligned) by `workgroups` workgroups of 256 threads, each
+ * folding its contiguous slice into one word of `sink` (4 bytes per
+ * workgroup, nibble_read_probe_sink_bytes(...)).  The achievable HBM read
+ * bandwidth the decode GEMV is compared with.  No counterpart in the
+ * reference, whose harness times a device copy (bench/harness.py:189-200).
+ */
+NIBBLE_API int nibble_read_probe(const void* src, size_t bytes, int64_t workgroups, void* sink,
+                                 void* stream);
+NIBBLE_API size_t nibble_read_probe_sink_bytes(size_t bytes, int64_t workgroups);
+
 #ifdef __cplusplus
 }
 #endif

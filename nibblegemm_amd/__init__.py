@@ -6,10 +6,11 @@ Drop-in for the Python surface of arvindcr4/nibblegemm
 kernel entry points, the batch-size dispatch and ``QuantLinear``.  The kernels
 are hand-written HIP behind the C ABI in ``include/nibblegemm_amd.h``.
 
-GPTQ (``gptq_quantize``, ``quantize_model_gptq``, ``HessianAccumulator``,
-``find_decoder_blocks``) and the Triton baseline of the reference are not part
-of this package.  Symmetric GPTQ / AWQ 4-bit checkpoints are ingested by
-:mod:`nibblegemm_amd.convert`.
+The reference's GPTQ quantiser is here too (``gptq_quantize``,
+``quantize_model_gptq``, ``HessianAccumulator``, ``find_decoder_blocks``, in
+:mod:`nibblegemm_amd.gptq`, its column loop a kernel of this library);
+symmetric GPTQ / AWQ 4-bit checkpoints are converted by
+:mod:`nibblegemm_amd.convert`.  The reference's Triton baseline is not.
 """
 
 from . import convert, gptq

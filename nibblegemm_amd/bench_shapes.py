@@ -25,12 +25,15 @@ from __future__ import annotations
 
 import argparse
 import json
+import os
+import statistics
 import sys
+import time
 
 import torch
 
 from . import harness as H
-from . import ops
+from . import ops, quant
 from .quant import QuantizedWeight, pack_nibbles
 
 DECODE_SHAPES = [(4096, 4096), (4096, 14336), (14336, 4096), (8192, 8192), (4096, 1024)]
@@ -67,8 +70,57 @@ def _emit(rows, row):
     print(json.dumps(row), flush=True)
 
 
+def _clock(t: "H.Timing") -> dict:
+    """The shader clock over a timing's window (mean MHz) and the reference's
+    5% throttle flag."""
+    c = t.clocks
+    return {"clock_mhz": c.get("clock_mean_mhz"), "throttled": c.get("throttled")}
+
+
+def _host_median_ms(fn, reps: int) -> float:
+    fn()  # warm-up
+    samples = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        samples.append((time.perf_counter() - t0) * 1e3)
+    return statistics.median(samples)
+
+
+def cpu_facts() -> dict:
+    """Threads the host leg uses and what it runs on."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as fh:
+            model = next((ln.split(":", 1)[1].strip() for ln in fh if ln.startswith("model name")),
+                         model)
+    except OSError:
+        pass
+    # The host dequantize is numpy elementwise work (one thread); the fp32
+    # matmul is torch's (its intra-op thread count).
+    return {"cpu_dequant_threads": 1, "cpu_matmul_threads": torch.get_num_threads(),
+            "host_cpu_count": os.cpu_count(), "cpu_model": model}
+
+
+def cpu_reference_ms(qw: QuantizedWeight, X: torch.Tensor, reps: int = 5) -> dict:
+    """The reference's CPU path on this host (python/nibblegemm/quant.py:199-215,
+    in this package's restatement): ``dequantize`` (unpack, scale, fp16), then
+    the fp32 matmul rounded to fp16; median of ``reps`` after one warm-up,
+    each half separately."""
+    qw_cpu = qw.to("cpu")
+    x = X.cpu()
+    dq = _host_median_ms(lambda: quant.dequantize(qw_cpu), reps)
+    W = quant.dequantize(qw_cpu).float()
+    mm = _host_median_ms(lambda: (x.float() @ W).to(torch.float16), reps)
+    return {"cpu_dequant_ms": round(dq, 2), "cpu_matmul_ms": round(mm, 2),
+            "cpu_ms": round(dq + mm, 2)}
+
+
 def decode(args, rows):
     copy = H.measured_copy_gbps()
+    read = H.measured_read_gbps()["read_gbps"]
+    print(json.dumps({"bench": "decode-setup", "copy_gbps": round(copy, 1), "read_gbps": read,
+                      **cpu_facts()}), flush=True)
     for K, N in DECODE_SHAPES:
         qws, gen = _weights(K, N, args.group_size, seed=K + N)
         w16 = _fp16_baseline(qws[0])
@@ -80,14 +132,18 @@ def decode(args, rows):
             d = H.bench_graph(lambda i: torch.mm(X, ops.dequant(qws[i])), reps=8, trials=args.trials)
             nb = H.total_bytes(M, K, N, args.group_size, 4)
             gbps = H.achieved_gbps(nb, t.median_ms)
-            _emit(rows, {"bench": "decode", "M": M, "K": K, "N": N, "impl": "gemv v4",
-                         "us": round(t.median_ms * 1e3, 2), "GB/s": round(gbps),
-                         "%8TB/s": round(100 * gbps / H.HBM_PEAK_GBPS, 1),
-                         "%copy": round(100 * gbps / copy, 1),
-                         "hipblaslt_fp16_us": round(f.median_ms * 1e3, 2),
-                         "vs_fp16": round(f.median_ms / t.median_ms, 2),
-                         "dequant+fp16_us": round(d.median_ms * 1e3, 2),
-                         "max_err_rms": float(f"{err:.2e}")})
+            row = {"bench": "decode", "M": M, "K": K, "N": N, "impl": "gemv v4",
+                   "us": round(t.median_ms * 1e3, 2), "GB/s": round(gbps),
+                   "%8TB/s": round(100 * gbps / H.HBM_PEAK_GBPS, 1),
+                   "%copy": round(100 * gbps / copy, 1), "%read": round(100 * gbps / read, 1),
+                   "hipblaslt_fp16_us": round(f.median_ms * 1e3, 2),
+                   "vs_fp16": round(f.median_ms / t.median_ms, 2),
+                   "dequant+fp16_us": round(d.median_ms * 1e3, 2),
+                   "max_err_rms": float(f"{err:.2e}"), **_clock(t)}
+            if not args.no_cpu:
+                row.update(cpu_reference_ms(qws[0], X))
+                row["vs_cpu"] = round(row["cpu_ms"] / (t.median_ms), 0)
+            _emit(rows, row)
         del qws, w16
         torch.cuda.empty_cache()
 
@@ -111,7 +167,7 @@ def prefill_points(K: int, N: int, Ms, group_size: int = 128, trials: int = 10,
                         "%2.5PF": round(100 * tf / H.FP16_MFMA_PEAK_TFLOPS, 1),
                         "hipblaslt_fp16_us": round(f.median_ms * 1e3, 2),
                         "vs_fp16": round(f.median_ms / t.median_ms, 2),
-                        "max_err_rms": float(f"{err:.2e}")})
+                        "max_err_rms": float(f"{err:.2e}"), **_clock(t)})
     del qws, w16
     torch.cuda.empty_cache()
     return out
@@ -126,15 +182,22 @@ def prefill(args, rows):
 
 def dequant(args, rows):
     copy = H.measured_copy_gbps()
+    print(json.dumps({"bench": "dequant-setup", "copy_gbps": round(copy, 1), **cpu_facts()}),
+          flush=True)
     for K, N in DECODE_SHAPES:
         qws, _ = _weights(K, N, args.group_size, seed=K + N)
         t = H.bench_graph(lambda i: ops.dequant(qws[i]), reps=16, trials=args.trials)
         nb = H.dequant_bytes(K, N, args.group_size)
         gbps = H.achieved_gbps(nb, t.median_ms)
-        _emit(rows, {"bench": "dequant", "K": K, "N": N, "impl": "dequant fast",
-                     "us": round(t.median_ms * 1e3, 2), "GB/s": round(gbps),
-                     "%8TB/s": round(100 * gbps / H.HBM_PEAK_GBPS, 1),
-                     "%copy": round(100 * gbps / copy, 1)})
+        row = {"bench": "dequant", "K": K, "N": N, "impl": "dequant fast",
+               "us": round(t.median_ms * 1e3, 2), "GB/s": round(gbps),
+               "%8TB/s": round(100 * gbps / H.HBM_PEAK_GBPS, 1),
+               "%copy": round(100 * gbps / copy, 1), **_clock(t)}
+        if not args.no_cpu:
+            qw_cpu = qws[0].to("cpu")
+            row["cpu_dequant_ms"] = round(_host_median_ms(lambda: quant.dequantize(qw_cpu), 5), 2)
+            row["vs_cpu"] = round(row["cpu_dequant_ms"] / t.median_ms, 0)
+        _emit(rows, row)
         del qws
         torch.cuda.empty_cache()
 
@@ -226,6 +289,8 @@ def main(argv=None) -> int:
     ap.add_argument("--group-size", type=int, default=128)
     ap.add_argument("--trials", type=int, default=10)
     ap.add_argument("--markdown", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true",
+                    help="skip the host (CPU) timing of the reference path in decode / dequant")
     args = ap.parse_args(argv)
     if not torch.cuda.is_available():
         print("bench_shapes needs a GPU", file=sys.stderr)

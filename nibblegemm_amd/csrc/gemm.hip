@@ -328,6 +328,8 @@ gemm_tile_kernel(TileArgs args) {
         if (gm < M) store_coherent(part + static_cast<size_t>(gm) * N + gn, acc[i][j][r]);
       }
     }
+  // Last-arriver exchange; relies on gfx950 hardware ordering: see
+  // "HARDWARE ASSUMPTION" in nibble_decode.h.
   wait_vm_stores();
   __syncthreads();
   const int tile = blockIdx.y * gridDim.x + blockIdx.x;
@@ -401,6 +403,8 @@ __device__ __forceinline__ void pc_epilogue(const f16_t (&acc)[TM][TN], const Ti
         }
       }
   }
+  // Last-arriver exchange; relies on gfx950 hardware ordering: see
+  // "HARDWARE ASSUMPTION" in nibble_decode.h.
   wait_vm_stores();
   __syncthreads();
   const int tile = blockIdx.y * gridDim.x + blockIdx.x;

@@ -391,6 +391,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs a) {
   // The partials were written with device-coherent stores; waiting for them
   // to complete orders them before the counter update without the whole-L2
   // write-back / invalidate an agent-scope fence costs on a multi-XCD device.
+  // Relies on gfx950 hardware ordering: see "HARDWARE ASSUMPTION" in
+  // nibble_decode.h.
   wait_vm_stores();
   __syncthreads();
   uint32_t* counter = a.counters + blockIdx.z * gridDim.x + strip;

@@ -260,6 +260,8 @@ __global__ __launch_bounds__(kGlueThreads) void attention_decode_kernel(AttnArgs
   }
   if (direct) return;
 
+  // Last-arriver exchange; relies on gfx950 hardware ordering: see
+  // "HARDWARE ASSUMPTION" in nibble_decode.h.
   wait_vm_stores();
   __syncthreads();
   if (tid == 0) {

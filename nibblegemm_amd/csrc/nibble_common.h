@@ -10,6 +10,13 @@
 
 #include "../../include/nibblegemm_amd.h"
 
+// Every kernel of this library is written for gfx950 (CDNA4) alone: MFMA
+// shapes, LDS size, the 8-XCD workgroup mapping and the cross-workgroup
+// ordering described in nibble_decode.h ("HARDWARE ASSUMPTION") all assume it.
+#if defined(__HIP_DEVICE_COMPILE__) && !defined(__gfx950__)
+#error "nibblegemm_amd is built for gfx950 only"
+#endif
+
 namespace nibble {
 
 // Records a printf-style message as this thread's last error and returns `code`.

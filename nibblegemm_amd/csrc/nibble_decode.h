@@ -133,6 +133,29 @@ __device__ __forceinline__ int nibble_value(uint32_t q, int k) {
   return static_cast<int>((q >> (4 * slot)) & 0xFu) - 8;
 }
 
+// Cross-workgroup exchange ("last arriver reduces").  Every split-K reduction
+// in this library (gemv.hip split kernel, gemm.hip split-K epilogues,
+// glue.hip attention splits) follows one protocol:
+//   1. each workgroup writes its partials with store_coherent();
+//   2. wait_vm_stores(), then __syncthreads();
+//   3. one thread does a relaxed agent-scope fetch_add on the tile's counter;
+//      the workgroup that sees count == splits - 1 is the last;
+//   4. the last workgroup reads every partial with load_coherent(), writes
+//      the output and stores the counter back to zero.
+// HARDWARE ASSUMPTION (gfx950 / CDNA4; not true of the C++ memory model in
+// general): the ordering between 1 and 3 comes from the hardware, not from a
+// release/acquire pair.  On gfx9 a vector store counts in vmcnt until it has
+// been acknowledged by the memory side, an agent-scope store is written
+// through past the issuing XCD's L2 (and an agent-scope load misses in it),
+// and the counter atomic is performed at the device's coherence point.  So
+// once step 2 has waited vmcnt to zero, every partial is visible to an
+// agent-scope load from any XCD before the counter can show this workgroup's
+// increment.  This replaces the agent-scope release/acquire fences, which on
+// a multi-XCD device write back and invalidate the whole L2 (measured at
+// several microseconds per decode launch).  A port to another target has to
+// re-establish the ordering with __ATOMIC_RELEASE / __ATOMIC_ACQUIRE on the
+// counter; the #error in nibble_common.h stops a build for any other target.
+
 // Device-coherent (agent-scope, relaxed) accesses for data exchanged between
 // workgroups of one launch.  On a multi-XCD device each XCD has its own L2;
 // these bypass its non-coherent copy instead of writing back / invalidating

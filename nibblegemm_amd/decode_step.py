@@ -109,6 +109,10 @@ class DecodeStep:
         for x, qw, fn in self.calls:
             fn(x, qw)
 
+    def outputs(self) -> List[torch.Tensor]:
+        """The step with every call's output kept, in call order."""
+        return [fn(x, qw) for x, qw, fn in self.calls]
+
     @property
     def launches(self) -> int:
         return len(self.calls)
@@ -193,6 +197,8 @@ def measure_glue(layers: List[Dict[str, QuantizedWeight]], pos: int = 1023, tria
         "tok_s": round(1000.0 / eager.median_ms, 1),
         "graph_tok_s": round(1000.0 / graph.median_ms, 1),
         "graph_gbps": round(nbytes / (graph.median_ms * 1e-3) / 1e9, 1),
+        "clock_mhz": graph.clocks.get("clock_mean_mhz"),
+        "throttled": graph.clocks.get("throttled"),
     }
 
 
@@ -211,6 +217,8 @@ def measure(layers: List[Dict[str, QuantizedWeight]], trials: int = 10, warmup: 
         "tok_s": round(1000.0 / eager.median_ms, 1),
         "graph_tok_s": round(1000.0 / graph.median_ms, 1),
         "graph_gbps": round(nbytes / (graph.median_ms * 1e-3) / 1e9, 1),
+        "clock_mhz": graph.clocks.get("clock_mean_mhz"),
+        "throttled": graph.clocks.get("throttled"),
     }
 
 

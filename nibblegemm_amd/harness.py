@@ -18,9 +18,15 @@ MI355X memory hierarchy:
 """
 from __future__ import annotations
 
+import glob
+import math
+import os
+import re
 import statistics
+import threading
+import time
 from dataclasses import dataclass, field
-from typing import Callable, List, Optional, Sequence
+from typing import Callable, Dict, List, Optional, Sequence
 
 import torch
 
@@ -37,6 +43,135 @@ def device_summary() -> str:
             f"{p.total_memory / 2**30:.0f} GiB HBM")
 
 
+# --------------------------------------------------------------------------
+# Clock, power and temperature of the GPU (the reference samples the SM clock
+# around each timing with nvidia-smi, bench/harness.py:49-57, :69-89).  Here
+# the amdgpu driver's sysfs files of torch device 0 are read directly -- no
+# helper process -- by a thread that polls them through the timed window, so
+# a clock drop during the run is seen, not only the idle clock before/after.
+# --------------------------------------------------------------------------
+class GpuTelemetry:
+    """Readings of one GPU's amdgpu sysfs node (None where a file is
+    missing or unreadable): shader and memory clock in MHz (the active DPM
+    level, or the hwmon frequency), board power in W, edge/hotspot
+    temperature in C."""
+
+    def __init__(self, device: int = 0):
+        self.path = self._find(device)
+        hw = glob.glob(os.path.join(self.path, "hwmon", "hwmon*")) if self.path else []
+        self.hwmon = hw[0] if hw else None
+
+    @staticmethod
+    def _find(device: int) -> Optional[str]:
+        try:
+            p = torch.cuda.get_device_properties(device)
+            addr = f"{p.pci_domain_id:04x}:{p.pci_bus_id:02x}:{p.pci_device_id:02x}.0"
+        except Exception:  # noqa: BLE001 -- no GPU / older torch: no telemetry
+            return None
+        path = os.path.join("/sys/bus/pci/devices", addr)
+        return path if os.path.isdir(path) else None
+
+    @staticmethod
+    def _read(path: Optional[str]) -> Optional[str]:
+        if not path:
+            return None
+        try:
+            with open(path) as fh:
+                return fh.read()
+        except OSError:
+            return None
+
+    def _dpm_mhz(self, name: str) -> Optional[float]:
+        text = self._read(os.path.join(self.path, name) if self.path else None)
+        if not text:
+            return None
+        for line in text.splitlines():
+            if line.rstrip().endswith("*"):
+                m = re.search(r"(\d+)\s*[Mm]hz", line)
+                if m:
+                    return float(m.group(1))
+        return None
+
+    def _hwmon(self, name: str, scale: float) -> Optional[float]:
+        text = self._read(os.path.join(self.hwmon, name) if self.hwmon else None)
+        try:
+            return float(text) * scale if text else None
+        except ValueError:
+            return None
+
+    def sample(self) -> Dict[str, Optional[float]]:
+        sclk = self._dpm_mhz("pp_dpm_sclk")
+        if sclk is None:
+            sclk = self._hwmon("freq1_input", 1e-6)
+        power = self._hwmon("power1_average", 1e-6)
+        if power is None:
+            power = self._hwmon("power1_input", 1e-6)
+        return {"sclk_mhz": sclk, "mclk_mhz": self._dpm_mhz("pp_dpm_mclk"), "power_w": power,
+                "temp_c": self._hwmon("temp1_input", 1e-3),
+                "temp_hotspot_c": self._hwmon("temp2_input", 1e-3)}
+
+
+_telemetry: Optional[GpuTelemetry] = None
+
+
+def telemetry() -> GpuTelemetry:
+    global _telemetry
+    if _telemetry is None:
+        _telemetry = GpuTelemetry(0)
+    return _telemetry
+
+
+class ClockMonitor:
+    """Samples :class:`GpuTelemetry` every ``period_s`` from a thread between
+    ``start()`` and ``stop()``; ``summary()`` gives the first and last shader
+    clock, its min / mean / max over the window, mean power and peak
+    temperature.  ``throttled`` follows the reference's test -- the clock
+    moving by more than 5% -- applied to the whole window."""
+
+    def __init__(self, period_s: float = 0.01):
+        self.period = period_s
+        self.samples: List[Dict[str, Optional[float]]] = []
+        self._stop = threading.Event()
+        self._thread: Optional[threading.Thread] = None
+
+    def start(self) -> "ClockMonitor":
+        tel = telemetry()
+        self.samples = [tel.sample()]
+
+        def run():
+            while not self._stop.wait(self.period):
+                self.samples.append(tel.sample())
+
+        self._thread = threading.Thread(target=run, daemon=True)
+        self._thread.start()
+        return self
+
+    def stop(self) -> Dict[str, object]:
+        self._stop.set()
+        if self._thread is not None:
+            self._thread.join()
+        self.samples.append(telemetry().sample())
+        return self.summary()
+
+    def summary(self) -> Dict[str, object]:
+        def col(key):
+            return [s[key] for s in self.samples if s.get(key) is not None]
+
+        sclk, power, temp = col("sclk_mhz"), col("power_w"), col("temp_hotspot_c") or col("temp_c")
+        out: Dict[str, object] = {"telemetry_samples": len(self.samples)}
+        if sclk:
+            out.update(clock_before_mhz=sclk[0], clock_after_mhz=sclk[-1], clock_min_mhz=min(sclk),
+                       clock_mean_mhz=round(statistics.mean(sclk), 1), clock_max_mhz=max(sclk),
+                       throttled=(max(sclk) - min(sclk)) > 0.05 * max(sclk))
+        if col("mclk_mhz"):
+            out["mclk_mhz"] = statistics.median(col("mclk_mhz"))
+        if power:
+            out["power_mean_w"] = round(statistics.mean(power), 1)
+        if temp:
+            out["temp_max_c"] = max(temp)
+        return out
+
+
 @dataclass
 class Timing:
     median_ms: float
@@ -45,19 +180,25 @@ class Timing:
     trials: int
     reps: int
     samples: Sequence[float] = field(default_factory=list, repr=False)
+    clocks: Dict[str, object] = field(default_factory=dict)
 
     @property
     def spread_pct(self) -> float:
         return 100.0 * (self.p95_ms - self.p05_ms) / self.median_ms if self.median_ms else 0.0
 
+    @property
+    def throttled(self) -> bool:
+        return bool(self.clocks.get("throttled", False))
 
-def _summarise(samples: List[float], trials: int, reps: int) -> Timing:
+
+def _summarise(samples: List[float], trials: int, reps: int,
+               clocks: Optional[Dict[str, object]] = None) -> Timing:
     samples = sorted(samples)
     return Timing(
         median_ms=statistics.median(samples),
         p05_ms=samples[max(0, int(0.05 * len(samples)) - 1)],
         p95_ms=samples[min(len(samples) - 1, int(0.95 * len(samples)))],
-        trials=trials, reps=reps, samples=samples,
+        trials=trials, reps=reps, samples=samples, clocks=clocks or {},
     )
 
 
@@ -70,6 +211,7 @@ def bench(fn: Callable[[int], object], *, reps: int = 32, trials: int = 20,
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     samples = []
+    mon = ClockMonitor().start()
     for _ in range(trials):
         torch.cuda.synchronize()
         start.record()
@@ -78,7 +220,7 @@ def bench(fn: Callable[[int], object], *, reps: int = 32, trials: int = 20,
         end.record()
         torch.cuda.synchronize()
         samples.append(start.elapsed_time(end) / reps)
-    return _summarise(samples, trials, reps)
+    return _summarise(samples, trials, reps, mon.stop())
 
 
 class GraphRunner:
@@ -103,19 +245,52 @@ class GraphRunner:
         torch.cuda.synchronize()
         self.reps = reps
 
-    def time(self, trials: int = 20) -> Timing:
+    def warm(self, seconds: float) -> None:
+        """Keeps the GPU busy with untimed replays for about ``seconds`` and
+        returns while the last of them is still running, so what is queued
+        next starts at the loaded clock.  MI355X drops its shader clock within
+        ~100 ms of going idle and takes a comparable time to raise it again; a
+        timing that starts from idle runs its first milliseconds slow."""
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
-        self.graph.replay()  # warm
-        torch.cuda.synchronize()
+        start.record()
+        self.graph.replay()
+        end.record()
+        end.synchronize()
+        per = max(start.elapsed_time(end) / 1e3, 1e-6)
+        n = max(1, math.ceil(seconds / per))
+        for _ in range(n):
+            self.graph.replay()
+        time.sleep(max(0.0, (n - 1) * per))
+
+    def time_once(self, warm_s: float = 0.25):
+        """One timed replay after :meth:`warm`; returns (ms per call, clock
+        summary).  The clock monitor starts while the GPU is still busy with
+        the warm-up, so its first sample is the clock the timed replay starts
+        at and its last the clock it ends at."""
+        self.warm(warm_s)
+        mon = ClockMonitor().start()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        self.graph.replay()
+        end.record()
+        end.synchronize()
+        return start.elapsed_time(end) / self.reps, mon.stop()
+
+    def time(self, trials: int = 20, warm_s: float = 0.05) -> Timing:
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        self.warm(warm_s)
         samples = []
+        mon = ClockMonitor().start()
         for _ in range(trials):
             start.record()
             self.graph.replay()
             end.record()
             end.synchronize()
             samples.append(start.elapsed_time(end) / self.reps)
-        return _summarise(samples, trials, self.reps)
+        return _summarise(samples, trials, self.reps, mon.stop())
 
 
 def bench_graph(fn: Callable[[int], object], *, reps: int = 32, trials: int = 20,
@@ -134,9 +309,9 @@ def bench_graph_pair(fn_a: Callable[[int], object], fn_b: Callable[[int], object
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     for r in runners:
-        r.graph.replay()  # warm
-    torch.cuda.synchronize()
+        r.warm(0.025)
     samples = ([], [])
+    mon = ClockMonitor().start()
     for _ in range(trials):
         for r, out in zip(runners, samples):
             start.record()
@@ -144,7 +319,8 @@ def bench_graph_pair(fn_a: Callable[[int], object], fn_b: Callable[[int], object
             end.record()
             end.synchronize()
             out.append(start.elapsed_time(end) / reps)
-    return tuple(_summarise(s, trials, reps) for s in samples)
+    clocks = mon.stop()
+    return tuple(_summarise(s, trials, reps, clocks) for s in samples)
 
 
 def measured_copy_gbps(size_bytes: int = 2 << 30) -> float:
@@ -157,6 +333,49 @@ def measured_copy_gbps(size_bytes: int = 2 << 30) -> float:
     del src, dst
     torch.cuda.empty_cache()
     return (2 * n * 2) / (t.median_ms * 1e-3) / 1e9
+
+
+_probe = None
+
+
+def _read_probe_fn():
+    global _probe
+    if _probe is None:
+        import ctypes  # noqa: PLC0415
+
+        from . import _native  # noqa: PLC0415
+
+        _native.binding()  # fail loudly when the library is not built
+        lib = ctypes.CDLL(_native.LIBRARY_PATH)
+        fn = lib.nibble_read_probe
+        fn.restype = ctypes.c_int
+        fn.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int64, ctypes.c_void_p,
+                       ctypes.c_void_p]
+        _probe = fn
+    return _probe
+
+
+def measured_read_gbps(size_bytes: int = 2 << 30, workgroups=(2048, 4096, 8192)) -> Dict[str, float]:
+    """Achievable HBM read bandwidth: the library's streaming-read probe over
+    ``size_bytes`` (>= 2 GiB, eight times the Infinity Cache), best over a few
+    workgroup counts.  Returns ``{"read_gbps": ..., "read_workgroups": ...}``."""
+    fn = _read_probe_fn()
+    src = torch.ones(size_bytes // 4, dtype=torch.int32, device="cuda")
+    sink = torch.zeros(max(workgroups), dtype=torch.int32, device="cuda")
+    best = None
+    for wgs in workgroups:
+        def run(_):
+            rc = fn(src.data_ptr(), size_bytes, wgs, sink.data_ptr(),
+                    torch.cuda.current_stream().cuda_stream)
+            if rc:
+                raise RuntimeError(f"read probe failed ({rc})")
+        t = bench(run, reps=4, trials=8, warmup=2)
+        gbps = size_bytes / (t.median_ms * 1e-3) / 1e9
+        if best is None or gbps > best[0]:
+            best = (gbps, wgs)
+    del src, sink
+    torch.cuda.empty_cache()
+    return {"read_gbps": round(best[0], 1), "read_workgroups": best[1]}
 
 
 class Rotation:

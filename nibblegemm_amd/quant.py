@@ -250,7 +250,8 @@ def dequantize(qw: QuantizedWeight) -> torch.Tensor:
     codes = unpack_nibbles(qw.qweight.cpu().numpy(), qw.K)
     signed = codes.astype(np.float32) - np.float32(ZERO_POINT)
     per_row = np.repeat(qw.scales.cpu().numpy().astype(np.float32), qw.group_size, axis=0)
-    return torch.from_numpy((signed * per_row).astype(np.float16))
+    with np.errstate(over="ignore"):  # products beyond fp16 range round to inf, as in torch
+        return torch.from_numpy((signed * per_row).astype(np.float16))
 
 
 def reference_matmul(X: torch.Tensor, qw: QuantizedWeight) -> torch.Tensor:

@@ -58,3 +58,79 @@ def test_decode_step_runs_and_counts_launches():
     nbytes = D.weight_bytes(layers)
     shapes = D.projection_shapes(cfg)
     assert nbytes == 2 * sum(k * n // 2 + (k // 128) * n * 2 for k, n in shapes.values())
+
+
+# ---------------------------------------------------------------------------
+# The config-5 step at its real shapes (2 distinct Llama-3-8B layers)
+# ---------------------------------------------------------------------------
+@pytest.fixture(scope="module")
+def layers_8b():
+    return D.build_layers(2, seed=21)
+
+
+def _replays_match(run, between, replays: int = 3):
+    """``run()`` captured in a HIP graph: every replay, with eager work and
+    synchronisation in between, reproduces the eager outputs bit for bit."""
+    eager = [t.clone() for t in run()]
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        outs = run()
+    torch.cuda.synchronize()
+    for _ in range(replays):
+        for t in outs:
+            t.zero_()
+        between()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for got, want in zip(outs, eager):
+            assert torch.equal(got, want)
+    return eager
+
+
+@pytest.mark.parametrize("variant", ["projections", "fused", "fused_swiglu"])
+def test_full_size_step_graph_replays_equal_eager(layers_8b, variant):
+    layers = {"projections": layers_8b,
+              "fused": [D.fuse(layer) for layer in layers_8b],
+              "fused_swiglu": [D.fuse(layer, swiglu=True) for layer in layers_8b]}[variant]
+    step = D.DecodeStep(layers)
+    assert step.launches == {"projections": 14, "fused": 8, "fused_swiglu": 8}[variant]
+    other = D.DecodeStep(layers_8b[:1], seed=5)
+    _replays_match(step.outputs, other)
+
+
+def test_full_size_glue_step_graph_replays_equal_eager(layers_8b):
+    layers = [D.fuse(layer, swiglu=True) for layer in layers_8b]
+    step = D.GlueDecodeStep(layers, pos=300, max_seq=320)
+    other = D.DecodeStep(layers_8b[:1], seed=6)
+    _replays_match(lambda: [step()], other)
+
+
+def test_full_size_fused_launches_equal_the_separate_ones(layers_8b):
+    """Each fused launch computes its columns with the separate launches'
+    plan, so q|k|v and gate|up give the separate outputs' bits, and the SwiGLU
+    epilogue the bits of silu(gate) * up in fp16."""
+    layer = layers_8b[1]
+    x = torch.randn(1, 4096, device="cuda").half()
+    sep = {name: ng.matmul(x, layer[name]) for name in ("q", "k", "v", "gate", "up")}
+    fused = D.fuse(layer)
+    assert torch.equal(ng.matmul(x, fused["qkv"]), torch.cat([sep["q"], sep["k"], sep["v"]], 1))
+    assert torch.equal(ng.matmul(x, fused["gate_up"]), torch.cat([sep["gate"], sep["up"]], 1))
+    h = ng.matmul_swiglu(x, D.fuse(layer, swiglu=True)["gate_up_swiglu"])
+    assert torch.equal(h, torch.nn.functional.silu(sep["gate"]) * sep["up"])
+
+
+def test_full_size_projections_match_the_oracle(oracle, layers_8b):
+    """Layer 0's seven projections at M = 1 against the oracle's dequantize +
+    fp32 matmul, within the north-star bound."""
+    step = D.DecodeStep(layers_8b[:1])
+    outs = step.outputs()
+    for (x, qw, _), y in zip(step.calls, outs):
+        ref = oracle.reference_matmul(x.cpu().numpy(), qw.qweight.cpu().numpy(),
+                                      qw.scales.cpu().numpy(), qw.K, qw.group_size)
+        ref = ref.astype(np.float64)
+        err = float(np.abs(y.float().cpu().numpy() - ref).max() / np.sqrt(np.mean(ref ** 2)))
+        assert err <= 1e-2, (qw.K, qw.N, err)

@@ -92,6 +92,22 @@ def test_prefill_configs_sampled_rows(M, K_, N):
     assert np.all(np.isfinite(y))
 
 
+@pytest.mark.parametrize("M", [128, 512, 2048])
+@pytest.mark.parametrize("K_,N", [(4096, 14336), (14336, 4096)])
+def test_prefill_configs_whole_output(M, K_, N):
+    """Every output of the prefill configs, both versions, against an fp32
+    product on the GPU of the dequant kernel's weights (bit-exact with the
+    oracle's dequantize, tests/test_dequant.py): a wrong tile, split or row
+    block anywhere fails."""
+    _, _, _, Xd, qw = synthetic(M, K_, N, 128, seed=300 + M + N)
+    ref = Xd.float() @ ng.dequant(qw).float()
+    rms = ref.pow(2).mean().sqrt()
+    for version in (6, 7):
+        y = ng.gemm(Xd, qw, version=version).float()
+        assert torch.isfinite(y).all()
+        assert float((y - ref).abs().max() / rms) <= RMS_TOL, version
+
+
 def test_gemm_is_deterministic():
     _, _, _, Xd, qw = synthetic(257, 2048, 1024, 128, seed=5)
     a = ng.gemm(Xd, qw)

@@ -8,9 +8,11 @@ asserted on every comparison:
 * the reference suite's ``max|y - ref| / mean|ref| < 5e-2`` (REL_TOL,
   tests/test_gemv.py:29 there).
 
-The streaming kernel accumulates exact fp16 x fp16 products in fp32
-(v_dot2_f32_f16) and scales fp32 group sums, so its error against the oracle is
-fp32 summation order plus the final fp16 rounding: ~1e-3 of RMS at most.
+The streaming kernels (the strip kernel for the default plan up to K = 8192,
+the split kernel beyond it and for explicit overrides) accumulate exact fp16 x
+fp16 products in fp32 on the matrix cores (v_mfma_f32_16x16x32_f16) and scale
+fp32 group sums, so their error against the oracle is fp32 summation order plus
+the final fp16 rounding: ~1e-3 of RMS at most.
 """
 from __future__ import annotations
 
