@@ -174,6 +174,16 @@ def main() -> int:
         fp16_bytes = H.total_bytes(M, K, N, G, 16)
         extras["byte_ratio_ceiling"] = round(fp16_bytes / nbytes, 3)
         del rot16, w16
+        # The same GEMV on strip-major copies of the rotation (the decode
+        # kernel's contiguous-strip layout; same bytes per call).
+        sm = H.Cycle([ng.to_strip_major(variants[i]) for i in range(rot_w.count)])
+        smt = H.bench_graph(lambda i: ng.matmul(X, sm[i]), reps=64, trials=10)
+        extras["strip_major"] = {
+            "strip_cols": sm[0].strip_cols, "us": round(smt.median_ms * 1e3, 2),
+            "gbps": round(H.achieved_gbps(nbytes, smt.median_ms), 1),
+            "pct_hbm_peak": round(100 * H.achieved_gbps(nbytes, smt.median_ms) / H.HBM_PEAK_GBPS, 2),
+            "clock_mhz": smt.clocks.get("clock_mean_mhz")}
+        del sm
         log(f"copy {copy:.0f} GB/s; 2 GiB read {read['read_gbps']:.0f} GB/s; hipBLASLt fp16 "
             f"{fp16.median_ms * 1e3:.2f} us; eager {eager.median_ms * 1e3:.2f} us/call")
 
@@ -191,7 +201,11 @@ def main() -> int:
             f"with the SwiGLU epilogue {decode['fused_swiglu']['graph_tok_s']} tok/s; "
             f"full step with norms, attention over {decode['glue']['context']} tokens and "
             f"residual adds {decode['glue']['graph_tok_s']} tok/s ({decode['glue']['launches']} "
-            f"launches); {time.perf_counter() - t0:.1f} s")
+            f"launches); strip-major weights: projections "
+            f"{decode['projections_strips']['graph_tok_s']}, fused "
+            f"{decode['fused_strips']['graph_tok_s']}, SwiGLU "
+            f"{decode['fused_swiglu_strips']['graph_tok_s']}, full step "
+            f"{decode['glue_strips']['graph_tok_s']} tok/s; {time.perf_counter() - t0:.1f} s")
 
     prefill = None
     if not args.skip_prefill:

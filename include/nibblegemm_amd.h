@@ -50,7 +50,7 @@
 extern "C" {
 #endif
 
-#define NIBBLE_ABI_VERSION 7
+#define NIBBLE_ABI_VERSION 8
 
 #if defined(__GNUC__) || defined(__clang__)
 #define NIBBLE_API __attribute__((visibility("default")))
@@ -184,6 +184,45 @@ NIBBLE_API size_t nibble_matmul_fused_workspace_bytes(int64_t M, int64_t K, int6
                                            int64_t group_size, void* stream);
 NIBBLE_API size_t nibble_matmul_fused_counter_bytes(int64_t M, int64_t K, int64_t N,
                                          int64_t group_size, void* stream);
+
+/*
+ * Strip-major weights for the decode GEMV (M <= 8).  No counterpart in the
+ * reference, which keeps only the packed layout above (python/nibblegemm/
+ * quant.py:28-50); this is an MI355X layout for decode-bound callers that can
+ * hold a second copy of a weight (or convert once at load).  The N columns
+ * are cut into strips of `strip_cols` (16, 32 or 64; 16 needs group_size 128)
+ * and each strip is stored whole, so one workgroup of the decode kernel
+ * streams one contiguous run:
+ *   Wt  int32 [N/strip_cols, K/8, strip_cols]   Wt[s][r][j] = Wq[r][s*strip_cols + j]
+ *   St  fp16  [N/strip_cols, K/G, strip_cols]   St[s][g][j] = S[g][s*strip_cols + j]
+ * Same bytes as Wq and S; the nibble format within a word is unchanged.
+ *
+ * nibble_strip_major_cols: the strip width this library measures fastest for
+ * a [K, N] weight (0 when none fits: N not a multiple of 16, or of 32 with
+ * group_size 64).  Pure host computation.
+ *
+ * nibble_pack_strip_major: writes Wt and St from Wq and S on `stream` (an
+ * exact permutation).  Wq, S, Wt, St 16-byte aligned; the outputs must not
+ * overlap the inputs.
+ *
+ * nibble_gemv_w4a16_strip_major: Y = X @ dequant(W) for M = x_rows <= 8 from
+ * Wt and St packed with this `strip_cols`, with nibble_matmul_w4a16_fused's
+ * epilogue (0 none, 1 fp16 bias, 2 SwiGLU of a gate|up interleaved weight,
+ * strip_cols >= 32) and optional RMSNorm prologue (same arithmetic and
+ * limits).  No workspace.  The result agrees with nibble_gemv_w4a16 on the
+ * packed weight within fp32 summation order (the two may sum in a different
+ * order); it is deterministic.
+ */
+NIBBLE_API int64_t nibble_strip_major_cols(int64_t K, int64_t N, int64_t group_size);
+NIBBLE_API int nibble_pack_strip_major(const void* Wq, int64_t wq_rows, int64_t wq_cols,
+                      const void* S, int64_t s_rows, int64_t s_cols,
+                      int64_t group_size, int64_t strip_cols, void* Wt, void* St,
+                      void* stream);
+NIBBLE_API int nibble_gemv_w4a16_strip_major(const void* X, int64_t x_rows, int64_t x_cols,
+                      const void* Wt, const void* St, int64_t K, int64_t N,
+                      int64_t group_size, int64_t strip_cols, int64_t epilogue,
+                      const void* bias, const void* norm_weight, float norm_eps,
+                      void* Y, void* stream);
 
 /*
  * Dense fp16 W [K, N] from packed weights, bit-exact with the reference's

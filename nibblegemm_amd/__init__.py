@@ -16,9 +16,10 @@ symmetric GPTQ / AWQ 4-bit checkpoints are converted by
 from . import convert, gptq
 from .gptq import HessianAccumulator, find_decoder_blocks, gptq_quantize, quantize_model_gptq
 from .ops import (DECODE_MAX_M, QuantLinear, dequant, extension, gemm, gemv, matmul, matmul_bias,
-                  matmul_swiglu, rmsnorm_matmul)
+                  matmul_swiglu, rmsnorm_matmul, strip_major_cols, to_strip_major)
 from .quant import (
     QuantizedWeight,
+    StripMajorWeight,
     concat_columns,
     dequantize,
     interleave_swiglu,
@@ -54,6 +55,9 @@ __all__ = [
     "quantize_model_gptq",
     "reference_matmul",
     "rmsnorm_matmul",
+    "StripMajorWeight",
+    "strip_major_cols",
+    "to_strip_major",
     "unpack_nibbles",
 ]
 __version__ = "0.1.0"

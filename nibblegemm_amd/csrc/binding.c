@@ -134,6 +134,48 @@ static PyObject* py_fused_ws(PyObject* self, PyObject* const* a, Py_ssize_t n) {
   return Py_BuildValue("(nn)", (Py_ssize_t)ws, (Py_ssize_t)cb);
 }
 
+/* strip_major_cols(K, N, g) */
+static PyObject* py_sm_cols(PyObject* self, PyObject* const* a, Py_ssize_t n) {
+  (void)self;
+  if (!nargs_is(n, 3, "strip_major_cols")) return NULL;
+  long long K, N, g;
+  if (!take_i64(a[0], &K) || !take_i64(a[1], &N) || !take_i64(a[2], &g)) return NULL;
+  return PyLong_FromLongLong((long long)nibble_strip_major_cols(K, N, g));
+}
+
+/* pack_strip_major(Wq, wr, wc, S, sr, sc, g, strip_cols, Wt, St, stream) */
+static PyObject* py_sm_pack(PyObject* self, PyObject* const* a, Py_ssize_t n) {
+  (void)self;
+  if (!nargs_is(n, 11, "pack_strip_major")) return NULL;
+  void *Wq, *S, *Wt, *St, *stream;
+  long long wr, wc, sr, sc, g, sw;
+  if (!take_ptr(a[0], &Wq) || !take_i64(a[1], &wr) || !take_i64(a[2], &wc) ||
+      !take_ptr(a[3], &S) || !take_i64(a[4], &sr) || !take_i64(a[5], &sc) ||
+      !take_i64(a[6], &g) || !take_i64(a[7], &sw) || !take_ptr(a[8], &Wt) ||
+      !take_ptr(a[9], &St) || !take_ptr(a[10], &stream))
+    return NULL;
+  return PyLong_FromLong(nibble_pack_strip_major(Wq, wr, wc, S, sr, sc, g, sw, Wt, St, stream));
+}
+
+/* gemv_strip_major(X, xr, xc, Wt, St, K, N, g, strip_cols, epilogue, bias, norm_w, norm_eps, Y,
+ *                  stream) */
+static PyObject* py_sm_gemv(PyObject* self, PyObject* const* a, Py_ssize_t n) {
+  (void)self;
+  if (!nargs_is(n, 15, "gemv_strip_major")) return NULL;
+  void *X, *Wt, *St, *bias, *norm, *Y, *stream;
+  long long xr, xc, K, N, g, sw, ep;
+  double eps = PyFloat_AsDouble(a[12]);
+  if (eps == -1.0 && PyErr_Occurred()) return NULL;
+  if (!take_ptr(a[0], &X) || !take_i64(a[1], &xr) || !take_i64(a[2], &xc) ||
+      !take_ptr(a[3], &Wt) || !take_ptr(a[4], &St) || !take_i64(a[5], &K) ||
+      !take_i64(a[6], &N) || !take_i64(a[7], &g) || !take_i64(a[8], &sw) ||
+      !take_i64(a[9], &ep) || !take_ptr(a[10], &bias) || !take_ptr(a[11], &norm) ||
+      !take_ptr(a[13], &Y) || !take_ptr(a[14], &stream))
+    return NULL;
+  return PyLong_FromLong(nibble_gemv_w4a16_strip_major(X, xr, xc, Wt, St, K, N, g, sw, ep, bias,
+                                                       norm, (float)eps, Y, stream));
+}
+
 /* rmsnorm(X, rows, cols, W, eps, Y, stream) */
 static PyObject* py_rmsnorm(PyObject* self, PyObject* const* a, Py_ssize_t n) {
   (void)self;
@@ -233,6 +275,12 @@ static PyMethodDef kMethods[] = {
      "nibble_matmul_w4a16_fused"},
     {"matmul_fused_workspace_bytes", (PyCFunction)(void (*)(void))py_fused_ws, METH_FASTCALL,
      "nibble_matmul_fused_workspace_bytes / nibble_matmul_fused_counter_bytes"},
+    {"strip_major_cols", (PyCFunction)(void (*)(void))py_sm_cols, METH_FASTCALL,
+     "nibble_strip_major_cols"},
+    {"pack_strip_major", (PyCFunction)(void (*)(void))py_sm_pack, METH_FASTCALL,
+     "nibble_pack_strip_major"},
+    {"gemv_strip_major", (PyCFunction)(void (*)(void))py_sm_gemv, METH_FASTCALL,
+     "nibble_gemv_w4a16_strip_major"},
     {"rmsnorm", (PyCFunction)(void (*)(void))py_rmsnorm, METH_FASTCALL, "nibble_rmsnorm_f16"},
     {"attention", (PyCFunction)(void (*)(void))py_attention, METH_FASTCALL,
      "nibble_attention_decode_f16"},

@@ -64,6 +64,13 @@ struct GemvArgs {
   float norm_eps;
   int strips;             // strip kernel: column strips of the launch
   int strips_per_xcd;     // strip kernel: strips run by each XCD's workgroups
+  // Strip kernel addressing, in bytes.  Word (packed row r, strip column
+  // 4 c + j) of strip s is at s * w_strip + r * w_row + 16 c + 4 j; the scale
+  // of (group g, strip column j) at s * s_strip + g * s_row + 2 j.  The
+  // packed [K / 8, N] layout has w_row = 4 N, w_strip = 4 SW, s_row = 2 N,
+  // s_strip = 2 SW; the strip-major layout has w_row = 4 SW,
+  // w_strip = 4 SW K / 8, s_row = 2 SW, s_strip = 2 SW K / G.
+  uint32_t w_row, w_strip, s_row, s_strip;
 };
 
 // Output epilogues of the streaming kernel (fused forms of what a caller
@@ -493,12 +500,12 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_strip_kernel(GemvArgs a) {
   const uint32_t c = lane % LPR, r = lane / LPR;
   const uint32_t col = strip * SW + 4 * c;
   const bool col_ok = strip < static_cast<uint32_t>(a.strips) && col < N;
-  const uint32_t row_bytes = N * 4u;
-  const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.Wq, (K / 8) * row_bytes);
+  const uint32_t row_bytes = a.w_row, s_row = a.s_row;
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.Wq, (K / 8) * N * 4u);
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.X, static_cast<uint32_t>(a.M) * K * 2u);
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.S, total_groups * N * 2u);
-  const uint32_t voff_w = col_ok ? r * row_bytes + col * 4u : kOutOfRange;
-  const uint32_t voff_s = col_ok ? col * 2u : kOutOfRange;
+  const uint32_t voff_w = col_ok ? strip * a.w_strip + r * row_bytes + 16u * c : kOutOfRange;
+  const uint32_t voff_s = col_ok ? strip * a.s_strip + 8u * c : kOutOfRange;
   // A side: lane (m', kb) holds row m' = RPT p + mm of each tile at k block
   // kb, i.e. the 8 k of packed row P kb + p of a wave load.
   const uint32_t mq = lane & 15u, kb = lane >> 4;
@@ -536,7 +543,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_strip_kernel(GemvArgs a) {
       if (ch < chunks)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
             rs, (lds_ptr)(s_lds + blk * 512), 16,
-            strip < static_cast<uint32_t>(a.strips) && scol < N ? (g * N + scol) * 2u : kOutOfRange,
+            strip < static_cast<uint32_t>(a.strips) && scol < N
+                ? strip * a.s_strip + g * s_row + 16u * part
+                : kOutOfRange,
             0, 0, 0);
     }
     // Rows past M read as zeros from LDS (no masking in the loop).
@@ -581,7 +590,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_strip_kernel(GemvArgs a) {
     if constexpr (!STAGED)
       st.s = __builtin_bit_cast(
           h4_t, __builtin_amdgcn_raw_buffer_load_b64(rs, in ? voff_s : kOutOfRange,
-                                                     static_cast<uint32_t>(g) * N * 2u, kWPolicy));
+                                                     static_cast<uint32_t>(g) * s_row, kWPolicy));
   };
 
   f4_t tot[TILES][4];
@@ -878,6 +887,7 @@ template <int MT, int GROUP>
 hipError_t launch_strip_mt(const GemvArgs& a, const StreamPlan& p, hipStream_t stream) {
   const int key = p.strip_cols * 10000 + p.waves * 100 + p.depth;
   switch (key) {
+    case 16 * 10000 + 8 * 100 + 4: return launch_strip_geometry<MT, GROUP, 16, 8, 4>(a, stream);
     case 32 * 10000 + 8 * 100 + 2: return launch_strip_geometry<MT, GROUP, 32, 8, 2>(a, stream);
     case 32 * 10000 + 16 * 100 + 2: return launch_strip_geometry<MT, GROUP, 32, 16, 2>(a, stream);
     case 64 * 10000 + 4 * 100 + 2: return launch_strip_geometry<MT, GROUP, 64, 4, 2>(a, stream);
@@ -991,6 +1001,45 @@ int plan_stream(int64_t M, int64_t K, int64_t N, int64_t G, bool split_k, int64_
   return plan_split_kernel(M, K, N, G, split_k, splits_override, threads_override, p);
 }
 
+// Strip width for strip-major weights (the layout fixes it, so it is chosen
+// once, when the weight is packed).  Measured on MI355X, M = 1, graph replay,
+// strip-major against the packed layout at the same geometry and against
+// the packed layout's own plan: 14336 x 4096 7.6 us with 16-column strips
+// (split kernel 9.5); 4096 x 1024 3.7 (4.3); 4096 x 4096 4.5 (4.7);
+// 4096 x 6144 4.8 (5.5); 4096 x 14336 7.2 (7.3); 4096 x 28672 12.1 (13.0);
+// 8192 x 8192 8.0 (9.2).  Narrow strips of the packed layout read 64 or 128
+// contiguous bytes per packed row, 4 N bytes apart, which HBM serves at a
+// fraction of its streaming rate; a strip-major strip is one contiguous run.
+int64_t strip_major_cols(int64_t K, int64_t N, int64_t G) {
+  if (K <= 0 || N <= 0 || (G != 64 && G != 128) || K % G != 0) return 0;
+  if (N >= kStripWideN && N % 64 == 0) return 64;
+  const bool narrow = G == 128 && N % 16 == 0;  // a 16-column wave load spans 128 k
+  if (narrow && (N <= 2048 || K >= 12288)) return 16;  // too few 32-column strips to fill the chip
+  if (N % 32 == 0) return 32;
+  return narrow ? 16 : 0;
+}
+
+bool plan_strip_major(int64_t M, int64_t K, int64_t N, int64_t G, int64_t SW, StreamPlan* p) {
+  if (M < 1 || M > 8 || K <= 0 || N <= 0 || (G != 64 && G != 128) || K % G != 0) return false;
+  if ((SW != 16 && SW != 32 && SW != 64) || N % SW != 0 || (SW == 16 && G != 128)) return false;
+  StreamPlan q;
+  q.kernel = kStripKernel;
+  q.mt = mt_for(M);
+  q.mblocks = 1;
+  q.splits = 1;
+  q.groups_per_split = static_cast<int>(K / G);
+  q.strip_cols = static_cast<int>(SW);
+  // 16-column strips keep 4 groups of loads in flight per wave (1 KiB each);
+  // wider strips hold enough bytes with 2.
+  q.waves = SW == 64 ? 4 : 8;
+  q.depth = SW == 16 ? 4 : 2;
+  q.strips = static_cast<int>(N / SW);
+  q.counter_bytes = 0;
+  q.workspace_bytes = 0;
+  *p = q;
+  return true;
+}
+
 bool stream_supported(const void* X, const void* Wq, const void* S, const void* Y, int64_t M,
                       int64_t K, int64_t N, int64_t G) {
   const int64_t lim = int64_t(1) << 31;
@@ -1019,7 +1068,9 @@ int launch_stream(const void* X, const void* Wq, const void* S, void* Y, int64_t
 int launch_stream_split(const void* X, const void* Wq, const void* S, void* Y, int64_t M,
                         int64_t K, int64_t N, int64_t G, const StreamPlan& p, void* counters,
                         void* partials, hipStream_t stream, const char* who, int epilogue,
-                        const void* bias, const void* norm_w, float norm_eps) {
+                        const void* bias, const void* norm_w, float norm_eps, bool strip_major) {
+  if (strip_major && p.kernel != kStripKernel)
+    return fail(NIBBLE_ERR_UNSUPPORTED, "%s: strip-major weights need the strip kernel", who);
   GemvArgs a;
   a.X = static_cast<const _Float16*>(X);
   a.Wq = static_cast<const uint32_t*>(Wq);
@@ -1040,6 +1091,18 @@ int launch_stream_split(const void* X, const void* Wq, const void* S, void* Y, i
   if (p.kernel == kStripKernel) {
     a.strips = p.strips;
     a.strips_per_xcd = static_cast<int>(ceil_div(p.strips, 8));
+    const uint32_t sw = static_cast<uint32_t>(p.strip_cols);
+    if (strip_major) {
+      a.w_row = sw * 4u;
+      a.w_strip = static_cast<uint32_t>(K / 8) * sw * 4u;
+      a.s_row = sw * 2u;
+      a.s_strip = static_cast<uint32_t>(K / G) * sw * 2u;
+    } else {
+      a.w_row = static_cast<uint32_t>(N) * 4u;
+      a.w_strip = sw * 4u;
+      a.s_row = static_cast<uint32_t>(N) * 2u;
+      a.s_strip = sw * 2u;
+    }
     e = G == 128 ? launch_strip_group<128>(a, p, stream) : launch_strip_group<64>(a, p, stream);
   } else {
     e = G == 128 ? launch_group<128>(a, p, stream) : launch_group<64>(a, p, stream);
@@ -1391,5 +1454,144 @@ extern "C" int nibble_gemv_w4a16_noalloc(const void* X, int64_t x_rows, int64_t 
   rc = launch_stream_split(X, Wq, S, Y, M, K, N, group_size, p, base,
                            static_cast<char*>(base) + kScratchCounterBytes, stream,
                            "gemv (no-alloc) kernel launch");
+  return rc == NIBBLE_OK ? ok() : rc;
+}
+
+// ---------------------------------------------------------------------------
+// Strip-major weights for the decode GEMV.  No counterpart in the reference,
+// which has only the packed [K / 8, N] layout (python/nibblegemm/quant.py:
+// 28-50).  The layout splits the N columns into strips of `strip_cols` and
+// stores each strip's packed rows (and group scales) contiguously, so a
+// workgroup of the strip kernel streams one contiguous run instead of short
+// pieces of every packed row.
+
+namespace {
+// One 16-byte chunk per thread iteration: packed words (4 columns) of the
+// source row-major [rows, n] array go to strip n / sw, row r, column n % sw;
+// scale chunks hold 8 columns.
+__global__ __launch_bounds__(256) void pack_strip_major_kernel(const u4_t* __restrict__ wq,
+                                                               const u4_t* __restrict__ s,
+                                                               u4_t* __restrict__ wt,
+                                                               u4_t* __restrict__ st,
+                                                               uint32_t rows, uint32_t srows,
+                                                               uint32_t n, uint32_t sw) {
+  const uint32_t wq_row = n / 4, s_row = n / 8;
+  const uint32_t wchunks = rows * wq_row, total = wchunks + srows * s_row;
+  for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < total; i += gridDim.x * 256u) {
+    if (i < wchunks) {
+      const uint32_t r = i / wq_row, col = (i % wq_row) * 4u;
+      wt[((col / sw) * rows + r) * (sw / 4u) + (col % sw) / 4u] = wq[i];
+    } else {
+      const uint32_t e = i - wchunks;
+      const uint32_t g = e / s_row, col = (e % s_row) * 8u;
+      st[((col / sw) * srows + g) * (sw / 8u) + (col % sw) / 8u] = s[e];
+    }
+  }
+}
+
+bool overlaps(const void* a, size_t an, const void* b, size_t bn) {
+  const char *pa = static_cast<const char*>(a), *pb = static_cast<const char*>(b);
+  return pa < pb + bn && pb < pa + an;
+}
+
+int check_strip_cols(int64_t N, int64_t G, int64_t SW) {
+  NIBBLE_CHECK(SW == 16 || SW == 32 || SW == 64, "strip_cols must be 16, 32 or 64, got %lld",
+               (long long)SW);
+  NIBBLE_CHECK(N % SW == 0, "N=%lld is not a multiple of strip_cols=%lld", (long long)N,
+               (long long)SW);
+  NIBBLE_CHECK(SW != 16 || G == 128, "16-column strips need group_size 128");
+  return NIBBLE_OK;
+}
+}  // namespace
+
+extern "C" int64_t nibble_strip_major_cols(int64_t K, int64_t N, int64_t group_size) {
+  return strip_major_cols(K, N, group_size);
+}
+
+extern "C" int nibble_pack_strip_major(const void* Wq, int64_t wq_rows, int64_t wq_cols,
+                                       const void* S, int64_t s_rows, int64_t s_cols,
+                                       int64_t group_size, int64_t strip_cols, void* Wt,
+                                       void* St, void* stream_) {
+  NIBBLE_CHECK(wq_rows > 0 && wq_cols > 0 && s_rows > 0 && s_cols > 0,
+               "bad dimension (K and N must be positive)");
+  const int64_t K = wq_rows * 8, N = wq_cols;
+  NIBBLE_CHECK(group_size == 64 || group_size == 128, "group_size must be 64 or 128");
+  NIBBLE_CHECK(s_rows * group_size == K, "scale rows disagree with K/group_size");
+  NIBBLE_CHECK(s_cols == N, "scale columns disagree with N");
+  int rc = check_strip_cols(N, group_size, strip_cols);
+  if (rc != NIBBLE_OK) return rc;
+  NIBBLE_CHECK(Wq != nullptr && S != nullptr && Wt != nullptr && St != nullptr, "null pointer");
+  NIBBLE_CHECK(aligned(Wq, 16) && aligned(S, 16) && aligned(Wt, 16) && aligned(St, 16),
+               "weights and scales must be 16-byte aligned");
+  const size_t wbytes = static_cast<size_t>(K / 8) * N * 4;
+  const size_t sbytes = static_cast<size_t>(s_rows) * N * 2;
+  NIBBLE_CHECK(wbytes < (size_t(1) << 31) && sbytes < (size_t(1) << 31),
+               "weights beyond 32-bit offsets");
+  NIBBLE_CHECK(!overlaps(Wt, wbytes, Wq, wbytes) && !overlaps(Wt, wbytes, S, sbytes) &&
+                   !overlaps(St, sbytes, Wq, wbytes) && !overlaps(St, sbytes, S, sbytes) &&
+                   !overlaps(Wt, wbytes, St, sbytes),
+               "the strip-major outputs must not overlap the inputs or each other");
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  DeviceGuard guard;
+  int dev = 0;
+  NIBBLE_HIP(guard.enter(stream, &dev));
+  const int64_t chunks = (K / 8) * (N / 4) + s_rows * (N / 8);
+  const unsigned blocks = static_cast<unsigned>(std::min<int64_t>(ceil_div(chunks, 256), 8192));
+  pack_strip_major_kernel<<<blocks, 256, 0, stream>>>(
+      static_cast<const u4_t*>(Wq), static_cast<const u4_t*>(S), static_cast<u4_t*>(Wt),
+      static_cast<u4_t*>(St), static_cast<uint32_t>(K / 8), static_cast<uint32_t>(s_rows),
+      static_cast<uint32_t>(N), static_cast<uint32_t>(strip_cols));
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, "strip-major pack kernel launch");
+  return ok();
+}
+
+extern "C" int nibble_gemv_w4a16_strip_major(const void* X, int64_t x_rows, int64_t x_cols,
+                                             const void* Wt, const void* St, int64_t K, int64_t N,
+                                             int64_t group_size, int64_t strip_cols,
+                                             int64_t epilogue, const void* bias,
+                                             const void* norm_weight, float norm_eps, void* Y,
+                                             void* stream_) {
+  NIBBLE_CHECK(x_rows >= 0 && K > 0 && N > 0, "bad dimension (K and N must be positive)");
+  NIBBLE_CHECK(x_cols == K, "activation columns (%lld) disagree with K=%lld", (long long)x_cols,
+               (long long)K);
+  const int64_t M = x_rows;
+  NIBBLE_CHECK(M <= 8, "strip-major gemv supports M <= 8, got %lld", (long long)M);
+  NIBBLE_CHECK(group_size == 64 || group_size == 128, "group_size must be 64 or 128");
+  NIBBLE_CHECK(K % group_size == 0, "K=%lld is not a multiple of group_size=%lld", (long long)K,
+               (long long)group_size);
+  int rc = check_strip_cols(N, group_size, strip_cols);
+  if (rc != NIBBLE_OK) return rc;
+  NIBBLE_CHECK(epilogue == kEpilogueNone || epilogue == kEpilogueBias ||
+                   epilogue == kEpilogueSwiglu,
+               "epilogue must be 0 (none), 1 (bias) or 2 (swiglu), got %lld", (long long)epilogue);
+  NIBBLE_CHECK(epilogue != kEpilogueSwiglu || strip_cols >= 2 * kSwigluBlock,
+               "swiglu needs strips of at least 32 columns (gate|up 16-column blocks)");
+  NIBBLE_CHECK(epilogue != kEpilogueBias || M == 0 || bias != nullptr, "null bias");
+  NIBBLE_CHECK(epilogue != kEpilogueBias || aligned(bias, 2), "misaligned bias");
+  if (norm_weight != nullptr) {
+    NIBBLE_CHECK(K <= kNormMaxK, "the fused RMSNorm supports K <= %d, got %lld", kNormMaxK,
+                 (long long)K);
+    NIBBLE_CHECK(M == 0 || mt_for(M) * K * 2 <= 65536,
+                 "the fused RMSNorm needs %lld rows x K=%lld fp16 of LDS, above 64 KiB",
+                 (long long)mt_for(M), (long long)K);
+    NIBBLE_CHECK(aligned(norm_weight, 16), "norm weight must be 16-byte aligned");
+    NIBBLE_CHECK(std::isfinite(norm_eps) && norm_eps >= 0.0f, "norm eps must be finite and >= 0");
+  }
+  if (M == 0) return ok();
+  NIBBLE_CHECK(X != nullptr && Wt != nullptr && St != nullptr && Y != nullptr, "null pointer");
+  NIBBLE_CHECK(stream_supported(X, Wt, St, Y, M, K, N, group_size),
+               "operands must be aligned (X, Wt 16-byte; St, Y 8-byte) and within 32-bit offsets");
+  StreamPlan p;
+  if (!plan_strip_major(M, K, N, group_size, strip_cols, &p))
+    return fail(NIBBLE_ERR_UNSUPPORTED, "no strip-major plan for M=%lld K=%lld N=%lld",
+                (long long)M, (long long)K, (long long)N);
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  DeviceGuard guard;
+  int dev = 0;
+  NIBBLE_HIP(guard.enter(stream, &dev));
+  rc = launch_stream_split(X, Wt, St, Y, M, K, N, group_size, p, nullptr, nullptr, stream,
+                           "strip-major gemv kernel launch", static_cast<int>(epilogue), bias,
+                           norm_weight, norm_eps, true);
   return rc == NIBBLE_OK ? ok() : rc;
 }

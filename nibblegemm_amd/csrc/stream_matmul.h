@@ -73,12 +73,20 @@ int launch_stream(const void* X, const void* Wq, const void* S, void* Y, int64_t
 
 // launch_stream with the split-K workspace given as its two parts: the
 // counter region (zero on entry, left zero) and the fp32 partials.  The plan
-// must fit whatever those point at; no checks are made here.
+// must fit whatever those point at; no checks are made here.  `strip_major`
+// reads Wq and S in the strip-major layout of the plan's strip width (strip
+// kernel plans only).
 int launch_stream_split(const void* X, const void* Wq, const void* S, void* Y, int64_t M,
                         int64_t K, int64_t N, int64_t G, const StreamPlan& p, void* counters,
                         void* partials, hipStream_t stream, const char* who, int epilogue = 0,
                         const void* bias = nullptr, const void* norm_w = nullptr,
-                        float norm_eps = 0.0f);
+                        float norm_eps = 0.0f, bool strip_major = false);
+
+// Strip width recommended for strip-major weights of this shape (0: none
+// fits), and the strip kernel's plan for a strip-major weight of width SW.
+// Pure host arithmetic.
+int64_t strip_major_cols(int64_t K, int64_t N, int64_t G);
+bool plan_strip_major(int64_t M, int64_t K, int64_t N, int64_t G, int64_t SW, StreamPlan* p);
 
 // Largest K the fused-RMSNorm prologue takes (8 chunks of 256 x 8 columns).
 constexpr int kNormMaxK = 16384;

@@ -24,6 +24,11 @@ gate and up instead and runs them through the SwiGLU epilogue
 (each output column is computed from the same weights, scales and
 activations); it only removes launches.
 
+The ``*_strips`` variants run the same steps on strip-major copies of the
+weights (:func:`~nibblegemm_amd.ops.to_strip_major`, the decode GEMV's
+contiguous-strip layout; same codes and scales, so the same bytes per
+step).
+
 ``glue`` runs a whole token step instead (:class:`GlueDecodeStep`): per
 layer RMSNorm, the q|k|v projection, rotary embedding and grouped-query
 attention over a KV cache of ``pos`` tokens, the o projection with the
@@ -48,7 +53,7 @@ import torch
 
 from . import harness as H
 from .glue import attention_bytes, attention_decode, rmsnorm, rope_tables
-from .ops import matmul, matmul_bias, matmul_swiglu, rmsnorm_matmul
+from .ops import matmul, matmul_bias, matmul_swiglu, rmsnorm_matmul, to_strip_major
 from .quant import QuantizedWeight, concat_columns, interleave_swiglu, quantize_device
 
 LLAMA3_8B = {"hidden": 4096, "kv": 1024, "intermediate": 14336, "layers": 32,
@@ -88,6 +93,11 @@ def fuse(layer: Dict[str, QuantizedWeight], swiglu: bool = False) -> Dict[str, Q
                else concat_columns(layer["gate"], layer["up"]))
     return {"qkv": concat_columns(layer["q"], layer["k"], layer["v"]), "o": layer["o"],
             ("gate_up_swiglu" if swiglu else "gate_up"): gate_up, "down": layer["down"]}
+
+
+def strips(layers: List[Dict[str, QuantizedWeight]]) -> list:
+    """Strip-major copies of every weight (each at its recommended width)."""
+    return [{name: to_strip_major(qw) for name, qw in layer.items()} for layer in layers]
 
 
 def weight_bytes(layers: List[Dict[str, QuantizedWeight]]) -> int:
@@ -222,7 +232,8 @@ def measure(layers: List[Dict[str, QuantizedWeight]], trials: int = 10, warmup: 
     }
 
 
-VARIANTS = ("projections", "fused", "fused_swiglu", "glue")
+VARIANTS = ("projections", "fused", "fused_swiglu", "glue", "projections_strips", "fused_strips",
+            "fused_swiglu_strips", "glue_strips")
 
 
 def run(n_layers: int = 32, group_size: int = 128, trials: int = 10, glue_pos: int = 1023,
@@ -231,19 +242,32 @@ def run(n_layers: int = 32, group_size: int = 128, trials: int = 10, glue_pos: i
     nbytes = weight_bytes(layers)
     res = {"config": f"Llama-3-8B shapes, {n_layers} distinct layers, g={group_size}, M=1",
            "roofline_tok_s": round(H.HBM_PEAK_GBPS * 1e9 / nbytes, 1)}
-    if "projections" in variants:
+    want = set(variants)
+    if "projections" in want:
         res["projections"] = measure(layers, trials)
-    if "fused" in variants:
+    if "projections_strips" in want:
+        res["projections_strips"] = measure(strips(layers), trials)
+    if want & {"fused", "fused_strips"}:
         fused = [fuse(layer) for layer in layers]
-        res["fused"] = measure(fused, trials)
+        if "fused" in want:
+            res["fused"] = measure(fused, trials)
+        if "fused_strips" in want:
+            res["fused_strips"] = measure(strips(fused), trials)
         del fused
-    if "fused_swiglu" in variants or "glue" in variants:
+    if want & {"fused_swiglu", "glue", "fused_swiglu_strips", "glue_strips"}:
         swiglu = [fuse(layer, swiglu=True) for layer in layers]
         del layers
-        if "fused_swiglu" in variants:
+        if "fused_swiglu" in want:
             res["fused_swiglu"] = measure(swiglu, trials)
-        if "glue" in variants and glue_pos >= 0:
+        if "glue" in want and glue_pos >= 0:
             res["glue"] = measure_glue(swiglu, glue_pos, trials)
+        if want & {"fused_swiglu_strips", "glue_strips"}:
+            swiglu_strips = strips(swiglu)
+            del swiglu
+            if "fused_swiglu_strips" in want:
+                res["fused_swiglu_strips"] = measure(swiglu_strips, trials)
+            if "glue_strips" in want and glue_pos >= 0:
+                res["glue_strips"] = measure_glue(swiglu_strips, glue_pos, trials)
     return res
 
 

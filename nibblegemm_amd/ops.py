@@ -32,7 +32,8 @@ from typing import Dict, Optional, Tuple
 import torch
 
 from . import _native
-from .quant import SWIGLU_BLOCK, QuantizedWeight, quantize, split_swiglu  # noqa: F401
+from .quant import (SWIGLU_BLOCK, QuantizedWeight, StripMajorWeight, quantize,  # noqa: F401
+                    split_swiglu)
 
 #: Batch sizes at or below this go to the bandwidth-bound decode kernel
 #: (reference ops.py:30).
@@ -290,14 +291,86 @@ def gemm(X: torch.Tensor, qw: QuantizedWeight, version: int = 6) -> torch.Tensor
     return Y
 
 
-def matmul(X: torch.Tensor, qw: QuantizedWeight, splits: int = 0,
-           block_threads: int = 0) -> torch.Tensor:
+def strip_major_cols(K: int, N: int, group_size: int) -> int:
+    """The strip width :func:`to_strip_major` picks for a ``[K, N]`` weight
+    (0 when no strip-major layout fits it)."""
+    return int(_bind().strip_major_cols(K, N, group_size))
+
+
+def to_strip_major(qw: QuantizedWeight, strip_cols: int = 0) -> StripMajorWeight:
+    """A device copy of ``qw`` in the strip-major layout of the decode GEMV
+    (one permutation kernel on the current stream; same bytes again).
+    ``strip_cols`` 0 picks :func:`strip_major_cols`.  The result serves
+    :func:`matmul` and the fused decode ops for batches of at most 8 rows."""
+    ext = _bind()
+    Wq, S = qw.qweight, qw.scales
+    if not (Wq.is_cuda and S.is_cuda):
+        raise RuntimeError("tensors must live on the GPU")
+    if Wq.dtype != torch.int32 or S.dtype != torch.float16:
+        raise RuntimeError("packed weights must be int32 and scales fp16")
+    if not (Wq.is_contiguous() and S.is_contiguous()) or Wq.dim() != 2 or S.dim() != 2:
+        raise RuntimeError("expected contiguous 2-D weights and scales")
+    sw = int(strip_cols) or strip_major_cols(qw.K, qw.N, qw.group_size)
+    if sw == 0:
+        raise ValueError(f"no strip-major layout fits K={qw.K}, N={qw.N}, "
+                         f"group_size={qw.group_size}")
+    if sw <= 0 or qw.N % sw:
+        raise ValueError(f"N={qw.N} is not a multiple of strip_cols={sw}")
+    dev = Wq.device
+    Wt = torch.empty((qw.N // sw, qw.K // 8, sw), dtype=torch.int32, device=dev)
+    St = torch.empty((qw.N // sw, S.shape[0], sw), dtype=torch.float16, device=dev)
+    rc = ext.pack_strip_major(Wq.data_ptr(), Wq.shape[0], Wq.shape[1], S.data_ptr(), S.shape[0],
+                              S.shape[1], qw.group_size, sw, Wt.data_ptr(), St.data_ptr(),
+                              _stream(dev))
+    if rc:
+        _raise(rc, ext)
+    return StripMajorWeight(Wt, St, qw.group_size, qw.K, qw.N, sw)
+
+
+def _strip_gemv(X: torch.Tensor, w: StripMajorWeight, epilogue: int,
+                bias: Optional[torch.Tensor], n_out: int,
+                norm: Optional[Tuple[torch.Tensor, float]] = None) -> torch.Tensor:
+    ext = _bind()
+    Wt, St = w.qweight, w.scales
+    if not (X.is_cuda and Wt.is_cuda and St.is_cuda):
+        raise RuntimeError("all tensors must live on the GPU")
+    if X.dtype != torch.float16:
+        raise RuntimeError("activations must be fp16")
+    if Wt.dtype != torch.int32 or St.dtype != torch.float16:
+        raise RuntimeError("strip-major weights must be int32 and scales fp16")
+    if not (X.is_contiguous() and Wt.is_contiguous() and St.is_contiguous()):
+        raise RuntimeError("inputs must be contiguous")
+    if not (X.device == Wt.device == St.device):
+        raise RuntimeError("all tensors must live on the same device")
+    M, K = X.shape
+    if M > DECODE_MAX_M:
+        raise ValueError(f"strip-major weights serve batches of at most {DECODE_MAX_M} rows, "
+                         f"got {M}; multiply larger batches with the packed weight")
+    dev = X.device
+    Y = torch.empty((M, n_out), dtype=torch.float16, device=dev)
+    rc = ext.gemv_strip_major(X.data_ptr(), M, K, Wt.data_ptr(), St.data_ptr(), w.K, w.N,
+                              w.group_size, w.strip_cols, epilogue,
+                              bias.data_ptr() if bias is not None else None,
+                              norm[0].data_ptr() if norm is not None else None,
+                              float(norm[1]) if norm is not None else 0.0, Y.data_ptr(),
+                              _stream(dev))
+    if rc:
+        _raise(rc, ext)
+    return Y
+
+
+def matmul(X: torch.Tensor, qw, splits: int = 0, block_threads: int = 0) -> torch.Tensor:
     """``X @ dequant(qw)``, dispatching on batch size (reference ops.py:89-104):
-    M <= DECODE_MAX_M goes to ``gemv(version=4)``, larger M to ``gemm``."""
+    M <= DECODE_MAX_M goes to ``gemv(version=4)``, larger M to ``gemm``.  A
+    :class:`StripMajorWeight` (M <= 8 only) runs the strip-major GEMV."""
     if X.dim() != 2:
         raise ValueError(f"expected a 2-D activation matrix, got {tuple(X.shape)}")
     if X.size(1) != qw.K:
         raise ValueError(f"K mismatch: activations have {X.size(1)}, weights have {qw.K}")
+    if isinstance(qw, StripMajorWeight):
+        if splits or block_threads:
+            raise ValueError("strip-major weights take no splits / block_threads override")
+        return _strip_gemv(X, qw, 0, None, qw.N)
     if X.size(0) <= DECODE_MAX_M:
         return gemv(X, qw, version=4, splits=splits, block_threads=block_threads)
     return gemm(X, qw)
@@ -361,8 +434,12 @@ def matmul_bias(X: torch.Tensor, qw: QuantizedWeight, bias: torch.Tensor) -> tor
     bias added in the kernel's epilogue, same bits); other cases run the two
     ops."""
     _check_2d(X, qw)
-    if (bias.dtype == torch.float16 and bias.dim() == 1 and bias.numel() == qw.N
-            and bias.device == X.device and bias.is_contiguous() and _fusable(X, qw)):
+    fp16_bias = (bias.dtype == torch.float16 and bias.dim() == 1 and bias.numel() == qw.N
+                 and bias.device == X.device and bias.is_contiguous())
+    if isinstance(qw, StripMajorWeight):
+        if fp16_bias:
+            return _strip_gemv(X, qw, 1, bias, qw.N)
+    elif fp16_bias and _fusable(X, qw):
         return _fused(X, qw, 1, bias, qw.N)
     return matmul(X, qw) + bias
 
@@ -374,6 +451,8 @@ def matmul_swiglu(X: torch.Tensor, qw: QuantizedWeight) -> torch.Tensor:
     _check_2d(X, qw)
     if qw.N % (2 * SWIGLU_BLOCK):
         raise ValueError(f"N={qw.N} is not an interleaved gate|up weight (multiple of 32)")
+    if isinstance(qw, StripMajorWeight):
+        return _strip_gemv(X, qw, 2, None, qw.N // 2)
     if _fusable(X, qw):
         return _fused(X, qw, 2, None, qw.N // 2)
     gate, up = split_swiglu(matmul(X, qw))
@@ -401,16 +480,19 @@ def rmsnorm_matmul(X: torch.Tensor, norm_weight: torch.Tensor, qw: QuantizedWeig
         raise ValueError(f"N={qw.N} is not an interleaved gate|up weight (multiple of 32)")
     M, K = X.shape
     mt = 1 if M <= 1 else 2 if M <= 2 else 4 if M <= 4 else 8
-    if (_fusable(X, qw) and M <= NORM_FUSED_MAX_M and K <= NORM_FUSED_MAX_K and mt * K * 2 <= 65536
+    strip = isinstance(qw, StripMajorWeight)
+    fusable = (X.dim() == 2 and X.is_cuda and X.is_contiguous()) if strip else _fusable(X, qw)
+    if (fusable and M <= NORM_FUSED_MAX_M and K <= NORM_FUSED_MAX_K and mt * K * 2 <= 65536
             and norm_weight.dtype == torch.float16 and norm_weight.is_contiguous()
             and norm_weight.device == X.device and norm_weight.numel() == K
             and norm_weight.data_ptr() % 16 == 0 and X.dtype == torch.float16
             and (bias is None or (bias.dtype == torch.float16 and bias.dim() == 1
                                   and bias.numel() == qw.N and bias.is_contiguous()
                                   and bias.device == X.device))):
+        run = _strip_gemv if strip else _fused
         if swiglu:
-            return _fused(X, qw, 2, None, qw.N // 2, (norm_weight, eps))
-        return _fused(X, qw, 1 if bias is not None else 0, bias, qw.N, (norm_weight, eps))
+            return run(X, qw, 2, None, qw.N // 2, (norm_weight, eps))
+        return run(X, qw, 1 if bias is not None else 0, bias, qw.N, (norm_weight, eps))
     from .glue import rmsnorm  # noqa: PLC0415  (glue imports this module)
     a = rmsnorm(X, norm_weight, eps)
     if swiglu:
@@ -427,7 +509,12 @@ class QuantLinear(torch.nn.Module):
     ``forward`` flattens leading dimensions, multiplies through
     :func:`matmul` and adds the bias; an fp16 bias is added inside the
     matmul's output stage where the kernel supports it (same bits as a
-    separate fp16 add)."""
+    separate fp16 add).
+
+    :meth:`prepare_decode` adds a strip-major copy of the weight (not part of
+    the state dict) that batches of at most 8 rows then multiply with; it
+    costs the weight's bytes again and is rebuilt when a state dict is
+    loaded."""
 
     def __init__(self, qw: QuantizedWeight, bias: Optional[torch.Tensor] = None):
         super().__init__()
@@ -436,6 +523,27 @@ class QuantLinear(torch.nn.Module):
         self.N = qw.N
         for name, tensor in (("qweight", qw.qweight), ("scales", qw.scales), ("bias", bias)):
             self.register_buffer(name, tensor)
+        self.strip_cols = 0
+        self.register_buffer("qweight_strips", None, persistent=False)
+        self.register_buffer("scales_strips", None, persistent=False)
+        self.register_load_state_dict_post_hook(QuantLinear._refresh_decode_copy)
+
+    def prepare_decode(self, strip_cols: int = 0) -> "QuantLinear":
+        """Build the strip-major copy of the weight on its GPU (``strip_cols``
+        0 picks :func:`strip_major_cols`); returns the module."""
+        sm = to_strip_major(self._qw(), strip_cols)
+        self.qweight_strips, self.scales_strips, self.strip_cols = sm.qweight, sm.scales, sm.strip_cols
+        return self
+
+    def release_decode(self) -> None:
+        """Drop the strip-major copy."""
+        self.qweight_strips = self.scales_strips = None
+        self.strip_cols = 0
+
+    @staticmethod
+    def _refresh_decode_copy(module: "QuantLinear", incompatible_keys) -> None:
+        if module.qweight_strips is not None:
+            module.prepare_decode(module.strip_cols)
 
     @classmethod
     def from_linear(cls, linear: torch.nn.Linear, group_size: int = 128) -> "QuantLinear":
@@ -449,8 +557,15 @@ class QuantLinear(torch.nn.Module):
     def _qw(self) -> QuantizedWeight:
         return QuantizedWeight(self.qweight, self.scales, self.group_size, self.K, self.N)
 
+    def _weight_for(self, m: int):
+        if self.qweight_strips is not None and 0 < m <= DECODE_MAX_M:
+            return StripMajorWeight(self.qweight_strips, self.scales_strips, self.group_size,
+                                    self.K, self.N, self.strip_cols)
+        return self._qw()
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         lead = x.shape[:-1]
         rows = x.reshape(-1, x.shape[-1]).contiguous()
-        y = matmul(rows, self._qw()) if self.bias is None else matmul_bias(rows, self._qw(), self.bias)
+        w = self._weight_for(rows.shape[0])
+        y = matmul(rows, w) if self.bias is None else matmul_bias(rows, w, self.bias)
         return y.reshape(*lead, self.N)

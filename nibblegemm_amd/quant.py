@@ -215,6 +215,55 @@ def split_swiglu(y: torch.Tensor):
     return (v[:, :, 0, :].reshape(rows, n2 // 2), v[:, :, 1, :].reshape(rows, n2 // 2))
 
 
+#: Strip widths of the strip-major layout (columns per strip).
+STRIP_COLS = (16, 32, 64)
+
+
+@dataclass(frozen=True)
+class StripMajorWeight:
+    """A quantised ``[K, N]`` weight in the strip-major layout of the decode
+    GEMV (an MI355X layout; the reference has only the packed one).  The N
+    columns are cut into strips of ``strip_cols`` and each strip is stored
+    whole: ``qweight`` int32 ``[N / strip_cols, K / 8, strip_cols]`` and
+    ``scales`` fp16 ``[N / strip_cols, K / group_size, strip_cols]`` hold the
+    words and scales of the packed layout, permuted (:func:`strip_major`).  A
+    decode workgroup then reads one contiguous run per strip.  Serves batches
+    of at most 8 rows (:func:`nibblegemm_amd.ops.to_strip_major` makes one on
+    the device)."""
+
+    qweight: torch.Tensor
+    scales: torch.Tensor
+    group_size: int
+    K: int
+    N: int
+    strip_cols: int
+
+    def to(self, device) -> "StripMajorWeight":
+        return dataclasses.replace(self, qweight=self.qweight.to(device),
+                                   scales=self.scales.to(device))
+
+    @property
+    def weight_bytes(self) -> int:
+        return sum(t.numel() * t.element_size() for t in (self.qweight, self.scales))
+
+
+def strip_major(qw: QuantizedWeight, strip_cols: int) -> StripMajorWeight:
+    """The strip-major copy of ``qw`` by tensor reshapes on its own device
+    (the layout's definition: word ``[s][r][j]`` is packed word ``[r][s *
+    strip_cols + j]``, scale ``[s][g][j]`` is scale ``[g][s * strip_cols +
+    j]``)."""
+    if strip_cols not in STRIP_COLS:
+        raise ValueError(f"strip_cols must be one of {STRIP_COLS}, got {strip_cols}")
+    if qw.N % strip_cols:
+        raise ValueError(f"N={qw.N} is not a multiple of strip_cols={strip_cols}")
+
+    def cut(t: torch.Tensor) -> torch.Tensor:
+        rows, n = t.shape
+        return t.reshape(rows, n // strip_cols, strip_cols).permute(1, 0, 2).contiguous()
+
+    return StripMajorWeight(cut(qw.qweight), cut(qw.scales), qw.group_size, qw.K, qw.N, strip_cols)
+
+
 def pack_nibbles(qu: np.ndarray) -> np.ndarray:
     """Codes ``[K, N]`` (values 0..15) to packed words ``int32 [K // 8, N]``
     (reference quant.py:164-182).  Each code is shifted to its nibble slot and
