@@ -36,7 +36,7 @@ from . import harness as H
 from . import ops, quant
 from .quant import QuantizedWeight, pack_nibbles
 
-DECODE_SHAPES = [(4096, 4096), (4096, 14336), (14336, 4096), (8192, 8192), (4096, 1024)]
+DECODE_SHAPES = [(4096, 4096), (4096, 14336), (14336, 4096), (8192, 8192), (4096, 1024), (4096, 6144)]
 PREFILL_SHAPES = [(4096, 14336), (14336, 4096)]
 TOL = 1e-2
 
@@ -124,10 +124,13 @@ def decode(args, rows):
     for K, N in DECODE_SHAPES:
         qws, gen = _weights(K, N, args.group_size, seed=K + N)
         w16 = _fp16_baseline(qws[0])
+        sms = H.Cycle(ops.to_strip_major(qw) for qw in qws.items)
         for M in args.M or [1, 2, 4, 8]:
             X = torch.randn((M, K), generator=gen).to(torch.float16).cuda()
             err = _check(ops.gemv(X, qws[0]), X, qws[0], f"gemv {M}x{K}x{N}")
+            sm_err = _check(ops.matmul(X, sms[0]), X, qws[0], f"strip-major {M}x{K}x{N}")
             t = H.bench_graph(lambda i: ops.gemv(X, qws[i]), reps=64, trials=args.trials)
+            ts = H.bench_graph(lambda i: ops.matmul(X, sms[i]), reps=64, trials=args.trials)
             f = H.bench_graph(lambda i: torch.mm(X, w16[i]), reps=64, trials=args.trials)
             d = H.bench_graph(lambda i: torch.mm(X, ops.dequant(qws[i])), reps=8, trials=args.trials)
             nb = H.total_bytes(M, K, N, args.group_size, 4)
@@ -139,12 +142,16 @@ def decode(args, rows):
                    "hipblaslt_fp16_us": round(f.median_ms * 1e3, 2),
                    "vs_fp16": round(f.median_ms / t.median_ms, 2),
                    "dequant+fp16_us": round(d.median_ms * 1e3, 2),
-                   "max_err_rms": float(f"{err:.2e}"), **_clock(t)}
+                   "max_err_rms": float(f"{err:.2e}"), **_clock(t),
+                   "strip_cols": sms[0].strip_cols, "strip_major_us": round(ts.median_ms * 1e3, 2),
+                   "strip_major_%8TB/s": round(100 * H.achieved_gbps(nb, ts.median_ms)
+                                               / H.HBM_PEAK_GBPS, 1),
+                   "strip_major_err_rms": float(f"{sm_err:.2e}")}
             if not args.no_cpu:
                 row.update(cpu_reference_ms(qws[0], X))
                 row["vs_cpu"] = round(row["cpu_ms"] / (t.median_ms), 0)
             _emit(rows, row)
-        del qws, w16
+        del qws, w16, sms
         torch.cuda.empty_cache()
 
 

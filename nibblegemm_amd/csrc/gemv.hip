@@ -180,6 +180,46 @@ __device__ __forceinline__ void norm_rows_to_lds(const GemvArgs& a, int m_base, 
   }
 }
 
+// norm_rows_to_lds for rows already copied to LDS: `xs` holds the raw
+// activation rows [mrows][K] and `ws` the norm weight [K]; each row is
+// normalised in place with norm_rows_to_lds's chunking and arithmetic (the
+// same bits).  Every chunk is read and written by the same thread.
+template <int THREADS>
+__device__ __forceinline__ void norm_rows_in_lds(const GemvArgs& a, int mrows, _Float16* xs,
+                                                 const _Float16* ws) {
+  static_assert(THREADS % kRmsThreads == 0, "the RMSNorm prologue runs on 256-thread multiples");
+  __shared__ float part[kRmsThreads / 64];
+  constexpr int kMaxChunks = kNormMaxK / (kRmsThreads * 8);
+  const int tid = threadIdx.x;
+  const bool active = THREADS == kRmsThreads || tid < kRmsThreads;
+  for (int r = 0; r < mrows; ++r) {
+    h8_t v[kMaxChunks], w[kMaxChunks];
+    float ss = 0.0f;
+    if (active) {
+#pragma unroll
+      for (int c = 0; c < kMaxChunks; ++c) {
+        const int col = (c * kRmsThreads + tid) * 8;
+        v[c] = col < a.K ? *reinterpret_cast<const h8_t*>(&xs[r * a.K + col]) : h8_t{};
+        w[c] = col < a.K ? *reinterpret_cast<const h8_t*>(&ws[col]) : h8_t{};
+        ss = sumsq_chunk(v[c], ss);
+      }
+      ss = wave_sum(ss);
+      if ((tid & 63) == 0) part[tid >> 6] = ss;
+    }
+    __syncthreads();
+    const float total = ((part[0] + part[1]) + part[2]) + part[3];
+    if (active) {
+      const float rr = rms_scale(total, a.K, a.norm_eps);
+#pragma unroll
+      for (int c = 0; c < kMaxChunks; ++c) {
+        const int col = (c * kRmsThreads + tid) * 8;
+        if (col < a.K) *reinterpret_cast<h8_t*>(&xs[r * a.K + col]) = rms_apply(v[c], w[c], rr);
+      }
+    }
+    __syncthreads();  // before `part` is written again, and before the loop reads xs
+  }
+}
+
 // STREAM: the launch reads every weight exactly once (a single row block), so
 // packed words and scales are loaded with the non-temporal hint -- measured
 // 1-2% faster at M <= 32; launches of several row blocks re-read the weights
@@ -479,7 +519,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_strip_kernel(GemvArgs a) {
   static_assert(DEPTH >= 2, "the ring prepares the next stage while computing this one");
   constexpr int kWPolicy = 2;            // non-temporal: the launch reads each weight once
   __shared__ __attribute__((aligned(16))) float red[WAVES][P][MT][SW];
-  // STAGED: [MT][K] activation rows, then [K / GROUP][SW] scales.
+  // STAGED: [MT][K] activation rows, (NORM) the [K] norm weight, then
+  // [K / GROUP][SW] scales.
   extern __shared__ __attribute__((aligned(16))) _Float16 xnorm[];
 
   // The grid is rounded up to whole XCD runs; a workgroup past the last
@@ -517,19 +558,30 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_strip_kernel(GemvArgs a) {
     const uint32_t m = t * RPT + mm;
     voff_x[t] = m < static_cast<uint32_t>(mrows) ? (m * K + kx_lane) * 2u : kOutOfRange;
   }
-  _Float16* const s_lds = xnorm + MT * K;  // STAGED scales
+  _Float16* const wn_lds = xnorm + MT * K;                     // NORM weight
+  _Float16* const s_lds = wn_lds + (NORM ? K : 0u);              // STAGED scales
 
   // STAGED: LDS-DMA copies of the activation rows and the strip's scales,
   // 16 bytes per lane, block i of a region landing at byte 1024 i; lanes
   // past the end are masked off.
   auto stage_to_lds = [&]() {
     using lds_ptr = __attribute__((address_space(3))) void*;
-    if constexpr (!NORM) {
+    {
       const uint32_t chunks = static_cast<uint32_t>(mrows) * K / 8;
       for (uint32_t blk = wave; blk * 64 < chunks; blk += WAVES) {
         const uint32_t ch = blk * 64 + lane;
         if (ch < chunks)
           __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr)(xnorm + blk * 512), 16, ch * 16u,
+                                                   0, 0, 0);
+      }
+    }
+    if constexpr (NORM) {
+      const __amdgpu_buffer_rsrc_t rn = make_rsrc(a.norm_w, K * 2u);
+      const uint32_t chunks = K / 8;
+      for (uint32_t blk = wave; blk * 64 < chunks; blk += WAVES) {
+        const uint32_t ch = blk * 64 + lane;
+        if (ch < chunks)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rn, (lds_ptr)(wn_lds + blk * 512), 16, ch * 16u,
                                                    0, 0, 0);
       }
     }
@@ -668,10 +720,12 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_strip_kernel(GemvArgs a) {
     load(st[d], d);
     __builtin_amdgcn_sched_barrier(0);
   }
-  if constexpr (NORM) norm_rows_to_lds<THREADS>(a, 0, mrows, xnorm);
   // Every wave's LDS-DMA copies have landed (each waits for its own, the
-  // barrier for the others').
-  if constexpr (STAGED && !NORM) __syncthreads();
+  // barrier for the others').  The RMSNorm prologue then normalises the
+  // staged rows in place: its inputs were copied ahead of the weight loads,
+  // so its wait does not include them.
+  if constexpr (STAGED) __syncthreads();
+  if constexpr (NORM) norm_rows_in_lds<THREADS>(a, mrows, xnorm, wn_lds);
   if constexpr (ONEPASS) {
     // Every group of the wave is already in flight (n <= DEPTH).
     if constexpr (STAGED) {
@@ -859,7 +913,8 @@ hipError_t launch_strip_geometry(const GemvArgs& a, hipStream_t stream) {
     // always stages, and is only planned when they fit).
     const bool onepass = (a.K / GROUP + WAVES - 1) / WAVES <= DEPTH;
     const size_t xbytes = static_cast<size_t>(MT) * a.K * sizeof(_Float16);
-    const size_t lds = xbytes + static_cast<size_t>(a.K / GROUP) * SW * sizeof(_Float16);
+    const size_t nbytes = a.norm_w != nullptr ? static_cast<size_t>(a.K) * sizeof(_Float16) : 0;
+    const size_t lds = xbytes + nbytes + static_cast<size_t>(a.K / GROUP) * SW * sizeof(_Float16);
     const bool staged = a.norm_w != nullptr || xbytes <= 65536;
     if (a.norm_w != nullptr) {
       if (onepass)

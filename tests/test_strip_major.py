@@ -210,7 +210,7 @@ def test_swiglu_epilogue_is_the_fp16_composition(M, K, Nh, sw):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("M,K,N,sw", [(1, 4096, 6144, 32), (4, 4096, 1024, 16), (8, 2048, 28672, 64),
-                                      (1, 14336, 4096, 16)])
+                                      (1, 14336, 4096, 16), (8, 4096, 6144, 32), (3, 8192, 512, 64)])
 def test_rmsnorm_prologue_is_the_two_step_composition(M, K, N, sw):
     _, _, _, Xd, _, sm = strip_case(M, K, N, 128, sw, seed=5)
     w = (torch.rand(K, generator=torch.Generator().manual_seed(K)) + 0.5).half().cuda()
