@@ -323,6 +323,24 @@ def bench_graph_pair(fn_a: Callable[[int], object], fn_b: Callable[[int], object
     return tuple(_summarise(s, trials, reps, clocks) for s in samples)
 
 
+def spin_up(seconds: float = 0.3) -> None:
+    """Keep the GPU busy with device copies for about ``seconds`` so the
+    shader clock is at its loaded level before a sweep's first timing."""
+    src = torch.empty(64 << 20, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    dst.copy_(src)
+    end.record()
+    end.synchronize()
+    per = max(start.elapsed_time(end) / 1e3, 1e-6)
+    for _ in range(max(1, math.ceil(seconds / per))):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+
 def measured_copy_gbps(size_bytes: int = 2 << 30) -> float:
     """Achievable HBM bandwidth: a large device copy, read + write counted."""
     n = size_bytes // 2
