@@ -64,6 +64,7 @@ struct GemvArgs {
   float norm_eps;
   int strips;             // strip kernel: column strips of the launch
   int strips_per_xcd;     // strip kernel: strips run by each XCD's workgroups
+  int stage_x;            // strip kernel: copy the activations to LDS (if they fit 64 KiB)
   // Strip kernel addressing, in bytes.  Word (packed row r, strip column
   // 4 c + j) of strip s is at s * w_strip + r * w_row + 16 c + 4 j; the scale
   // of (group g, strip column j) at s * s_strip + g * s_row + 2 j.  The
@@ -915,7 +916,7 @@ hipError_t launch_strip_geometry(const GemvArgs& a, hipStream_t stream) {
     const size_t xbytes = static_cast<size_t>(MT) * a.K * sizeof(_Float16);
     const size_t nbytes = a.norm_w != nullptr ? static_cast<size_t>(a.K) * sizeof(_Float16) : 0;
     const size_t lds = xbytes + nbytes + static_cast<size_t>(a.K / GROUP) * SW * sizeof(_Float16);
-    const bool staged = a.norm_w != nullptr || xbytes <= 65536;
+    const bool staged = a.norm_w != nullptr || (a.stage_x && xbytes <= 65536);
     if (a.norm_w != nullptr) {
       if (onepass)
         gemv_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, true, true, true><<<grid, WAVES * 64, lds, stream>>>(a);
@@ -1058,18 +1059,21 @@ int plan_stream(int64_t M, int64_t K, int64_t N, int64_t G, bool split_k, int64_
 
 // Strip width for strip-major weights (the layout fixes it, so it is chosen
 // once, when the weight is packed).  Measured on MI355X, M = 1, graph replay,
-// strip-major against the packed layout at the same geometry and against
-// the packed layout's own plan: 14336 x 4096 7.6 us with 16-column strips
-// (split kernel 9.5); 4096 x 1024 3.7 (4.3); 4096 x 4096 4.5 (4.7);
-// 4096 x 6144 4.8 (5.5); 4096 x 14336 7.2 (7.3); 4096 x 28672 12.1 (13.0);
-// 8192 x 8192 8.0 (9.2).  Narrow strips of the packed layout read 64 or 128
-// contiguous bytes per packed row, 4 N bytes apart, which HBM serves at a
-// fraction of its streaming rate; a strip-major strip is one contiguous run.
+// strip-major against the packed layout's own plan: 14336 x 4096 7.6 us with
+// 16-column strips (split kernel 9.5); 4096 x 1024 3.7 (4.3); 4096 x 4096
+// 4.1 with 16-column strips reading the activations per lane (4.7; 4.5 with
+// 32-column strips); 4096 x 6144 4.8 (5.5); 4096 x 14336 7.2 (7.3);
+// 4096 x 28672 12.1 (13.0); 8192 x 8192 8.0 (9.2).  Narrow strips of the
+// packed layout read 64 or 128 contiguous bytes per packed row, 4 N bytes
+// apart, which HBM serves at a fraction of its streaming rate; a strip-major
+// strip is one contiguous run.
 int64_t strip_major_cols(int64_t K, int64_t N, int64_t G) {
   if (K <= 0 || N <= 0 || (G != 64 && G != 128) || K % G != 0) return 0;
   if (N >= kStripWideN && N % 64 == 0) return 64;
   const bool narrow = G == 128 && N % 16 == 0;  // a 16-column wave load spans 128 k
-  if (narrow && (N <= 2048 || K >= 12288)) return 16;  // too few 32-column strips to fill the chip
+  // Too few 32-column strips to fill the chip, or (K <= 4096, N <= 4096)
+  // 16-column strips measured faster.
+  if (narrow && (N <= 2048 || K >= 12288 || (K <= 4096 && N <= 4096))) return 16;
   if (N % 32 == 0) return 32;
   return narrow ? 16 : 0;
 }
@@ -1088,6 +1092,10 @@ bool plan_strip_major(int64_t M, int64_t K, int64_t N, int64_t G, int64_t SW, St
   // wider strips hold enough bytes with 2.
   q.waves = SW == 64 ? 4 : 8;
   q.depth = SW == 16 ? 4 : 2;
+  // 16-column strips over a short K read their activations per lane with
+  // the weights: at 4096 x 4096 4.1 us against 4.4 staged (equal at
+  // 4096 x 1024; staging wins from K = 14336: 7.6 against 8.3).
+  q.stage_x = !(SW == 16 && K <= 4096);
   q.strips = static_cast<int>(N / SW);
   q.counter_bytes = 0;
   q.workspace_bytes = 0;
@@ -1147,6 +1155,7 @@ int launch_stream_split(const void* X, const void* Wq, const void* S, void* Y, i
     a.strips = p.strips;
     a.strips_per_xcd = static_cast<int>(ceil_div(p.strips, 8));
     const uint32_t sw = static_cast<uint32_t>(p.strip_cols);
+    a.stage_x = p.stage_x ? 1 : 0;
     if (strip_major) {
       a.w_row = sw * 4u;
       a.w_strip = static_cast<uint32_t>(K / 8) * sw * 4u;

@@ -33,6 +33,7 @@ struct StreamPlan {
   int groups_per_split = 0;
   int strip_cols = 64;  // strip kernel: 16, 32 or 64
   int depth = 2;        // strip kernel: groups in flight per wave
+  bool stage_x = true;  // strip kernel: activations copied to LDS (when they fit 64 KiB)
   size_t counter_bytes = 0;
   size_t workspace_bytes = 0;
 };
