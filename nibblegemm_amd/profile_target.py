@@ -8,7 +8,10 @@ holds only that kernel (plus setup copies).
     python3 -m nibblegemm_amd.profile_target gemm --M 2048 --K 4096 --N 14336 --calls 10
     python3 -m nibblegemm_amd.profile_target gemm --M 4096 --K 14336 --N 4096 --version 7
     python3 -m nibblegemm_amd.profile_target copy --mib 256 --calls 20
+    python3 -m nibblegemm_amd.profile_target fp16mm --M 2048 --K 4096 --N 14336 --calls 10
 
+``fp16mm`` is the baseline the prefill GEMM is compared with: ``torch.mm``
+(hipBLASLt) on fp16 weights of the same shape, rotated the same way.
 ``copy`` is the calibration kernel for the HBM byte counters: a device copy
 of a known size (reads and writes ``--mib`` MiB each), so FETCH_SIZE and
 WRITE_SIZE per dispatch can be scaled to bytes.  The weights of gemv,
@@ -39,7 +42,7 @@ def _weights(K: int, N: int, G: int, dev):
 
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
-    ap.add_argument("kernel", choices=["gemv", "gemm", "dequant", "copy"])
+    ap.add_argument("kernel", choices=["gemv", "gemm", "dequant", "copy", "fp16mm"])
     ap.add_argument("--M", type=int, default=1)
     ap.add_argument("--K", type=int, default=4096)
     ap.add_argument("--N", type=int, default=14336)
@@ -60,6 +63,14 @@ def main(argv=None) -> int:
         torch.cuda.synchronize()
         for _ in range(args.calls):
             dst.copy_(src)
+    elif args.kernel == "fp16mm":
+        qws, gen = _weights(args.K, args.N, args.G, dev)
+        X = torch.randn((args.M, args.K), generator=gen).to(torch.float16).to(dev)
+        w16 = H.Rotation(ops.dequant(qws[0]))
+        torch.backends.cuda.matmul.allow_tf32 = False
+        torch.cuda.synchronize()
+        for i in range(args.calls):
+            torch.mm(X, w16[i])
     else:
         qws, gen = _weights(args.K, args.N, args.G, dev)
         X = torch.randn((args.M, args.K), generator=gen).to(torch.float16).to(dev)
