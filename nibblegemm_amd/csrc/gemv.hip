@@ -409,14 +409,17 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs a) {
   // quad e % 8 and up quad e % 8 + 8 of the strip.
   const bool direct = a.splits == 1;
   auto wave_sum = [&](int r, int qq) {
-    f4_t sum = red[0][r][qq];
+    f4_t v[WAVES];
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) v[w] = red[w][r][qq];
+    __builtin_amdgcn_sched_barrier(0);  // every read ahead of the adds
+    f4_t sum = v[0];
 #pragma unroll
     for (int w = 1; w < WAVES; ++w) {
-      const f4_t v = red[w][r][qq];
-      sum[0] += v[0];
-      sum[1] += v[1];
-      sum[2] += v[2];
-      sum[3] += v[3];
+      sum[0] += v[w][0];
+      sum[1] += v[w][1];
+      sum[2] += v[w][2];
+      sum[3] += v[w][3];
     }
     return sum;
   };
@@ -452,13 +455,29 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs a) {
   __syncthreads();
   if (!s_last) return;
 
+  // The partials of up to kSplitBatch splits are loaded in one round and then
+  // added in split order: one memory round trip per batch instead of one per
+  // split.  Loads past the last split re-read split 0 and are not added.
   auto split_sum = [&](int r, int qq) {
+    constexpr int kSplitBatch = 8;
     const int ocol = strip * kStripCols + 4 * qq;
     f4_t sum = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int sp = 0; sp < a.splits; ++sp) {
-      const float* src = a.partial + (static_cast<size_t>(sp) * a.M + m_base + r) * a.N + ocol;
+    for (int sp0 = 0; sp0 < a.splits; sp0 += kSplitBatch) {
+      f4_t v[kSplitBatch];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) sum[c] += load_coherent(src + c);
+      for (int b = 0; b < kSplitBatch; ++b) {
+        const int sp = sp0 + b < a.splits ? sp0 + b : 0;
+        const float* src = a.partial + (static_cast<size_t>(sp) * a.M + m_base + r) * a.N + ocol;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) v[b][c] = load_coherent(src + c);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int b = 0; b < kSplitBatch; ++b)
+        if (sp0 + b < a.splits) {
+#pragma unroll
+          for (int c = 0; c < 4; ++c) sum[c] += v[b][c];
+        }
     }
     return sum;
   };
@@ -780,18 +799,30 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_strip_kernel(GemvArgs a) {
       }
     }
   __syncthreads();
+  // Sum the WAVES * P partials of an output quad in (wave, phase) order.  The
+  // reads go out in batches of up to 16 ahead of their adds (a scheduling
+  // barrier keeps the compiler from interleaving each read with its add,
+  // which exposed the LDS latency once per partial).
   auto strip_sum = [&](int row, int qq) {
+    constexpr int E = WAVES * P;
+    constexpr int BATCH = E < 16 ? E : 16;
+    static_assert(E % BATCH == 0, "whole batches");
     f4_t sum = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int w = 0; w < WAVES; ++w)
+    for (int e0 = 0; e0 < E; e0 += BATCH) {
+      f4_t v[BATCH];
 #pragma unroll
-      for (int p = 0; p < P; ++p) {
-        const f4_t v = *reinterpret_cast<const f4_t*>(&red[w][p][row][4 * qq]);
-        sum[0] += v[0];
-        sum[1] += v[1];
-        sum[2] += v[2];
-        sum[3] += v[3];
+      for (int b = 0; b < BATCH; ++b)
+        v[b] = *reinterpret_cast<const f4_t*>(&red[(e0 + b) / P][(e0 + b) % P][row][4 * qq]);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int b = 0; b < BATCH; ++b) {
+        sum[0] += v[b][0];
+        sum[1] += v[b][1];
+        sum[2] += v[b][2];
+        sum[3] += v[b][3];
       }
+    }
     return sum;
   };
   emit_outputs<MT, THREADS, SW>(a, strip, 0, mrows, strip_sum);
