@@ -137,6 +137,44 @@ struct TileArgs {
   int splits;
 };
 
+// Last-arriver sum of one lane's 16 accumulator rows of a 32 x 32 MFMA tile
+// (rows row0 + 8 (r / 4) + r % 4, column gn) over every K split, in split
+// order, then the fp16 store.  Up to 4 splits' partials are loaded in one
+// round before their adds: one memory round trip per 4 splits instead of one
+// per split and element.  Rows past M load a valid row and are not stored.
+__device__ __forceinline__ void sum_splits_store(const TileArgs& args, int gn, int row0) {
+  constexpr int kBatch = 4;
+  const int M = args.M, N = args.N;
+  float sum[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) sum[r] = 0.0f;
+  for (int sp0 = 0; sp0 < args.splits; sp0 += kBatch) {
+    float v[kBatch][16];
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      const int sp = sp0 + b < args.splits ? sp0 + b : 0;
+      const float* part = args.partial + static_cast<size_t>(sp) * M * N + gn;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int gm = row0 + 8 * (r >> 2) + (r & 3);
+        v[b][r] = load_coherent(part + static_cast<size_t>(gm < M ? gm : 0) * N);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b)
+      if (sp0 + b < args.splits) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sum[r] += v[b][r];
+      }
+  }
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int gm = row0 + 8 * (r >> 2) + (r & 3);
+    if (gm < M) args.Y[static_cast<size_t>(gm) * N + gn] = (_Float16)sum[r];
+  }
+}
+
 template <int BM, int BN, int GROUP>
 __global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(1, 2))) void
 gemm_tile_kernel(TileArgs args) {
@@ -346,16 +384,7 @@ gemm_tile_kernel(TileArgs args) {
     for (int j = 0; j < C::TN; ++j) {
       const int gn = n0 + wn + 32 * j + r32;
       if (gn >= N) continue;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int gm = m0 + wm + 32 * i + 8 * (r >> 2) + rq + (r & 3);
-        if (gm >= M) continue;
-        const size_t off = static_cast<size_t>(gm) * N + gn;
-        float sum = 0.0f;
-        for (int sp = 0; sp < args.splits; ++sp)
-          sum += load_coherent(args.partial + static_cast<size_t>(sp) * M * N + off);
-        Y[off] = (_Float16)sum;
-      }
+      sum_splits_store(args, gn, m0 + wm + 32 * i + rq);
     }
   if (tid == 0)
     __hip_atomic_store(args.counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -421,16 +450,7 @@ __device__ __forceinline__ void pc_epilogue(const f16_t (&acc)[TM][TN], const Ti
     for (int j = 0; j < TN; ++j) {
       const int gn = nw + 32 * j + r32;
       if (gn >= N) continue;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int gm = mw + 32 * i + 8 * (r >> 2) + rq + (r & 3);
-        if (gm >= M) continue;
-        const size_t off = static_cast<size_t>(gm) * N + gn;
-        float sum = 0.0f;
-        for (int sp = 0; sp < args.splits; ++sp)
-          sum += load_coherent(args.partial + static_cast<size_t>(sp) * M * N + off);
-        Y[off] = (_Float16)sum;
-      }
+      sum_splits_store(args, gn, mw + 32 * i + rq);
     }
   if (threadIdx.x == 0)
     __hip_atomic_store(args.counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -877,17 +897,28 @@ TilePlan plan_tile(int64_t M, int64_t K, int64_t N, int64_t version, int bn_max)
     tiles = t256;
   } else if (K % 64 == 0 && bn_max >= 256) {
     // The producer/consumer kernel wherever it applies (whole 64-k steps,
-    // 16-byte packed-word loads).  Measured on MI355X over M = 160..2048 at
-    // 4096 x 14336 and 14336 x 4096: 128-row tiles win once the launch has
-    // ~192 of them (4096 x 14336 from M = 160, 14336 x 4096 from M = 768),
-    // 64-row tiles below; a K split pays only for long K with at most 128
-    // tiles, two ways there (M = 160 at 14336 x 4096: 75 -> 64 us), while
-    // more splits, or splits of larger grids, lose to the partial exchange.
+    // 16-byte packed-word loads).  Measured on MI355X, graph replay:
+    //  * K < 8192 (no split): 128-row tiles once the launch has ~192 of them
+    //    (4096 x 14336 from M = 160), 64-row tiles below;
+    //  * K >= 8192: 128-row tiles, split over K by the tile count -- at
+    //    14336 x 4096, M = 160 / 256 (64 tiles) 4 ways: 44 / 46 us (64-row
+    //    tiles, 2 ways: 58 / 59); M = 384 / 512 (96 / 128 tiles) 2 ways:
+    //    74 / 77 us (97 / 101); M = 768 / 1024 (192 / 256 tiles) unsplit;
+    //    M = 1536 (384 tiles, a round and a half) 2 ways: 221 us (242
+    //    unsplit); M = 2048 (512 tiles) unsplit.  The split's partials are
+    //    summed by the last workgroup of each tile, every split's loads in
+    //    one round.
     const int64_t t128 = ceil_div(M, 128) * ceil_div(N, 128);
-    p.t = TileChoice{version == 7 || t128 >= 192 ? 128 : 64, 128, true};
+    p.t = TileChoice{version == 7 || K >= 8192 || t128 >= 192 ? 128 : 64, 128, true};
     tiles = ceil_div(M, p.t.bm) * ceil_div(N, 128);
-    if (K >= 8192 && tiles <= 128)
-      splits = static_cast<int>(std::min<int64_t>(ceil_div(192, tiles), 4));
+    if (K >= 8192) {
+      if (tiles <= 64)
+        splits = 4;
+      else if (tiles <= 128)
+        splits = 2;
+      else if (tiles > kPlanCUs && tiles < 2 * kPlanCUs)
+        splits = 2;
+    }
   } else {
     p.t = version == 7 ? TileChoice{128, std::min(128, bn_max)} : choose_tile(M, N, bn_max);
     tiles = ceil_div(M, p.t.bm) * ceil_div(N, p.t.bn);

@@ -103,17 +103,24 @@ def test_gemm_workspace_formula():
     # M = 33 streams in two 32-row blocks: 112 groups split 4 ways, counters
     # for 64 strips x 2 blocks
     assert ext.gemm_workspace_bytes(33, 14336, 4096, 128, 6, None) == (512 + 4 * 33 * 4096 * 4, 512)
-    # M > 128 runs the producer/consumer kernel: 64 x 128 tiles here (2 x 32
-    # of 128 x 128 would be too few), 3 x 32 = 96 of them over a long K (224
-    # steps of 64) split 2 ways; counters padded to 512 bytes
-    assert ext.gemm_workspace_bytes(129, 14336, 4096, 128, 6, None) == (512 + 2 * 129 * 4096 * 4, 512)
-    # version 7 keeps 128 x 128 tiles: 2 x 32 = 64 of them, split 3 ways
-    assert ext.gemm_workspace_bytes(129, 14336, 4096, 128, 7, None) == (256 + 3 * 129 * 4096 * 4, 256)
+    # M > 128 runs the producer/consumer kernel; over a long K (224 steps of
+    # 64) with 128 x 128 tiles split by their count: 2 x 32 = 64 tiles 4 ways
+    # (both versions: the same plan, so the same bits)
+    assert ext.gemm_workspace_bytes(129, 14336, 4096, 128, 6, None) == (256 + 4 * 129 * 4096 * 4, 256)
+    assert ext.gemm_workspace_bytes(129, 14336, 4096, 128, 7, None) == (256 + 4 * 129 * 4096 * 4, 256)
+    # 3 x 32 = 96 and 4 x 32 = 128 tiles split 2 ways; 1536 rows (384 tiles,
+    # a round and a half of the CUs) 2 ways; counters padded to 512 bytes
+    assert ext.gemm_workspace_bytes(384, 14336, 4096, 128, 6, None) == (512 + 2 * 384 * 4096 * 4, 512)
+    assert ext.gemm_workspace_bytes(512, 14336, 4096, 128, 6, None) == (512 + 2 * 512 * 4096 * 4, 512)
+    assert ext.gemm_workspace_bytes(1536, 14336, 4096, 128, 6, None) == \
+        (1536 + 2 * 1536 * 4096 * 4, 1536)
     # N % 4 != 0 cannot stream nor take 16-byte B loads: the tile kernel, 33
     # tiles of 64 x 128, split 4 ways
     assert ext.gemm_workspace_bytes(16, 14336, 4098, 128, 6, None) == (256 + 4 * 16 * 4098 * 4, 256)
-    # M = 512: 256 tiles of 64 x 128, enough not to split; a short K never splits
-    assert ext.gemm_workspace_bytes(512, 14336, 4096, 128, 6, None) == (0, 0)
+    # 192 and 256 tiles of 128 x 128 are not split; a short K never splits
+    assert ext.gemm_workspace_bytes(768, 14336, 4096, 128, 6, None) == (0, 0)
+    assert ext.gemm_workspace_bytes(1024, 14336, 4096, 128, 7, None) == (0, 0)
+    assert ext.gemm_workspace_bytes(512, 4096, 14336, 128, 6, None) == (0, 0)
     assert ext.gemm_workspace_bytes(64, 4096, 14336, 128, 6, None) == (0, 0)
     # from M = 1024 version 6 takes 256 x 256 tiles where they make one round
     # of the CUs (224 tiles here), never split; 2048 x 4096 has 512 tiles of
