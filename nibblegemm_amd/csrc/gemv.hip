@@ -692,6 +692,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_strip_kernel(GemvArgs a) {
       }
       st.corr[t] = corr;
     }
+    // The group's scales, read a stage ahead of their use.
+    if constexpr (STAGED) st.s = *reinterpret_cast<const h4_t*>(&s_lds[st.g * SW + 4 * c]);
   };
   auto compute = [&](const Stage& st) {
     f4_t acc[TILES][4];
@@ -707,11 +709,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_strip_kernel(GemvArgs a) {
 #pragma unroll
         for (int t = 0; t < TILES; ++t) acc[t][j] = mfma16(st.x[t][cc], b, acc[t][j]);
       }
-    h4_t sc;
-    if constexpr (STAGED)
-      sc = *reinterpret_cast<const h4_t*>(&s_lds[st.g * SW + 4 * c]);
-    else
-      sc = st.s;
+    const h4_t sc = st.s;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const float sj = static_cast<float>(sc[j]);
