@@ -292,8 +292,11 @@ __global__ __launch_bounds__(kGlueThreads) void attention_decode_kernel(AttnArgs
   }
   for (int e = tid; e < a.chunks * QPK; e += kGlueThreads) {
     const float* P = chunk_part(e / QPK, e % QPK);
-    wchunk[e / QPK][e % QPK] = load_coherent(P);
-    lchunk[e / QPK][e % QPK] = load_coherent(P + 1);
+    const float mx = load_coherent(P);
+    const float sm = load_coherent(P + 1);
+    __builtin_amdgcn_sched_barrier(0);  // both loads in flight before either store waits
+    wchunk[e / QPK][e % QPK] = mx;
+    lchunk[e / QPK][e % QPK] = sm;
   }
   __syncthreads();
   // Per head, over the chunks in order: the global max M, the chunk weights
