@@ -137,41 +137,64 @@ struct TileArgs {
   int splits;
 };
 
-// Last-arriver sum of one lane's 16 accumulator rows of a 32 x 32 MFMA tile
-// (rows row0 + 8 (r / 4) + r % 4, column gn) over every K split, in split
-// order, then the fp16 store.  Up to 4 splits' partials are loaded in one
-// round before their adds: one memory round trip per 4 splits instead of one
-// per split and element.  Rows past M load a valid row and are not stored.
-__device__ __forceinline__ void sum_splits_store(const TileArgs& args, int gn, int row0) {
-  constexpr int kBatch = 4;
+// Last-arriver sum of a split output tile [m0, m0 + BM) x [n0, n0 + BN) by
+// the whole workgroup: each thread takes 16-byte chunks of 4 columns and
+// loads the chunk's partial of every split (up to 4 in one round, with the
+// same device-coherent cache policy as load_coherent) before adding them in
+// split order, then stores the 4 fp16 results.  Chunks go two at a time, so
+// a thread has at most 8 loads in flight and the kernels keep their
+// register budget.  Needs N % 4 == 0 (16-byte partial rows, 8-byte output
+// stores) and M * N * 4 < 2^31 (32-bit buffer offsets; the plans split only
+// grids of a few hundred tiles).
+template <int THREADS, int BM, int BN>
+__device__ __forceinline__ void tile_sum_splits(const TileArgs& args, int m0, int n0) {
+  constexpr int QUADS = BN / 4;
+  constexpr int CHUNKS = BM * QUADS;
+  constexpr int kPair = 2, kBatch = 4;
+  static_assert(CHUNKS % (THREADS * kPair) == 0, "whole rounds of chunk pairs");
+  constexpr uint32_t kCoherent = 16;  // sc1: the cache policy of an agent-scope load
   const int M = args.M, N = args.N;
-  float sum[16];
+  const uint32_t plane = static_cast<uint32_t>(M) * static_cast<uint32_t>(N);
+#pragma nounroll
+  for (int c0 = 0; c0 < CHUNKS; c0 += THREADS * kPair) {
+    uint32_t off[kPair];
+    bool ok[kPair];
 #pragma unroll
-  for (int r = 0; r < 16; ++r) sum[r] = 0.0f;
-  for (int sp0 = 0; sp0 < args.splits; sp0 += kBatch) {
-    float v[kBatch][16];
-#pragma unroll
-    for (int b = 0; b < kBatch; ++b) {
-      const int sp = sp0 + b < args.splits ? sp0 + b : 0;
-      const float* part = args.partial + static_cast<size_t>(sp) * M * N + gn;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int gm = row0 + 8 * (r >> 2) + (r & 3);
-        v[b][r] = load_coherent(part + static_cast<size_t>(gm < M ? gm : 0) * N);
-      }
+    for (int u = 0; u < kPair; ++u) {
+      const int c = c0 + u * THREADS + static_cast<int>(threadIdx.x);
+      const int gm = m0 + c / QUADS, gn = n0 + 4 * (c % QUADS);
+      ok[u] = gm < M && gn < N;
+      off[u] = ok[u] ? (static_cast<uint32_t>(gm) * N + gn) * 4u : kOutOfRange;
     }
-    __builtin_amdgcn_sched_barrier(0);
+    f4_t sum[kPair] = {};
+    for (int sp0 = 0; sp0 < args.splits; sp0 += kBatch) {
+      f4_t v[kBatch][kPair];
 #pragma unroll
-    for (int b = 0; b < kBatch; ++b)
-      if (sp0 + b < args.splits) {
+      for (int b = 0; b < kBatch; ++b) {
+        const int sp = sp0 + b < args.splits ? sp0 + b : 0;
+        const __amdgpu_buffer_rsrc_t rp =
+            make_rsrc(args.partial + static_cast<size_t>(sp) * plane, plane * 4u);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) sum[r] += v[b][r];
+        for (int u = 0; u < kPair; ++u)
+          v[b][u] = __builtin_bit_cast(
+              f4_t, __builtin_amdgcn_raw_buffer_load_b128(rp, off[u], 0, kCoherent));
       }
-  }
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int gm = row0 + 8 * (r >> 2) + (r & 3);
-    if (gm < M) args.Y[static_cast<size_t>(gm) * N + gn] = (_Float16)sum[r];
+      for (int b = 0; b < kBatch; ++b)
+        if (sp0 + b < args.splits) {
+#pragma unroll
+          for (int u = 0; u < kPair; ++u)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sum[u][e] += v[b][u][e];
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < kPair; ++u)
+      if (ok[u]) {
+        const h4_t y = {(_Float16)sum[u][0], (_Float16)sum[u][1], (_Float16)sum[u][2],
+                        (_Float16)sum[u][3]};
+        *reinterpret_cast<h4_t*>(args.Y + off[u] / 4) = y;
+      }
   }
 }
 
@@ -378,14 +401,27 @@ gemm_tile_kernel(TileArgs args) {
   }
   __syncthreads();
   if (!s_last) return;
+  if (N % 4 == 0) {
+    tile_sum_splits<kGemmThreads, BM, BN>(args, m0, n0);
+  } else {
 #pragma unroll
-  for (int i = 0; i < C::TM; ++i)
+    for (int i = 0; i < C::TM; ++i)
 #pragma unroll
-    for (int j = 0; j < C::TN; ++j) {
-      const int gn = n0 + wn + 32 * j + r32;
-      if (gn >= N) continue;
-      sum_splits_store(args, gn, m0 + wm + 32 * i + rq);
-    }
+      for (int j = 0; j < C::TN; ++j) {
+        const int gn = n0 + wn + 32 * j + r32;
+        if (gn >= N) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int gm = m0 + wm + 32 * i + 8 * (r >> 2) + rq + (r & 3);
+          if (gm >= M) continue;
+          const size_t off = static_cast<size_t>(gm) * N + gn;
+          float sum = 0.0f;
+          for (int sp = 0; sp < args.splits; ++sp)
+            sum += load_coherent(args.partial + static_cast<size_t>(sp) * M * N + off);
+          Y[off] = (_Float16)sum;
+        }
+      }
+  }
   if (tid == 0)
     __hip_atomic_store(args.counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -393,7 +429,7 @@ gemm_tile_kernel(TileArgs args) {
 // Epilogue of the producer/consumer kernels: the consumer waves hold the
 // results (wave block top-left (mw, nw), the tile kernel's register layout);
 // every wave passes the barriers of the K-split exchange.
-template <int TM, int TN>
+template <int TM, int TN, int THREADS, int BM, int BN, bool CAN_SPLIT = true>
 __device__ __forceinline__ void pc_epilogue(const f16_t (&acc)[TM][TN], const TileArgs& args,
                                             bool producer, int mw, int nw, int& s_last) {
   const int M = args.M, N = args.N;
@@ -401,7 +437,8 @@ __device__ __forceinline__ void pc_epilogue(const f16_t (&acc)[TM][TN], const Ti
   const int r32 = lane & 31;
   const int rq = (lane >> 5) * 4;
   _Float16* __restrict__ Y = args.Y;
-  if (args.splits == 1) {
+  // The large-tile kernel never splits K (CAN_SPLIT false): only this path.
+  if (!CAN_SPLIT || args.splits == 1) {
     if (producer) return;
 #pragma unroll
     for (int i = 0; i < TM; ++i)
@@ -443,15 +480,10 @@ __device__ __forceinline__ void pc_epilogue(const f16_t (&acc)[TM][TN], const Ti
     s_last = (prev == static_cast<uint32_t>(args.splits - 1));
   }
   __syncthreads();
-  if (!s_last || producer) return;
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int gn = nw + 32 * j + r32;
-      if (gn >= N) continue;
-      sum_splits_store(args, gn, mw + 32 * i + rq);
-    }
+  if (!s_last) return;
+  // Every wave (producers too) sums the tile: N % 4 == 0 for these kernels.
+  tile_sum_splits<THREADS, BM, BN>(args, static_cast<int>(blockIdx.y) * BM,
+                                   static_cast<int>(blockIdx.x) * BN);
   if (threadIdx.x == 0)
     __hip_atomic_store(args.counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -615,7 +647,8 @@ __global__ __launch_bounds__(2 * kGemmThreads) void gemm_pc64_kernel(TileArgs ar
       __syncthreads();
     }
   }
-  pc_epilogue<C::TM, C::TN>(acc, args, producer, m0 + wm, n0 + wn, s_last);
+  pc_epilogue<C::TM, C::TN, 2 * kGemmThreads, BM, BN>(acc, args, producer, m0 + wm, n0 + wn,
+                                                       s_last);
 }
 
 template <int BM>
@@ -794,7 +827,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_big_kernel(TileArgs args) {
     compute_step(0);
     __syncthreads();
   }
-  pc_epilogue<TM, TN>(acc, args, false, m0 + wm, n0 + wn, s_last);
+  pc_epilogue<TM, TN, kGemmThreads, BM, BN, false>(acc, args, false, m0 + wm, n0 + wn, s_last);
 }
 
 template <int BM, int BN>
