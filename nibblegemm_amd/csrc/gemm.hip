@@ -934,13 +934,12 @@ TilePlan plan_tile(int64_t M, int64_t K, int64_t N, int64_t version, int bn_max)
     //  * K < 8192 (no split): 128-row tiles once the launch has ~192 of them
     //    (4096 x 14336 from M = 160), 64-row tiles below;
     //  * K >= 8192: 128-row tiles, split over K by the tile count -- at
-    //    14336 x 4096, M = 160 / 256 (64 tiles) 4 ways: 44 / 46 us (64-row
-    //    tiles, 2 ways: 58 / 59); M = 384 / 512 (96 / 128 tiles) 2 ways:
-    //    74 / 77 us (97 / 101); M = 768 / 1024 (192 / 256 tiles) unsplit;
-    //    M = 1536 (384 tiles, a round and a half) 2 ways: 221 us (242
-    //    unsplit); M = 2048 (512 tiles) unsplit.  The split's partials are
-    //    summed by the last workgroup of each tile, every split's loads in
-    //    one round.
+    //    14336 x 4096, M = 160 (64 tiles) 4 ways: 41 us (64-row tiles,
+    //    2 ways: 58); M = 384 / 512 (96 / 128 tiles) 2 ways: 74 / 76 us
+    //    (97 / 101); M = 768 / 1024 (192 / 256 tiles) unsplit; M = 1536
+    //    (384 tiles, a round and a half) 2 ways: 202 us (242 unsplit);
+    //    M = 2048 (512 tiles) unsplit.  The split's partials are summed by
+    //    the whole last workgroup of each tile (tile_sum_splits).
     const int64_t t128 = ceil_div(M, 128) * ceil_div(N, 128);
     p.t = TileChoice{version == 7 || K >= 8192 || t128 >= 192 ? 128 : 64, 128, true};
     tiles = ceil_div(M, p.t.bm) * ceil_div(N, 128);
