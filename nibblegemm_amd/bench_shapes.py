@@ -8,6 +8,7 @@ bench/launch_overhead.py and bench/autotune.py, at the benchmark shapes).
     python3 -m nibblegemm_amd.bench_shapes crossover   # gemv vs gemm over M
     python3 -m nibblegemm_amd.bench_shapes launch      # eager vs graph-replayed matmul
     python3 -m nibblegemm_amd.bench_shapes autotune    # gemv splits x block_threads
+    python3 -m nibblegemm_amd.bench_shapes attention   # decode-step attention over cache length
 
 Every timing is a HIP-graph replay of many calls; a kernel and its hipBLASLt
 baseline are timed with interleaved trials (the same clock state for both).  Each call streams its
@@ -260,6 +261,52 @@ def launch(args, rows):
         torch.cuda.empty_cache()
 
 
+def _attention_ref(qkv, kc, vc, pos, n_heads, n_kv, cos, sin):
+    """fp32 attention of the token at ``pos`` over cache rows 0 .. pos - 1
+    plus its own k (rotated, rounded to fp16 as the cache stores it) and v."""
+    hd = 128
+    q = qkv[0, :n_heads * hd].float().view(n_heads, hd)
+    k = qkv[0, n_heads * hd:(n_heads + n_kv) * hd].float().view(n_kv, hd)
+    v = qkv[0, (n_heads + n_kv) * hd:].float().view(n_kv, hd)
+    c, s = cos[pos], sin[pos]
+
+    def rot(x):
+        lo, hi = x[:, :hd // 2], x[:, hd // 2:]
+        return torch.cat([lo * c - hi * s, hi * c + lo * s], dim=1)
+
+    q, k = rot(q), rot(k).half().float()
+    K = torch.cat([kc[:, :pos].float(), k[:, None]], dim=1).repeat_interleave(n_heads // n_kv, 0)
+    V = torch.cat([vc[:, :pos].float(), v[:, None]], dim=1).repeat_interleave(n_heads // n_kv, 0)
+    p = torch.softmax(torch.bmm(K.contiguous(), q[:, :, None].contiguous())[:, :, 0] / hd ** 0.5, -1)
+    return torch.bmm(p[:, None, :].contiguous(), V.contiguous())[:, 0].reshape(1, -1)
+
+
+def attention(args, rows):
+    """The decode step's attention (Llama-3-8B: 32 query heads, 8 kv heads,
+    head_dim 128, rotary) at several cache lengths, over 32 distinct caches
+    as the 32 layers of a step would hold them; each position checked against
+    an fp32 reference first."""
+    from .glue import attention_bytes, attention_decode, rope_tables
+    n_heads, n_kv, max_seq, layers = 32, 8, 4096, 32
+    gen = torch.Generator().manual_seed(7)
+    cos, sin = rope_tables(max_seq)
+    kcs = [torch.randn((n_kv, max_seq, 128), generator=gen).half().cuda() for _ in range(layers)]
+    vcs = [torch.randn((n_kv, max_seq, 128), generator=gen).half().cuda() for _ in range(layers)]
+    qkv = torch.randn((1, (n_heads + 2 * n_kv) * 128), generator=gen).half().cuda()
+    for pos in args.pos:
+        ref = _attention_ref(qkv, kcs[0], vcs[0], pos, n_heads, n_kv, cos, sin)
+        y = attention_decode(qkv, kcs[0], vcs[0], pos, (cos, sin))
+        err = float((y.float() - ref).abs().max() / ref.pow(2).mean().sqrt())
+        if not err <= TOL:
+            raise RuntimeError(f"attention pos={pos}: max|y - ref| = {err:.3e} * rms(ref)")
+        t = H.bench_graph(lambda i: attention_decode(qkv, kcs[i % layers], vcs[i % layers], pos,
+                                                     (cos, sin)), reps=32, trials=args.trials)
+        _emit(rows, {"bench": "attention", "pos": pos, "chunks": (pos + 128) // 128,
+                     "us": round(t.median_ms * 1e3, 2),
+                     "kv_GB/s": round(H.achieved_gbps(attention_bytes(n_kv, pos), t.median_ms)),
+                     "max_err_rms": float(f"{err:.2e}"), **_clock(t)})
+
+
 def autotune(args, rows):
     """The GEMV's launch geometry swept over K splits x workgroup size, each
     point checked first, against the built-in plan (reference
@@ -296,8 +343,10 @@ def autotune(args, rows):
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("what", choices=["decode", "prefill", "dequant", "crossover", "launch",
-                                     "autotune"])
+                                     "autotune", "attention"])
     ap.add_argument("--M", type=int, nargs="*", help="batch sizes (default: the benchmark shapes)")
+    ap.add_argument("--pos", type=int, nargs="*", default=[0, 127, 128, 511, 1023, 2047, 4095],
+                    help="attention: cache positions of the decoded token")
     ap.add_argument("--group-size", type=int, default=128)
     ap.add_argument("--trials", type=int, default=10)
     ap.add_argument("--markdown", action="store_true")
@@ -312,7 +361,7 @@ def main(argv=None) -> int:
     print(f"# {H.device_summary()}", file=sys.stderr, flush=True)
     rows = []
     {"decode": decode, "prefill": prefill, "dequant": dequant, "crossover": crossover,
-     "launch": launch, "autotune": autotune}[args.what](args, rows)
+     "launch": launch, "autotune": autotune, "attention": attention}[args.what](args, rows)
     if args.markdown and rows:
         cols = [k for k in rows[0] if k != "bench"]
         print(H.markdown_table(rows, cols), file=sys.stderr)
