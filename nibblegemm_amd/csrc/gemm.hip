@@ -155,6 +155,8 @@ __device__ __forceinline__ void tile_sum_splits(const TileArgs& args, int m0, in
   constexpr uint32_t kCoherent = 16;  // sc1: the cache policy of an agent-scope load
   const int M = args.M, N = args.N;
   const uint32_t plane = static_cast<uint32_t>(M) * static_cast<uint32_t>(N);
+  // The ABI asks only 2-byte alignment of Y: 8-byte stores when it has more.
+  const bool y_quads = (reinterpret_cast<uintptr_t>(args.Y) & 7u) == 0;
 #pragma nounroll
   for (int c0 = 0; c0 < CHUNKS; c0 += THREADS * kPair) {
     uint32_t off[kPair];
@@ -193,7 +195,13 @@ __device__ __forceinline__ void tile_sum_splits(const TileArgs& args, int m0, in
       if (ok[u]) {
         const h4_t y = {(_Float16)sum[u][0], (_Float16)sum[u][1], (_Float16)sum[u][2],
                         (_Float16)sum[u][3]};
-        *reinterpret_cast<h4_t*>(args.Y + off[u] / 4) = y;
+        _Float16* dst = args.Y + off[u] / 4;
+        if (y_quads) {
+          *reinterpret_cast<h4_t*>(dst) = y;
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) dst[e] = y[e];
+        }
       }
   }
 }

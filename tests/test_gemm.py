@@ -254,3 +254,28 @@ def test_split_k_gemm_replays_in_a_graph():
         ng.gemm(Xd, qw)
         torch.cuda.synchronize()
     assert rms_err(host(eager), oracle_y(X, packed, scales, 14336, 128)) <= RMS_TOL
+
+
+def test_split_k_sum_into_under_aligned_output():
+    """The C ABI asks only 2-byte alignment of Y.  The split-K tile sum stores
+    4 columns at once when Y allows it and element by element otherwise; both
+    give the bits of the call into a freshly allocated Y."""
+    M, K_, N = 160, 14336, 512
+    X, packed, scales, Xd, qw = synthetic(M, K_, N, 128, seed=11)
+    ext = ng.extension()
+    ws_bytes, counter_bytes = ext.gemm_workspace_bytes(M, K_, N, 128, 6, None)
+    assert counter_bytes > 0  # this plan splits K
+    want = ng.gemm(Xd, qw)
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=Xd.device)
+    buf = torch.zeros(M * N + 8, dtype=torch.float16, device=Xd.device)
+    for start in (1, 2, 4):  # Y 2-, 4- and 8-byte aligned
+        y = buf[start:start + M * N].view(M, N)
+        assert y.data_ptr() % 8 == 2 * start % 8
+        rc = ext.gemm(Xd.data_ptr(), M, K_, qw.qweight.data_ptr(), qw.qweight.shape[0], N,
+                      qw.scales.data_ptr(), qw.scales.shape[0], qw.scales.shape[1], 128, 6,
+                      y.data_ptr(), ws.data_ptr(), ws_bytes, torch.cuda.current_stream().cuda_stream)
+        assert rc == 0, ext.last_error()
+        torch.cuda.synchronize()
+        assert torch.equal(y, want), start
+        assert buf[:start].eq(0).all() and buf[start + M * N:].eq(0).all(), start
+        buf.zero_()
