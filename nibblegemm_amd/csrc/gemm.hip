@@ -151,7 +151,7 @@ __device__ __forceinline__ void tile_sum_splits(const TileArgs& args, int m0, in
   constexpr int QUADS = BN / 4;
   constexpr int CHUNKS = BM * QUADS;
   constexpr int kPair = 2, kBatch = 4;
-  static_assert(CHUNKS % (THREADS * kPair) == 0, "whole rounds of chunk pairs");
+  constexpr bool kWholeRounds = CHUNKS % (THREADS * kPair) == 0;
   constexpr uint32_t kCoherent = 16;  // sc1: the cache policy of an agent-scope load
   const int M = args.M, N = args.N;
   const uint32_t plane = static_cast<uint32_t>(M) * static_cast<uint32_t>(N);
@@ -165,7 +165,7 @@ __device__ __forceinline__ void tile_sum_splits(const TileArgs& args, int m0, in
     for (int u = 0; u < kPair; ++u) {
       const int c = c0 + u * THREADS + static_cast<int>(threadIdx.x);
       const int gm = m0 + c / QUADS, gn = n0 + 4 * (c % QUADS);
-      ok[u] = gm < M && gn < N;
+      ok[u] = gm < M && gn < N && (kWholeRounds || c < CHUNKS);
       off[u] = ok[u] ? (static_cast<uint32_t>(gm) * N + gn) * 4u : kOutOfRange;
     }
     f4_t sum[kPair] = {};
@@ -507,50 +507,62 @@ __device__ __forceinline__ int lds_unit64(int r, int c) {
   return 8 * ((r & ~1) | s0) + (c ^ f);
 }
 
-// Producer/consumer form of the tile kernel, with 64-k steps: eight waves,
-// four of each role.
+// Producer/consumer form of the tile kernel, with 64-k steps: four producer
+// waves and CWAVES (4 or 8) consumer waves.
 //
 // In the tile kernel above every wave loads, decodes and stores its share of
 // the next step, waits at the barrier and then multiplies, so its MFMA pipe
 // idles while it does the rest (busy about a quarter of a wave's lifetime at
-// M = 2048).  Here the four consumer waves only read operands from LDS and
-// issue MFMAs (the tile kernel's 2 x 2 arrangement and wave tiles, 16 MFMAs
-// per wave per step), while the four producer waves run the global-load
-// pipeline and the decode, storing step t + 1 into the other LDS buffer
-// while step t is multiplied.  One consumer and one producer share each
-// SIMD, so the decode VALU work and the memory waits overlap the MFMAs.  Both
-// roles pass the same barriers, ntiles + 1 of them, one per step.
+// M = 2048).  Here the consumer waves only read operands from LDS and issue
+// MFMAs (a 64 x 64 or 32 x 64 wave tile, 16 or 8 MFMAs per wave per step),
+// while the four producer waves run the global-load pipeline and the decode,
+// storing step t + 1 into the other LDS buffer while step t is multiplied.
+// Consumers and producers share the SIMDs, so the decode VALU work and the
+// memory waits overlap the MFMAs.  Both roles pass the same barriers, ntiles
+// + 1 of them, one per step.
+//  * CWAVES = 4 (eight waves, 2 x 2 consumers): BM = 64 or 128; two
+//    workgroups per CU; PSTAGES = 4 steps of loads in flight.
+//  * CWAVES = 8 (twelve waves, 4 x 2 consumers of 64 x 64): BM = 256, one
+//    workgroup per CU (96 KiB of LDS).  Each decoded B tile then serves 256
+//    rows, which halves the decode work and the B stores per FLOP; A's LDS
+//    traffic per FLOP is unchanged.  PSTAGES = 2 (3 and 4 spill or measured
+//    slower, 1 exposes the load latency).
 //
-// Producers: thread tid loads four 16-byte A chunks (rows tid / 8 + 32 it,
+// Producers: thread tid loads BM / 32 16-byte A chunks (rows tid / 8 + 32 it,
 // unit tid % 8) and one dwordx4 of B -- packed row tid / 32 of the step,
 // columns 4 (tid % 32) .. + 3 -- with its four scales.  BN = 128.
-template <int BM, int GROUP>
-__global__ __launch_bounds__(2 * kGemmThreads) void gemm_pc64_kernel(TileArgs args) {
+template <int BM, int GROUP, int CWAVES = 4, int PSTAGES = kStages>
+__global__ __launch_bounds__((CWAVES + 4) * 64) void gemm_pc64_kernel(TileArgs args) {
   constexpr int BN = 128;
   constexpr int PBK = 64;
-  using C = TileCfg<BM, BN>;
+  constexpr int THREADS = (CWAVES + 4) * 64;
+  constexpr int WROWS = CWAVES / 2;                  // consumer waves as WROWS x 2
+  constexpr int WM = BM / WROWS, WN = BN / 2;
+  constexpr int TM = WM / 32, TN = WN / 32;          // 32 x 32 MFMA tiles per wave
   constexpr int A_IT = BM * (PBK / 8) / kGemmThreads;
+  static_assert(CWAVES == 4 || CWAVES == 8, "four or eight consumer waves");
+  static_assert(TM >= 1 && PSTAGES >= 1 && PSTAGES <= 4, "wave tile and load ring");
   __shared__ __attribute__((aligned(16))) _Float16 As[2][BM * PBK];
   __shared__ __attribute__((aligned(16))) _Float16 Bs[2][BN * PBK];
   __shared__ int s_last;
   const int M = args.M, K = args.K, N = args.N;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
-  const bool producer = wave >= 4;
-  const int tid = static_cast<int>(threadIdx.x) & (kGemmThreads - 1);
+  const bool producer = wave >= CWAVES;
+  const int tid = static_cast<int>(threadIdx.x) - (producer ? CWAVES * 64 : 0);
   const int lane = tid & 63;
   const int m0 = blockIdx.y * BM;
   const int n0 = blockIdx.x * BN;
   const int step0 = blockIdx.z * args.steps_per_split;
   const int ntiles = min(args.steps_per_split, K / PBK - step0);
-  const int wm = ((wave & 3) >> 1) * C::WM;
-  const int wn = (wave & 1) * C::WN;
+  const int wm = (wave >> 1) % WROWS * WM;
+  const int wn = (wave & 1) * WN;
   const int r32 = lane & 31;
 
-  f16_t acc[C::TM][C::TN];
+  f16_t acc[TM][TN];
 #pragma unroll
-  for (int i = 0; i < C::TM; ++i)
+  for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < C::TN; ++j)
+    for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
@@ -607,56 +619,68 @@ __global__ __launch_bounds__(2 * kGemmThreads) void gemm_pc64_kernel(TileArgs ar
         *reinterpret_cast<h8_t*>(&Bs[buf][b_st[j]]) = v;
       }
     };
-    Stage R[kStages];
+    // Ring of PSTAGES register stages: stage u holds step i while
+    // i % PSTAGES == u (each index is a compile-time constant).
+    Stage R[PSTAGES];
 #pragma unroll
-    for (int i = 0; i < kStages; ++i) load_step(R[i], i);
+    for (int i = 0; i < PSTAGES; ++i) load_step(R[i], i);
     auto piter = [&](auto u_const, int i) {
       constexpr int u = decltype(u_const)::value;
-      store_step(R[u], u & 1);
-      load_step(R[u], i + kStages);
+      store_step(R[u], i & 1);
+      load_step(R[u], i + PSTAGES);
       __syncthreads();
     };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, (PSTAGES > 1 ? 1 : 0)>;
+    using I2 = std::integral_constant<int, (PSTAGES > 2 ? 2 : 0)>;
+    using I3 = std::integral_constant<int, (PSTAGES > 3 ? 3 : 0)>;
     int i = 0;
-    for (; i + kStages <= ntiles; i += kStages) {
-      piter(std::integral_constant<int, 0>{}, i);
-      piter(std::integral_constant<int, 1>{}, i + 1);
-      piter(std::integral_constant<int, 2>{}, i + 2);
-      piter(std::integral_constant<int, 3>{}, i + 3);
+    for (; i + PSTAGES <= ntiles; i += PSTAGES) {
+      piter(I0{}, i);
+      if constexpr (PSTAGES > 1) piter(I1{}, i + 1);
+      if constexpr (PSTAGES > 2) piter(I2{}, i + 2);
+      if constexpr (PSTAGES > 3) piter(I3{}, i + 3);
     }
-    const int rem = ntiles - i;
-    if (rem > 0) piter(std::integral_constant<int, 0>{}, i);
-    if (rem > 1) piter(std::integral_constant<int, 1>{}, i + 1);
-    if (rem > 2) piter(std::integral_constant<int, 2>{}, i + 2);
+    const int rem = ntiles - i;  // < PSTAGES
+    if constexpr (PSTAGES > 1) {
+      if (rem > 0) piter(I0{}, i);
+    }
+    if constexpr (PSTAGES > 2) {
+      if (rem > 1) piter(I1{}, i + 1);
+    }
+    if constexpr (PSTAGES > 3) {
+      if (rem > 2) piter(I2{}, i + 2);
+    }
     __syncthreads();
   } else {
-    int rda[C::TM][PBK / 16], rdb[C::TN][PBK / 16];
+    int rda[TM][PBK / 16], rdb[TN][PBK / 16];
 #pragma unroll
     for (int ks = 0; ks < PBK / 16; ++ks) {
 #pragma unroll
-      for (int i = 0; i < C::TM; ++i) rda[i][ks] = lds_unit64(wm + 32 * i + r32, 2 * ks + (lane >> 5)) * 8;
+      for (int i = 0; i < TM; ++i) rda[i][ks] = lds_unit64(wm + 32 * i + r32, 2 * ks + (lane >> 5)) * 8;
 #pragma unroll
-      for (int j = 0; j < C::TN; ++j) rdb[j][ks] = lds_unit64(wn + 32 * j + r32, 2 * ks + (lane >> 5)) * 8;
+      for (int j = 0; j < TN; ++j) rdb[j][ks] = lds_unit64(wn + 32 * j + r32, 2 * ks + (lane >> 5)) * 8;
     }
     __syncthreads();
     for (int t = 0; t < ntiles; ++t) {
       const int buf = t & 1;
 #pragma unroll
       for (int ks = 0; ks < PBK / 16; ++ks) {
-        h8_t a[C::TM], b[C::TN];
+        h8_t a[TM], b[TN];
 #pragma unroll
-        for (int i = 0; i < C::TM; ++i) a[i] = *reinterpret_cast<const h8_t*>(&As[buf][rda[i][ks]]);
+        for (int i = 0; i < TM; ++i) a[i] = *reinterpret_cast<const h8_t*>(&As[buf][rda[i][ks]]);
 #pragma unroll
-        for (int j = 0; j < C::TN; ++j) b[j] = *reinterpret_cast<const h8_t*>(&Bs[buf][rdb[j][ks]]);
+        for (int j = 0; j < TN; ++j) b[j] = *reinterpret_cast<const h8_t*>(&Bs[buf][rdb[j][ks]]);
 #pragma unroll
-        for (int i = 0; i < C::TM; ++i)
+        for (int i = 0; i < TM; ++i)
 #pragma unroll
-          for (int j = 0; j < C::TN; ++j) acc[i][j] = mfma32(a[i], b[j], acc[i][j]);
+          for (int j = 0; j < TN; ++j) acc[i][j] = mfma32(a[i], b[j], acc[i][j]);
       }
       __syncthreads();
     }
   }
-  pc_epilogue<C::TM, C::TN, 2 * kGemmThreads, BM, BN>(acc, args, producer, m0 + wm, n0 + wn,
-                                                       s_last);
+  // The twelve-wave form is planned without a K split.
+  pc_epilogue<TM, TN, THREADS, BM, BN, CWAVES == 4>(acc, args, producer, m0 + wm, n0 + wn, s_last);
 }
 
 template <int BM>
@@ -667,6 +691,17 @@ hipError_t launch_pc64(const TileArgs& a, int64_t G, hipStream_t stream) {
     gemm_pc64_kernel<BM, 128><<<grid, 2 * kGemmThreads, 0, stream>>>(a);
   else
     gemm_pc64_kernel<BM, 64><<<grid, 2 * kGemmThreads, 0, stream>>>(a);
+  return hipGetLastError();
+}
+
+// 256-row tiles, eight consumer waves; never split over K.
+hipError_t launch_pc256(const TileArgs& a, int64_t G, hipStream_t stream) {
+  if (a.splits != 1) return hipErrorInvalidValue;
+  dim3 grid(static_cast<unsigned>(ceil_div(a.N, 128)), static_cast<unsigned>(ceil_div(a.M, 256)), 1);
+  if (G == 128)
+    gemm_pc64_kernel<256, 128, 8, 2><<<grid, 12 * 64, 0, stream>>>(a);
+  else
+    gemm_pc64_kernel<256, 64, 8, 2><<<grid, 12 * 64, 0, stream>>>(a);
   return hipGetLastError();
 }
 
@@ -868,6 +903,21 @@ struct TileChoice {
   bool big = false;  // the 256 x 256 large-tile kernel (64-k steps)
 };
 
+// Batches from this many rows up may run the twelve-wave producer/consumer
+// kernel (256 x 128 tiles, version 6).
+constexpr int64_t kPc256MinM = 2048;
+
+// The device the plans are made for: MI355X, 256 CUs.  Planning with a fixed
+// count keeps the workspace query pure host code and equal to the launch.
+constexpr int kPlanCUs = 256;
+
+// A grid of one-workgroup-per-CU tiles that fills whole rounds of the CUs,
+// the last at least 7/8 full.
+bool whole_rounds(int64_t tiles) {
+  const int64_t last = tiles % kPlanCUs;
+  return tiles >= kPlanCUs && (last == 0 || 8 * last >= 7 * kPlanCUs);
+}
+
 // Batches from this many rows up may run the large-tile kernel (version 6).
 constexpr int64_t kBigMinM = 1024;
 
@@ -884,10 +934,6 @@ int max_bn(int64_t N, const void* w, const void* s) {
   if (N % 2 == 0 && aligned(w, 8) && aligned(s, 4)) return 128;
   return 64;
 }
-
-// The device the plans are made for: MI355X, 256 CUs.  Planning with a fixed
-// count keeps the workspace query pure host code and equal to the launch.
-constexpr int kPlanCUs = 256;
 
 // Tile choice of the tile kernel (the shapes the producer/consumer kernel
 // does not take), measured on MI355X over M = 64..2048 at 4096 x 14336 and
@@ -936,6 +982,19 @@ TilePlan plan_tile(int64_t M, int64_t K, int64_t N, int64_t version, int bn_max)
   if (big) {
     p.t = TileChoice{256, 256, false, true};
     tiles = t256;
+  } else if (version == 6 && M >= kPc256MinM && K % 64 == 0 && bn_max >= 256 &&
+             whole_rounds(ceil_div(M, 256) * ceil_div(N, 128))) {
+    // 256 x 128 tiles with eight consumer waves, one workgroup per CU, where
+    // their grid makes whole rounds of the CUs (the last at least 7/8 full);
+    // never split over K.  Measured on MI355X against the 128 x 128 kernel
+    // (graph replays interleaved with hipBLASLt): 2048 x 14336 x 4096 (256
+    // tiles, one round) 232 vs 245 us; 4096 x 4096 x 14336 (1792 tiles,
+    // seven rounds) 470 vs 491.  With a part-filled last round the 128 x 128
+    // kernel's two workgroups per CU balance better: 2048 and 3072 x 4096 x
+    // 14336 (3.5 and 5.25 rounds) 254 vs 248 and 385 vs 378, 3072 x 14336 x
+    // 4096 (1.5 rounds) 405 vs 365.
+    p.t = TileChoice{256, 128, true};
+    tiles = ceil_div(M, 256) * ceil_div(N, 128);
   } else if (K % 64 == 0 && bn_max >= 256) {
     // The producer/consumer kernel wherever it applies (whole 64-k steps,
     // 16-byte packed-word loads).  Measured on MI355X, graph replay:
@@ -979,7 +1038,10 @@ hipError_t launch_choice(TileChoice t, const TileArgs& a, int64_t G, hipStream_t
   if (t.big) {
     return launch_big<256, 256>(a, G, stream);
   }
-  if (t.pc) return t.bm == 128 ? launch_pc64<128>(a, G, stream) : launch_pc64<64>(a, G, stream);
+  if (t.pc) {
+    if (t.bm == 256) return launch_pc256(a, G, stream);
+    return t.bm == 128 ? launch_pc64<128>(a, G, stream) : launch_pc64<64>(a, G, stream);
+  }
   if (t.bm == 128 && t.bn == 128) return launch_tile<128, 128>(a, G, stream);
   if (t.bm == 64 && t.bn == 128) return launch_tile<64, 128>(a, G, stream);
   if (t.bm == 128 && t.bn == 64) return launch_tile<128, 64>(a, G, stream);

@@ -123,10 +123,13 @@ def test_gemm_workspace_formula():
     assert ext.gemm_workspace_bytes(512, 4096, 14336, 128, 6, None) == (0, 0)
     assert ext.gemm_workspace_bytes(64, 4096, 14336, 128, 6, None) == (0, 0)
     # from M = 1024 version 6 takes 256 x 256 tiles where they make one round
-    # of the CUs (224 tiles here), never split; 2048 x 4096 has 512 tiles of
-    # 128 x 128, enough not to split
+    # of the CUs (224 tiles here), never split; from M = 2048, 256 x 128
+    # tiles where they make whole rounds (256 at 2048 x 4096), never split
     assert ext.gemm_workspace_bytes(1024, 4096, 14336, 128, 6, None) == (0, 0)
     assert ext.gemm_workspace_bytes(2048, 14336, 4096, 128, 6, None) == (0, 0)
+    # 3072 x 4096: 384 such tiles, a round and a half, so 128 x 128 tiles
+    # (768, enough not to split)
+    assert ext.gemm_workspace_bytes(3072, 14336, 4096, 128, 6, None) == (0, 0)
     # version 7 keeps 128 x 128 tiles: 16 x 32 of them at M = 2048, no split
     assert ext.gemm_workspace_bytes(2048, 14336, 4096, 128, 7, None) == (0, 0)
     assert ext.gemm_workspace_bytes(16, 14336, 4096, 128, 5, None) == (0, 0)

@@ -193,9 +193,28 @@ def test_large_tile_kernel(M, K_, N, g):
     """Version 6 runs 256 x 256 tiles from M = 1024 when the grid is one round
     over the CUs, at least 7/8 full: 224 tiles at 1024 x 14336, 256 at
     4096 x 4096, and with row and column tails 235 at 1100 x 12000 and 256
-    at 4000 x 4000; 2048 x 14336 (448 tiles) keeps the 128 x 128 kernel.
-    Both kernels sum each output over k in the same order, so version 6 and
-    version 7 (128 x 128) agree to the bit."""
+    at 4000 x 4000; 2048 x 14336 (448 tiles) runs the twelve-wave 256 x 128
+    kernel instead.  Every kernel sums each output over k in the same order,
+    so version 6 and version 7 (128 x 128) agree to the bit."""
+    X, packed, scales, Xd, qw = synthetic(M, K_, N, g, seed=M + K_ + N)
+    y6 = ng.gemm(Xd, qw, version=6)
+    y7 = ng.gemm(Xd, qw, version=7)
+    assert torch.equal(y6, y7)
+    assert torch.equal(ng.gemm(Xd, qw, version=6), y6)
+    ref = oracle_y(X, packed, scales, K_, g)
+    assert rms_err(host(y6), ref) <= RMS_TOL
+    assert rel_err(host(y6), ref) < REL_TOL
+
+
+@pytest.mark.parametrize("M,K_,N,g", [(2100, 256, 3500, 128), (2048, 320, 4096, 64),
+                                      (2049, 448, 3584, 64)])
+def test_twelve_wave_kernel(M, K_, N, g):
+    """Version 6 runs 256 x 128 tiles with eight consumer waves from M = 2048
+    when that grid makes whole rounds of the CUs (the last at least 7/8 full)
+    and the 256 x 256 kernel does not: with row and column tails (252 tiles
+    at 2100 x 3500), an odd number of 64-k steps with group 64 (256 tiles),
+    and a single-row tail (252 tiles at 2049 x 3584).  Its k order is the
+    128 x 128 kernel's, so version 6 and version 7 agree to the bit."""
     X, packed, scales, Xd, qw = synthetic(M, K_, N, g, seed=M + K_ + N)
     y6 = ng.gemm(Xd, qw, version=6)
     y7 = ng.gemm(Xd, qw, version=7)
