@@ -934,18 +934,27 @@ template <int MT, int GROUP, int SW, int WAVES, int DEPTH>
 hipError_t launch_strip_geometry(const GemvArgs& a, hipStream_t stream) {
   if constexpr (SW == 16 && GROUP != 128) {
     return hipErrorInvalidValue;  // a 16-column wave load spans 128 k
-  } else if constexpr (MT > 8) {
+  } else if constexpr (MT > 16) {
     return hipErrorInvalidValue;
   } else {
     const dim3 grid(8 * a.strips_per_xcd);
+    // A dispatch asking for more LDS than a workgroup can hold (160 KiB on
+    // gfx950) aborts the queue: every launch below is checked against it.
+    // Static LDS is the partials buffer, WAVES x phases x MT x SW floats, plus
+    // a few words.
+    constexpr size_t kLdsMax = 160 * 1024;
+    constexpr size_t kStaticLds = sizeof(float) * WAVES * (64 / SW) * MT * SW + 256;
     // One pass when no wave has more groups than the ring holds; activations
-    // and scales staged in LDS when the rows fit 64 KiB (the RMSNorm prologue
+    // and scales staged in LDS when the rows fit 64 KiB, or, for 16-row
+    // blocks, wherever they fit beside the partials (the RMSNorm prologue
     // always stages, and is only planned when they fit).
     const bool onepass = (a.K / GROUP + WAVES - 1) / WAVES <= DEPTH;
     const size_t xbytes = static_cast<size_t>(MT) * a.K * sizeof(_Float16);
     const size_t nbytes = a.norm_w != nullptr ? static_cast<size_t>(a.K) * sizeof(_Float16) : 0;
     const size_t lds = xbytes + nbytes + static_cast<size_t>(a.K / GROUP) * SW * sizeof(_Float16);
-    const bool staged = a.norm_w != nullptr || (a.stage_x && xbytes <= 65536);
+    const bool staged = a.norm_w != nullptr ||
+                        (a.stage_x && (xbytes <= 65536 || (MT == 16 && kStaticLds + lds <= kLdsMax)));
+    if (kStaticLds + (staged ? lds : 0) > kLdsMax) return hipErrorInvalidValue;
     if (a.norm_w != nullptr) {
       if (onepass)
         gemv_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, true, true, true><<<grid, WAVES * 64, lds, stream>>>(a);
@@ -987,6 +996,7 @@ hipError_t launch_strip_group(const GemvArgs& a, const StreamPlan& p, hipStream_
     case 2: return launch_strip_mt<2, GROUP>(a, p, stream);
     case 4: return launch_strip_mt<4, GROUP>(a, p, stream);
     case 8: return launch_strip_mt<8, GROUP>(a, p, stream);
+    case 16: return launch_strip_mt<16, GROUP>(a, p, stream);
     default: return hipErrorInvalidValue;
   }
 }
@@ -1051,12 +1061,20 @@ int plan_split_kernel(int64_t M, int64_t K, int64_t N, int64_t G, bool split_k,
 //    the best strip geometry.
 constexpr int64_t kStripMaxK = 8192;
 constexpr int64_t kStripWideN = 12288;
+// 9 <= M <= 16 (batches through gemm): 16-row blocks on 64-column strips
+// with the activations staged in LDS (128 KiB at K = 4096, beside 16 KiB of
+// partials).  Measured on MI355X against the split kernel, graph replay:
+// 4096 x 14336 M = 9 / 12 / 16 8.66 / 8.64 / 8.74 us (8.73 / 9.28 / 9.67),
+// 4096 x 28672 M = 12 / 16 16.1 / 16.4 (16.3 / 17.6).  Narrower N keeps the
+// split kernel (4096 x 4096, 64 strips: 7.7-7.8 against 6.9-8.1).
+constexpr int64_t kStrip16MaxK = 4096;
 
 bool plan_strip(int64_t M, int64_t K, int64_t N, int64_t G, StreamFusion fusion, StreamPlan* p) {
   (void)fusion;
-  if (M < 1 || M > 8 || K <= 0 || K > kStripMaxK || N <= 0 || (G != 64 && G != 128) ||
+  if (M < 1 || M > 16 || K <= 0 || K > kStripMaxK || N <= 0 || (G != 64 && G != 128) ||
       K % G != 0)
     return false;
+  if (M > 8 && (K > kStrip16MaxK || N < kStripWideN)) return false;
   StreamPlan q;
   q.kernel = kStripKernel;
   q.mt = mt_for(M);

@@ -19,7 +19,7 @@ from cases import host, oracle_y, synthetic, quantized
 pytestmark = pytest.mark.gpu
 
 SHAPES = [(1, 4096, 1024, 128), (4, 512, 260, 64), (8, 14336, 512, 128), (16, 1024, 4100, 128),
-          (100, 2048, 640, 64), (128, 8192, 384, 128)]
+          (12, 4096, 14336, 128), (100, 2048, 640, 64), (128, 8192, 384, 128)]
 
 
 @pytest.mark.parametrize("M,K,N,g", SHAPES)
@@ -32,7 +32,8 @@ def test_bias_epilogue_is_the_separate_add(M, K, N, g):
     assert torch.equal(fused, separate)
 
 
-SWIGLU = [(1, 4096, 1024, 128), (8, 14336, 512, 128), (33, 1024, 320, 64), (128, 2048, 96, 128)]
+SWIGLU = [(1, 4096, 1024, 128), (8, 14336, 512, 128), (16, 4096, 14336, 128), (33, 1024, 320, 64),
+          (128, 2048, 96, 128)]
 
 
 @pytest.mark.parametrize("M,K,Nh,g", SWIGLU)
@@ -44,12 +45,16 @@ def test_swiglu_epilogue_is_the_fp16_composition(M, K, Nh, g):
     assert fused.shape == (M, Nh)
     composed = torch.nn.functional.silu(ng.matmul(Xd, gate)) * ng.matmul(Xd, up)
     assert torch.equal(fused, composed)
-    # against fp32 arithmetic on the oracle's products of the same inputs
+    # against fp32 arithmetic on the oracle's products of the same inputs:
+    # 1e-2 of the RMS, plus, per element, the fp16 rounding of its own value
+    # (the product's heavy tail puts its largest outputs ~30 RMS out, where
+    # one fp16 ulp alone is ~1.5e-2 RMS)
     yg = torch.from_numpy(oracle_y(Xg, pg, sg, K, g)).float()
     yu = torch.from_numpy(oracle_y(Xg, pu, su, K, g)).float()
     ref = torch.nn.functional.silu(yg) * yu
-    err = float((torch.from_numpy(host(fused)).float() - ref).abs().max() / ref.pow(2).mean().sqrt())
-    assert err <= 1e-2
+    rms = ref.pow(2).mean().sqrt()
+    diff = (torch.from_numpy(host(fused)).float() - ref).abs()
+    assert bool((diff <= 1e-2 * rms + 2.0 ** -10 * ref.abs()).all())
 
 
 def test_swiglu_above_the_fused_batch_limit_composes():

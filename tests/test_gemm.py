@@ -171,6 +171,22 @@ def test_tile_kernel_split_k(M, K_, N):
         assert rms_err(host(ys[0]), ref) <= RMS_TOL, version
 
 
+@pytest.mark.parametrize("M", [9, 12, 16])
+@pytest.mark.parametrize("K_,N,g", [(4096, 14336, 128), (2048, 12292, 64)])
+def test_sixteen_row_strip_blocks(M, K_, N, g):
+    """9 <= M <= 16 over a short K and a wide N runs the decode GEMV's strip
+    kernel with 16-row blocks and the activations staged in LDS (128 KiB at
+    K = 4096), also with a 4-column strip tail (N = 12292); both versions
+    against the oracle, and repeatable."""
+    X, packed, scales, Xd, qw = synthetic(M, K_, N, g, seed=M + K_ + N)
+    ref = oracle_y(X, packed, scales, K_, g)
+    for version in (6, 7):
+        y = ng.gemm(Xd, qw, version=version)
+        assert torch.equal(y, ng.gemm(Xd, qw, version=version))
+        assert rms_err(host(y), ref) <= RMS_TOL, version
+        assert rel_err(host(y), ref) < REL_TOL, version
+
+
 @pytest.mark.parametrize("M,K_,N,g", [(129, 320, 132, 64), (257, 576, 260, 64), (1000, 128, 4100, 128),
                                       (300, 8256, 516, 64), (192, 4096, 640, 128)])
 def test_producer_consumer_kernel_edges(M, K_, N, g):
