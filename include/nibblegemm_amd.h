@@ -50,7 +50,7 @@
 extern "C" {
 #endif
 
-#define NIBBLE_ABI_VERSION 8
+#define NIBBLE_ABI_VERSION 9
 
 #if defined(__GNUC__) || defined(__clang__)
 #define NIBBLE_API __attribute__((visibility("default")))
@@ -149,6 +149,14 @@ NIBBLE_API size_t nibble_gemm_workspace_bytes(int64_t M, int64_t K, int64_t N, i
                                    int64_t version, void* stream);
 NIBBLE_API size_t nibble_gemm_counter_bytes(int64_t M, int64_t K, int64_t N, int64_t group_size,
                                  int64_t version, void* stream);
+/* 1 when nibble_gemm_w4a16 runs these sizes on the streaming kernel (given
+ * operands aligned as nibble_matmul_w4a16_fused requires), so that its result
+ * has the bits of nibble_matmul_w4a16_fused's epilogue 0; 0 when it takes
+ * tiles.  No counterpart in the reference, whose gemm_w4a16 has one kernel.
+ * Callers that compose a bias or activation themselves use it to choose
+ * between the fused entry and nibble_gemm_w4a16 + separate ops with the same
+ * bits either way. */
+NIBBLE_API int nibble_gemm_streams(int64_t M, int64_t K, int64_t N, int64_t group_size);
 
 /*
  * Streaming matmul (1 <= M <= 128) with a fused output epilogue.  No
@@ -156,7 +164,9 @@ NIBBLE_API size_t nibble_gemm_counter_bytes(int64_t M, int64_t K, int64_t N, int
  * fp16 op (python/nibblegemm/ops.py:131-135), and gate/up activations run as
  * separate ops after the matmul.  For callers that want one launch per
  * layer projection (decode steps, HIP graphs):
- *   epilogue 0  Y [M, N] = X @ W, as nibble_gemm_w4a16 writes it;
+ *   epilogue 0  Y [M, N] = X @ W, as nibble_gemm_w4a16 writes it where
+ *               nibble_gemm_streams(M, K, N, group_size) is 1 (within
+ *               tolerance of it elsewhere: different split sums);
  *   epilogue 1  Y [M, N] = fp16(fp16(X @ W) + bias), bias fp16 [N] -- the
  *               same bits as the separate fp16 add;
  *   epilogue 2  W is [gate | up] interleaved in 16-column blocks (N a

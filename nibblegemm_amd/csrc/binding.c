@@ -134,6 +134,16 @@ static PyObject* py_fused_ws(PyObject* self, PyObject* const* a, Py_ssize_t n) {
   return Py_BuildValue("(nn)", (Py_ssize_t)ws, (Py_ssize_t)cb);
 }
 
+/* gemm_streams(M, K, N, g) */
+static PyObject* py_gemm_streams(PyObject* self, PyObject* const* a, Py_ssize_t n) {
+  (void)self;
+  if (!nargs_is(n, 4, "gemm_streams")) return NULL;
+  long long M, K, N, g;
+  if (!take_i64(a[0], &M) || !take_i64(a[1], &K) || !take_i64(a[2], &N) || !take_i64(a[3], &g))
+    return NULL;
+  return PyBool_FromLong(nibble_gemm_streams(M, K, N, g));
+}
+
 /* strip_major_cols(K, N, g) */
 static PyObject* py_sm_cols(PyObject* self, PyObject* const* a, Py_ssize_t n) {
   (void)self;
@@ -275,6 +285,8 @@ static PyMethodDef kMethods[] = {
      "nibble_matmul_w4a16_fused"},
     {"matmul_fused_workspace_bytes", (PyCFunction)(void (*)(void))py_fused_ws, METH_FASTCALL,
      "nibble_matmul_fused_workspace_bytes / nibble_matmul_fused_counter_bytes"},
+    {"gemm_streams", (PyCFunction)(void (*)(void))py_gemm_streams, METH_FASTCALL,
+     "nibble_gemm_streams"},
     {"strip_major_cols", (PyCFunction)(void (*)(void))py_sm_cols, METH_FASTCALL,
      "nibble_strip_major_cols"},
     {"pack_strip_major", (PyCFunction)(void (*)(void))py_sm_pack, METH_FASTCALL,

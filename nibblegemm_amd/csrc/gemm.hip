@@ -979,7 +979,15 @@ TilePlan plan_tile(int64_t M, int64_t K, int64_t N, int64_t version, int bn_max)
   const int64_t t256 = ceil_div(M, 256) * ceil_div(N, 256);
   const bool big = version == 6 && M >= kBigMinM && K % 64 == 0 && bn_max >= 256 &&
                    8 * t256 >= 7 * kPlanCUs && t256 <= kPlanCUs;
-  if (big) {
+  if (M <= kStreamMaxM && K % 64 == 0 && bn_max >= 256) {
+    // Small batches that do not stream (gemm_streams): 64-row tiles of the
+    // producer/consumer kernel, K split so that the grid nears one round of
+    // the CUs -- the largest of 1, 2, 4, 8 ways keeping it within 320
+    // workgroups.  Both versions take this plan (so they agree to the bit).
+    p.t = TileChoice{64, 128, true};
+    tiles = ceil_div(M, 64) * ceil_div(N, 128);
+    while (splits < 8 && tiles * splits * 2 <= 320 && K / 64 >= 2 * splits) splits *= 2;
+  } else if (big) {
     p.t = TileChoice{256, 256, false, true};
     tiles = t256;
   } else if (version == 6 && M >= kPc256MinM && K % 64 == 0 && bn_max >= 256 &&
@@ -1006,7 +1014,12 @@ TilePlan plan_tile(int64_t M, int64_t K, int64_t N, int64_t version, int bn_max)
     //    (97 / 101); M = 768 / 1024 (192 / 256 tiles) unsplit; M = 1536
     //    (384 tiles, a round and a half) 2 ways: 202 us (242 unsplit);
     //    M = 2048 (512 tiles) unsplit.  The split's partials are summed by
-    //    the whole last workgroup of each tile (tile_sum_splits).
+    //    the whole last workgroup of each tile (tile_sum_splits);
+    //  * 4096 <= K < 8192 with at most 160 64-row tiles: 4 ways -- 4096 x
+    //    4096, M = 129 / 192 / 256 (96 / 96 / 128 tiles) 16.7 / 17.4 /
+    //    19.3 us unsplit 25.0 / 25.3 / 25.0; 4096 x 6144, M = 129 / 160 /
+    //    192 (144 tiles) 21.2 / 22.5 / 23.7 unsplit 25.6 / 25.3 / 25.0; at
+    //    192 tiles (4096 x 6144, M = 256) unsplit is ahead, 25.5 vs 27.4.
     const int64_t t128 = ceil_div(M, 128) * ceil_div(N, 128);
     p.t = TileChoice{version == 7 || K >= 8192 || t128 >= 192 ? 128 : 64, 128, true};
     tiles = ceil_div(M, p.t.bm) * ceil_div(N, 128);
@@ -1017,6 +1030,8 @@ TilePlan plan_tile(int64_t M, int64_t K, int64_t N, int64_t version, int bn_max)
         splits = 2;
       else if (tiles > kPlanCUs && tiles < 2 * kPlanCUs)
         splits = 2;
+    } else if (p.t.bm == 64 && K >= 4096 && tiles <= 160) {
+      splits = 4;
     }
   } else {
     p.t = version == 7 ? TileChoice{128, std::min(128, bn_max)} : choose_tile(M, N, bn_max);
@@ -1093,10 +1108,19 @@ namespace {
 // weight byte once and multiplies it against up to 32 rows (one or two
 // 16-row MFMA tiles), where a 64/128-row tile would leave most of the device
 // idle.  Measured on MI355X at K=4096, N=14336: M=16 takes 82 us through the
-// tile kernel and 11 us streaming; M=33 38.4 us tiled; the streaming cost
-// grows ~0.2 us per row, so it stays ahead up to M=128 (39 us tiled).
+// tile kernel and 11 us streaming.  Above 32 rows streaming takes one pass
+// per 32 rows; once those passes would move 48 MiB or more, 64-row tiles of
+// the producer/consumer kernel with a K split win (plan_tile).  Measured,
+// graph replay, streaming against tiles: 4096 x 14336 M = 48 / 64 / 128
+// 21.0 / 23.7 / 41.9 us against 19.6 / 20.1 / 26.5; 14336 x 4096 M = 33 /
+// 64 / 128 23.1 / 31.6 / 56.6 against 20.6 / 21.9 / 29.3; 8192 x 8192
+// M = 33 25.0 against 19.6; 4096 x 6144 M = 128 22.0 against 19.0.  Below
+// that streaming stays ahead: 4096 x 4096 M = 33..128 12.4-12.6 us against
+// 12.9-14.4, 4096 x 6144 M = 64 12.7 against 14.0.
 bool gemm_streams(int64_t M, int64_t K, int64_t N, int64_t G) {
-  return M >= 1 && M <= kStreamMaxM && K > 0 && N > 0 && N % 4 == 0 && K % G == 0;
+  if (!(M >= 1 && M <= kStreamMaxM && K > 0 && N > 0 && N % 4 == 0 && K % G == 0)) return false;
+  const int64_t pass_bytes = K * N / 2;
+  return M <= 32 || K % 64 != 0 || ceil_div(M, 32) * pass_bytes < (int64_t(48) << 20);
 }
 }  // namespace
 
@@ -1129,6 +1153,12 @@ extern "C" size_t nibble_gemm_workspace_bytes(int64_t M, int64_t K, int64_t N, i
   size_t ws, counters;
   gemm_plan_bytes(M, K, N, group_size, version, &ws, &counters);
   return ws;
+}
+
+extern "C" int nibble_gemm_streams(int64_t M, int64_t K, int64_t N, int64_t group_size) {
+  return (group_size == 64 || group_size == 128) && K % BK == 0 && gemm_streams(M, K, N, group_size)
+             ? 1
+             : 0;
 }
 
 extern "C" size_t nibble_gemm_counter_bytes(int64_t M, int64_t K, int64_t N, int64_t group_size,
@@ -1176,11 +1206,12 @@ extern "C" int nibble_gemm_w4a16(const void* X, int64_t x_rows, int64_t x_cols, 
   // grids are far too large to need a K split).
   const int64_t rows_max = std::max<int64_t>(256, ((int64_t(1) << 31) - 1) / (K * 2) / 256 * 256);
   // The workspace query plans for aligned operands; when the pointers force
-  // another kernel than that plan's, the call runs without a split, as do
+  // another kernel than that plan's (tiles where the query planned the
+  // streaming kernel, or another tile), the call runs without a split, as do
   // row-blocked tall launches.
   const TilePlan nominal = plan_tile(M, K, N, version, nominal_bn_max(N));
-  if (M > rows_max || p.t.pc != nominal.t.pc || p.t.big != nominal.t.big ||
-      p.t.bm != nominal.t.bm || p.t.bn != nominal.t.bn)
+  if (M > rows_max || gemm_streams(M, K, N, group_size) || p.t.pc != nominal.t.pc ||
+      p.t.big != nominal.t.big || p.t.bm != nominal.t.bm || p.t.bn != nominal.t.bn)
     p.splits = 1;
   if (p.splits > 1) {
     if (workspace == nullptr || workspace_bytes < p.workspace_bytes)

@@ -391,11 +391,15 @@ def _fused_workspace(ext, device: torch.device, stream: int, M: int, K: int, N: 
 
 
 def _fusable(X: torch.Tensor, qw: QuantizedWeight) -> bool:
-    """Whether the fused-epilogue launch takes these operands (else the
-    caller composes the same arithmetic from separate ops)."""
+    """Whether the fused-epilogue launch takes these operands and computes
+    the product with ``matmul``'s bits (else the caller composes the same
+    arithmetic from separate ops).  The fused launch streams; ``matmul``
+    takes tiles for batches of 33..128 rows over large weights, so those
+    compose."""
     return (X.dim() == 2 and X.is_cuda and 1 <= X.size(0) <= FUSED_MAX_M and qw.N % 4 == 0
             and X.is_contiguous() and X.data_ptr() % 16 == 0
-            and qw.qweight.data_ptr() % 16 == 0 and qw.scales.data_ptr() % 8 == 0)
+            and qw.qweight.data_ptr() % 16 == 0 and qw.scales.data_ptr() % 8 == 0
+            and _bind().gemm_streams(X.size(0), qw.K, qw.N, qw.group_size))
 
 
 def _fused(X: torch.Tensor, qw: QuantizedWeight, epilogue: int, bias: Optional[torch.Tensor],

@@ -95,14 +95,22 @@ def test_gemv_threads_override_validated():
 
 
 def test_gemm_workspace_formula():
-    """Batches of M <= 128 run the streaming kernel (split-K workspace as for
-    gemv); larger M runs tiles, split over K only when the tiles are few."""
+    """Batches of M <= 32 run the streaming kernel (split-K workspace as for
+    gemv), as do M <= 128 whose passes over the weights (one per 32 rows) stay
+    under 48 MiB; otherwise tiles, split over K only when the tiles are few."""
     ext = ng.extension()
     assert ext.gemm_workspace_bytes(16, 14336, 4096, 128, 6, None) == (256 + 4 * 16 * 4096 * 4, 256)
     assert ext.gemm_workspace_bytes(32, 4096, 14336, 128, 7, None) == (0, 0)
-    # M = 33 streams in two 32-row blocks: 112 groups split 4 ways, counters
-    # for 64 strips x 2 blocks
-    assert ext.gemm_workspace_bytes(33, 14336, 4096, 128, 6, None) == (512 + 4 * 33 * 4096 * 4, 512)
+    # M = 33 over 29.4 MB of weights would stream twice (58.7 MB): 64-row
+    # tiles instead, 32 of them split 8 ways (256 workgroups), both versions
+    assert ext.gemm_workspace_bytes(33, 14336, 4096, 128, 6, None) == (256 + 8 * 33 * 4096 * 4, 256)
+    assert ext.gemm_workspace_bytes(33, 14336, 4096, 128, 7, None) == (256 + 8 * 33 * 4096 * 4, 256)
+    # 4096 x 14336: 112 tiles split 2 ways at M = 64, 224 unsplit at M = 128
+    assert ext.gemm_workspace_bytes(64, 4096, 14336, 128, 6, None) == (512 + 2 * 64 * 14336 * 4, 512)
+    assert ext.gemm_workspace_bytes(128, 4096, 14336, 128, 6, None) == (0, 0)
+    # 4096 x 4096 (8.4 MB) keeps streaming up to M = 128 (4 passes, 33.6 MB):
+    # two 32-row blocks at M = 33, no split
+    assert ext.gemm_workspace_bytes(33, 4096, 4096, 128, 6, None) == (0, 0)
     # M > 128 runs the producer/consumer kernel; over a long K (224 steps of
     # 64) with 128 x 128 tiles split by their count: 2 x 32 = 64 tiles 4 ways
     # (both versions: the same plan, so the same bits)
@@ -114,14 +122,20 @@ def test_gemm_workspace_formula():
     assert ext.gemm_workspace_bytes(512, 14336, 4096, 128, 6, None) == (512 + 2 * 512 * 4096 * 4, 512)
     assert ext.gemm_workspace_bytes(1536, 14336, 4096, 128, 6, None) == \
         (1536 + 2 * 1536 * 4096 * 4, 1536)
+    # 4096 <= K < 8192 with few 64-row tiles: 4 ways (4096 x 4096, M = 129:
+    # 3 x 32 = 96 tiles); 4096 x 6144 at M = 256 (192 tiles) runs unsplit,
+    # as does version 7 (128-row tiles)
+    assert ext.gemm_workspace_bytes(129, 4096, 4096, 128, 6, None) == (512 + 4 * 129 * 4096 * 4, 512)
+    assert ext.gemm_workspace_bytes(256, 4096, 6144, 128, 6, None) == (0, 0)
+    assert ext.gemm_workspace_bytes(129, 4096, 4096, 128, 7, None) == (0, 0)
     # N % 4 != 0 cannot stream nor take 16-byte B loads: the tile kernel, 33
     # tiles of 64 x 128, split 4 ways
     assert ext.gemm_workspace_bytes(16, 14336, 4098, 128, 6, None) == (256 + 4 * 16 * 4098 * 4, 256)
-    # 192 and 256 tiles of 128 x 128 are not split; a short K never splits
+    # 192 and 256 tiles of 128 x 128 are not split; above 128 rows a short K
+    # never splits
     assert ext.gemm_workspace_bytes(768, 14336, 4096, 128, 6, None) == (0, 0)
     assert ext.gemm_workspace_bytes(1024, 14336, 4096, 128, 7, None) == (0, 0)
     assert ext.gemm_workspace_bytes(512, 4096, 14336, 128, 6, None) == (0, 0)
-    assert ext.gemm_workspace_bytes(64, 4096, 14336, 128, 6, None) == (0, 0)
     # from M = 1024 version 6 takes 256 x 256 tiles where they make one round
     # of the CUs (224 tiles here), never split; from M = 2048, 256 x 128
     # tiles where they make whole rounds (256 at 2048 x 4096), never split
@@ -318,15 +332,37 @@ def test_fused_rejections(kwargs, needle):
 
 def test_fused_workspace_matches_streaming_plan():
     """The fused entry runs the streaming kernel's plan: the same workspace as
-    nibble_gemm_w4a16 for M <= 128 (and as nibble_gemv_w4a16 v4 for M <= 8)."""
+    nibble_gemm_w4a16 wherever that streams too (M <= 32, and 33..128 rows
+    whose weight passes stay under 48 MiB), and as nibble_gemv_w4a16 v4 for
+    M <= 8.  Batches of 33..128 rows over large weights take tiles in
+    nibble_gemm_w4a16 but still stream in the fused entry."""
     ext = ng.extension()
-    for M, K, N in [(1, 4096, 14336), (1, 14336, 4096), (8, 14336, 512), (33, 14336, 4096),
-                    (128, 8192, 1024)]:
+    for M, K, N in [(1, 4096, 14336), (1, 14336, 4096), (8, 14336, 512), (32, 14336, 4096),
+                    (33, 4096, 4096), (128, 8192, 1024)]:
         assert ext.matmul_fused_workspace_bytes(M, K, N, 128, None) == \
             ext.gemm_workspace_bytes(M, K, N, 128, 6, None), (M, K, N)
     assert ext.matmul_fused_workspace_bytes(1, 14336, 4096, 128, None) == \
         ext.gemv_workspace_bytes(1, 14336, 4096, 128, 4, 0, 0, None)
     assert ext.matmul_fused_workspace_bytes(129, 4096, 4096, 128, None) == (0, 0)
+    assert ext.matmul_fused_workspace_bytes(33, 14336, 4096, 128, None) != \
+        ext.gemm_workspace_bytes(33, 14336, 4096, 128, 6, None)
+
+
+def test_gemm_streams_query():
+    """nibble_gemm_streams names the plan nibble_gemm_w4a16 takes: streaming
+    for M <= 32 and for 33..128 rows whose 32-row weight passes move under
+    48 MiB, tiles above (where the fused entry's plan differs from gemm's)."""
+    ext = ng.extension()
+    for M, K, N, g, streams in [(1, 4096, 14336, 128, True), (32, 14336, 4096, 128, True),
+                                (33, 14336, 4096, 128, False), (33, 4096, 4096, 128, True),
+                                (64, 4096, 14336, 128, False), (128, 4096, 6144, 64, False),
+                                (64, 4096, 6144, 128, True), (128, 8192, 1024, 128, True),
+                                (129, 4096, 4096, 128, False), (8, 4096, 4096, 32, False),
+                                (8, 4096, 4098, 128, False), (0, 4096, 4096, 128, False)]:
+        assert ext.gemm_streams(M, K, N, g) is streams, (M, K, N, g)
+        if streams:
+            assert ext.matmul_fused_workspace_bytes(M, K, N, g, None) == \
+                ext.gemm_workspace_bytes(M, K, N, g, 6, None), (M, K, N, g)
 
 
 def test_last_error_is_per_thread():

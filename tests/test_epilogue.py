@@ -14,12 +14,14 @@ import torch
 
 import nibblegemm_amd as ng
 from nibblegemm_amd import ops
+from nibblegemm_amd.quant import split_swiglu
 from cases import host, oracle_y, synthetic, quantized
 
 pytestmark = pytest.mark.gpu
 
 SHAPES = [(1, 4096, 1024, 128), (4, 512, 260, 64), (8, 14336, 512, 128), (16, 1024, 4100, 128),
-          (12, 4096, 14336, 128), (100, 2048, 640, 64), (128, 8192, 384, 128)]
+          (12, 4096, 14336, 128), (100, 2048, 640, 64), (128, 8192, 384, 128),
+          (64, 14336, 4096, 128)]
 
 
 @pytest.mark.parametrize("M,K,N,g", SHAPES)
@@ -33,7 +35,7 @@ def test_bias_epilogue_is_the_separate_add(M, K, N, g):
 
 
 SWIGLU = [(1, 4096, 1024, 128), (8, 14336, 512, 128), (16, 4096, 14336, 128), (33, 1024, 320, 64),
-          (128, 2048, 96, 128)]
+          (128, 2048, 96, 128), (48, 4096, 14336, 128)]
 
 
 @pytest.mark.parametrize("M,K,Nh,g", SWIGLU)
@@ -43,7 +45,14 @@ def test_swiglu_epilogue_is_the_fp16_composition(M, K, Nh, g):
     qw = ng.interleave_swiglu(gate, up)
     fused = ng.matmul_swiglu(Xd, qw)
     assert fused.shape == (M, Nh)
-    composed = torch.nn.functional.silu(ng.matmul(Xd, gate)) * ng.matmul(Xd, up)
+    if ng.extension().gemm_streams(M, K, 2 * Nh, g):
+        composed = torch.nn.functional.silu(ng.matmul(Xd, gate)) * ng.matmul(Xd, up)
+    else:
+        # large-weight batches take tiles split over K by the tile count, so
+        # the gate|up product sums in another order than the gate and up
+        # products alone: the bits are those of composing the one product
+        yg, yu = split_swiglu(ng.matmul(Xd, qw))
+        composed = torch.nn.functional.silu(yg) * yu
     assert torch.equal(fused, composed)
     # against fp32 arithmetic on the oracle's products of the same inputs:
     # 1e-2 of the RMS, plus, per element, the fp16 rounding of its own value

@@ -150,6 +150,44 @@ def test_small_batch_handover(M, K_, N, g):
         assert rel_err(y, ref) < REL_TOL, version
 
 
+@pytest.mark.parametrize("M", [33, 64, 100, 128])
+@pytest.mark.parametrize("K_,N", [(4096, 14336), (14336, 4096), (8192, 8192)])
+def test_small_batch_tiles(M, K_, N):
+    """Batches of 33..128 rows over large weights (32-row weight passes of
+    48 MiB or more) take 64-row producer/consumer tiles split over K instead
+    of streaming: every output, both versions (the same plan, so the same
+    bits), repeated calls bit-identical, against an fp32 product of the
+    dequant kernel's weights on the GPU."""
+    ext = ng.extension()
+    assert not ext.gemm_streams(M, K_, N, 128)
+    _, _, _, Xd, qw = synthetic(M, K_, N, 128, seed=400 + M + N)
+    ref = Xd.float() @ ng.dequant(qw).float()
+    rms = ref.pow(2).mean().sqrt()
+    y6 = ng.gemm(Xd, qw, version=6)
+    assert torch.equal(ng.gemm(Xd, qw, version=7), y6)
+    assert torch.equal(ng.gemm(Xd, qw, version=6), y6)
+    assert torch.equal(ng.matmul(Xd, qw), y6)
+    y = y6.float()
+    assert torch.isfinite(y).all()
+    assert float((y - ref).abs().max() / rms) <= RMS_TOL
+
+
+@pytest.mark.parametrize("M,K_,N", [(129, 4096, 4096), (192, 4096, 4096), (256, 4096, 4096),
+                                    (160, 4096, 6144), (200, 6144, 4096), (256, 4096, 6144)])
+def test_mid_k_split(M, K_, N):
+    """4096 <= K < 8192 with at most 160 64-row tiles splits K 4 ways (all
+    but 256 x 4096 x 6144, whose 192 tiles run unsplit; 200 x 6144 x 4096
+    has a row tail and 24 k steps per split): every output against an fp32
+    product of the dequant kernel's weights, repeated calls bit-identical."""
+    _, _, _, Xd, qw = synthetic(M, K_, N, 128, seed=500 + M + N)
+    ref = Xd.float() @ ng.dequant(qw).float()
+    rms = ref.pow(2).mean().sqrt()
+    y = ng.gemm(Xd, qw)
+    assert torch.equal(ng.gemm(Xd, qw), y)
+    assert torch.isfinite(y.float()).all()
+    assert float((y.float() - ref).abs().max() / rms) <= RMS_TOL
+
+
 def test_small_batch_split_k_is_deterministic():
     _, _, _, Xd, qw = synthetic(24, 14336, 1024, 128, seed=77)
     ys = [ng.gemm(Xd, qw) for _ in range(4)]
