@@ -40,7 +40,17 @@ launch), so a layer is 5 launches.  This is the per-token forward of
 the reference's model decode (bench/bench_model.py:177-188) without the
 embedding lookup and the fp16 lm_head, which are not W4A16.
 
+``--tp N`` builds every layer at one GPU's share of an N-way tensor-parallel
+split instead (:func:`projection_shapes`): q, k, v, gate and up split by
+columns (N / tp each), o and down by rows (K / tp, whole quant groups).  It
+times what one GPU's kernels cost per token at that split; the exchange a
+row-split layer needs after o and down (an all-reduce of its partial
+outputs) is not built, and the row-split projections here store fp16 where
+a sharded layer would keep fp32 partials for that sum.  The glue variants
+need every head and are full-model only.
+
     python -m nibblegemm_amd.decode_step --layers 32
+    python -m nibblegemm_amd.decode_step --layers 32 --tp 8 --variants projections_strips,fused_strips
 """
 from __future__ import annotations
 
@@ -53,7 +63,8 @@ import torch
 
 from . import harness as H
 from .glue import attention_bytes, attention_decode, rmsnorm, rope_tables
-from .ops import matmul, matmul_bias, matmul_swiglu, rmsnorm_matmul, to_strip_major
+from .ops import (matmul, matmul_bias, matmul_swiglu, rmsnorm_matmul, strip_major_cols,
+                  to_strip_major)
 from .quant import QuantizedWeight, concat_columns, interleave_swiglu, quantize_device
 
 LLAMA3_8B = {"hidden": 4096, "kv": 1024, "intermediate": 14336, "layers": 32,
@@ -61,18 +72,41 @@ LLAMA3_8B = {"hidden": 4096, "kv": 1024, "intermediate": 14336, "layers": 32,
 PROJECTIONS = ("q", "k", "v", "o", "gate", "up", "down")
 
 
-def projection_shapes(cfg=LLAMA3_8B) -> Dict[str, Tuple[int, int]]:
-    """(K, N) of every projection, consumed as ``Y = X @ W`` (bench_model.py:57-59)."""
+#: Projections split by output columns under tensor parallelism (the rest,
+#: o and down, split by input rows).
+COLUMN_SPLIT = ("q", "k", "v", "gate", "up")
+
+
+def projection_shapes(cfg=LLAMA3_8B, tp: int = 1,
+                      group_size: int = 128) -> Dict[str, Tuple[int, int]]:
+    """(K, N) of every projection, consumed as ``Y = X @ W`` (bench_model.py:57-59),
+    at one GPU's share of a ``tp``-way tensor-parallel split: N / tp for the
+    column-split projections, K / tp for o and down.  Column shares must stay
+    multiples of 16 (whole SwiGLU blocks) and row shares whole quant groups."""
     h, kv, inter = cfg["hidden"], cfg["kv"], cfg["intermediate"]
-    return {"q": (h, h), "k": (h, kv), "v": (h, kv), "o": (h, h),
+    full = {"q": (h, h), "k": (h, kv), "v": (h, kv), "o": (h, h),
             "gate": (h, inter), "up": (h, inter), "down": (inter, h)}
+    if tp < 1:
+        raise ValueError(f"tp={tp} must be >= 1")
+    out = {}
+    for name, (K, N) in full.items():
+        if name in COLUMN_SPLIT:
+            if N % (16 * tp):
+                raise ValueError(f"{name}: N={N} does not split {tp} ways in 16-column blocks")
+            out[name] = (K, N // tp)
+        else:
+            if K % (group_size * tp):
+                raise ValueError(f"{name}: K={K} does not split {tp} ways in groups of {group_size}")
+            out[name] = (K // tp, N)
+    return out
 
 
 def build_layers(layers: int, cfg=LLAMA3_8B, group_size: int = 128, device="cuda",
-                 seed: int = 0) -> List[Dict[str, QuantizedWeight]]:
-    """``layers`` distinct sets of RTN-quantised projections, built on the GPU."""
+                 seed: int = 0, tp: int = 1) -> List[Dict[str, QuantizedWeight]]:
+    """``layers`` distinct sets of RTN-quantised projections, built on the GPU
+    (at one GPU's ``tp``-way share, :func:`projection_shapes`)."""
     gen = torch.Generator(device=device).manual_seed(seed)
-    shapes = projection_shapes(cfg)
+    shapes = projection_shapes(cfg, tp, group_size)
     out = []
     for _ in range(layers):
         layer = {}
@@ -96,8 +130,13 @@ def fuse(layer: Dict[str, QuantizedWeight], swiglu: bool = False) -> Dict[str, Q
 
 
 def strips(layers: List[Dict[str, QuantizedWeight]]) -> list:
-    """Strip-major copies of every weight (each at its recommended width)."""
-    return [{name: to_strip_major(qw) for name, qw in layer.items()} for layer in layers]
+    """Strip-major copies of every weight, each at its recommended width (at
+    least 32 columns for the SwiGLU weight, whose strips must hold whole
+    gate|up block pairs)."""
+    def one(name, qw):
+        sw = strip_major_cols(qw.K, qw.N, qw.group_size)
+        return to_strip_major(qw, max(sw, 32) if name == "gate_up_swiglu" else sw)
+    return [{name: one(name, qw) for name, qw in layer.items()} for layer in layers]
 
 
 def weight_bytes(layers: List[Dict[str, QuantizedWeight]]) -> int:
@@ -237,12 +276,17 @@ VARIANTS = ("projections", "fused", "fused_swiglu", "glue", "projections_strips"
 
 
 def run(n_layers: int = 32, group_size: int = 128, trials: int = 10, glue_pos: int = 1023,
-        variants=VARIANTS) -> dict:
-    layers = build_layers(n_layers, group_size=group_size)
-    nbytes = weight_bytes(layers)
-    res = {"config": f"Llama-3-8B shapes, {n_layers} distinct layers, g={group_size}, M=1",
-           "roofline_tok_s": round(H.HBM_PEAK_GBPS * 1e9 / nbytes, 1)}
+        variants=VARIANTS, tp: int = 1) -> dict:
     want = set(variants)
+    if tp > 1 and want & {"glue", "glue_strips"}:
+        raise ValueError("the glue variants run the full model only (tp = 1)")
+    layers = build_layers(n_layers, group_size=group_size, tp=tp)
+    nbytes = weight_bytes(layers)
+    share = "" if tp == 1 else f", one GPU's share of a {tp}-way tensor-parallel split"
+    res = {"config": f"Llama-3-8B shapes{share}, {n_layers} distinct layers, g={group_size}, M=1",
+           "tp": tp, "shapes": {k: list(v) for k, v in projection_shapes(tp=tp,
+                                                                      group_size=group_size).items()},
+           "roofline_tok_s": round(H.HBM_PEAK_GBPS * 1e9 / nbytes, 1)}
     if "projections" in want:
         res["projections"] = measure(layers, trials)
     if "projections_strips" in want:
@@ -278,17 +322,27 @@ def main(argv=None) -> int:
     ap.add_argument("--trials", type=int, default=10)
     ap.add_argument("--glue-pos", type=int, default=1023,
                     help="position of the full-step (glue) variant's token; -1 skips it")
-    ap.add_argument("--variants", default=",".join(VARIANTS),
-                    help="comma-separated subset of " + ", ".join(VARIANTS))
+    ap.add_argument("--variants", default=None,
+                    help="comma-separated subset of " + ", ".join(VARIANTS)
+                    + " (default: all; with --tp > 1 all but the glue variants)")
+    ap.add_argument("--tp", type=int, default=1,
+                    help="time one GPU's share of a TP-way tensor-parallel split")
     args = ap.parse_args(argv)
-    variants = tuple(v for v in args.variants.split(",") if v)
+    default = VARIANTS if args.tp == 1 else tuple(v for v in VARIANTS if "glue" not in v)
+    variants = tuple(v for v in args.variants.split(",") if v) if args.variants else default
     if not set(variants) <= set(VARIANTS):
         ap.error(f"unknown variant in {args.variants!r}")
+    try:
+        projection_shapes(tp=args.tp, group_size=args.group_size)
+    except ValueError as e:
+        ap.error(str(e))
+    if args.tp > 1 and {"glue", "glue_strips"} & set(variants):
+        ap.error("the glue variants run the full model only (tp = 1)")
     if not torch.cuda.is_available():
         print("decode_step needs a GPU", file=sys.stderr)
         return 1
-    print(json.dumps(run(args.layers, args.group_size, args.trials, args.glue_pos, variants)),
-          flush=True)
+    print(json.dumps(run(args.layers, args.group_size, args.trials, args.glue_pos, variants,
+                         args.tp)), flush=True)
     return 0
 
 

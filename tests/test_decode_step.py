@@ -8,9 +8,30 @@ import torch
 import nibblegemm_amd as ng
 from nibblegemm_amd import decode_step as D
 
-pytestmark = pytest.mark.gpu
+
+def test_tensor_parallel_shares():
+    """One GPU's share of a tp-way split: q, k, v, gate, up by output columns,
+    o and down by input rows in whole quant groups; splits that would cut a
+    16-column SwiGLU block or a quant group are refused."""
+    full = D.projection_shapes()
+    assert full == D.projection_shapes(tp=1)
+    eight = D.projection_shapes(tp=8)
+    assert eight == {"q": (4096, 512), "k": (4096, 128), "v": (4096, 128), "o": (512, 4096),
+                     "gate": (4096, 1792), "up": (4096, 1792), "down": (1792, 4096)}
+    for tp in (2, 4, 8, 16):
+        share = D.projection_shapes(tp=tp)
+        for name, (K, N) in full.items():
+            k, n = share[name]
+            assert (k * tp, n) == (K, N) if name in ("o", "down") else (k, n * tp) == (K, N)
+    with pytest.raises(ValueError):
+        D.projection_shapes(tp=3)       # 14336 / 3
+    with pytest.raises(ValueError):
+        D.projection_shapes(tp=32)      # 14336 / 32 = 448 rows: not whole groups of 128
+    with pytest.raises(ValueError):
+        D.projection_shapes(tp=0)
 
 
+@pytest.mark.gpu
 @pytest.mark.parametrize("K,N,g", [(4096, 1024, 128), (512, 264, 64), (14336, 128, 128)])
 def test_quantize_device_is_bit_identical_to_the_oracle(oracle, K, N, g):
     gen = torch.Generator().manual_seed(K + N)
@@ -24,6 +45,7 @@ def test_quantize_device_is_bit_identical_to_the_oracle(oracle, K, N, g):
     assert np.array_equal(qw.scales.cpu().numpy().view(np.uint16), s16.view(np.uint16))
 
 
+@pytest.mark.gpu
 def test_concatenated_gemv_equals_the_separate_ones():
     """q|k|v and gate|up fusion: one launch over 64-column-aligned parts gives
     the same bits per column as separate launches."""
@@ -36,6 +58,7 @@ def test_concatenated_gemv_equals_the_separate_ones():
     assert torch.equal(fused, sep)
 
 
+@pytest.mark.gpu
 def test_decode_step_runs_and_counts_launches():
     cfg = {"hidden": 512, "kv": 128, "intermediate": 1024, "layers": 2}
     layers = D.build_layers(2, cfg=cfg)
@@ -91,6 +114,7 @@ def _replays_match(run, between, replays: int = 3):
     return eager
 
 
+@pytest.mark.gpu
 @pytest.mark.parametrize("variant", ["projections", "fused", "fused_swiglu"])
 def test_full_size_step_graph_replays_equal_eager(layers_8b, variant):
     layers = {"projections": layers_8b,
@@ -102,6 +126,7 @@ def test_full_size_step_graph_replays_equal_eager(layers_8b, variant):
     _replays_match(step.outputs, other)
 
 
+@pytest.mark.gpu
 def test_full_size_glue_step_graph_replays_equal_eager(layers_8b):
     layers = [D.fuse(layer, swiglu=True) for layer in layers_8b]
     step = D.GlueDecodeStep(layers, pos=300, max_seq=320)
@@ -109,6 +134,7 @@ def test_full_size_glue_step_graph_replays_equal_eager(layers_8b):
     _replays_match(lambda: [step()], other)
 
 
+@pytest.mark.gpu
 def test_full_size_fused_launches_equal_the_separate_ones(layers_8b):
     """Each fused launch computes its columns with the separate launches'
     plan, so q|k|v and gate|up give the separate outputs' bits, and the SwiGLU
@@ -123,6 +149,7 @@ def test_full_size_fused_launches_equal_the_separate_ones(layers_8b):
     assert torch.equal(h, torch.nn.functional.silu(sep["gate"]) * sep["up"])
 
 
+@pytest.mark.gpu
 def test_full_size_projections_match_the_oracle(oracle, layers_8b):
     """Layer 0's seven projections at M = 1 against the oracle's dequantize +
     fp32 matmul, within the north-star bound."""
@@ -134,3 +161,24 @@ def test_full_size_projections_match_the_oracle(oracle, layers_8b):
         ref = ref.astype(np.float64)
         err = float(np.abs(y.float().cpu().numpy() - ref).max() / np.sqrt(np.mean(ref ** 2)))
         assert err <= 1e-2, (qw.K, qw.N, err)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("tp", [2, 8])
+def test_tensor_parallel_share_projections_match_the_oracle(oracle, tp):
+    """One layer at one GPU's share of a tp-way split, each projection on
+    packed and strip-major weights, q|k|v and gate|up fused too, against the
+    oracle at M = 1."""
+    layers = D.build_layers(1, seed=30 + tp, tp=tp)
+    fused = [D.fuse(layers[0])]
+    for packed in (layers, fused):
+        steps = (D.DecodeStep(packed), D.DecodeStep(D.strips(packed)))
+        outs = [step.outputs() for step in steps]
+        for n, (x, qw, _) in enumerate(steps[0].calls):
+            ref = oracle.reference_matmul(x.cpu().numpy(), qw.qweight.cpu().numpy(),
+                                          qw.scales.cpu().numpy(), qw.K, qw.group_size)
+            ref = ref.astype(np.float64)
+            rms = np.sqrt(np.mean(ref ** 2))
+            for y in (outs[0][n], outs[1][n]):
+                err = float(np.abs(y.float().cpu().numpy() - ref).max() / rms)
+                assert err <= 1e-2, (tp, qw.K, qw.N, err)
