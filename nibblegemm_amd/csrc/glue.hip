@@ -75,15 +75,13 @@ struct AttnArgs {
 };
 
 // Element d of the rotary embedding of a 128-vector x at position pos, in the
-// rotate-half pairing of transformers' apply_rotary_pos_emb (d with d +- 64):
+// rotate-half pairing of transformers' apply_rotary_pos_emb (d with d +- 64),
+// from xd = x[d], its partner xp = x[d ^ 64] and the position's cos / sin of
+// d mod 64:
 //   d <  64: x[d] cos - x[d + 64] sin;   d >= 64: x[d] cos + x[d - 64] sin.
-__device__ __forceinline__ float rope_at(const _Float16* x, int d, const AttnArgs& a) {
-  const float v = static_cast<float>(x[d]);
-  if (a.rope_cos == nullptr) return v;
-  const size_t i = static_cast<size_t>(a.pos) * kRopeHalf + (d & (kRopeHalf - 1));
-  const float c = a.rope_cos[i], s = a.rope_sin[i];
-  return d < kRopeHalf ? v * c - static_cast<float>(x[d + kRopeHalf]) * s
-                       : v * c + static_cast<float>(x[d - kRopeHalf]) * s;
+__device__ __forceinline__ float rotate_half(_Float16 xd, _Float16 xp, float c, float s, int d) {
+  const float v = static_cast<float>(xd);
+  return d < kRopeHalf ? v * c - static_cast<float>(xp) * s : v * c + static_cast<float>(xp) * s;
 }
 
 // Grouped-query attention of one decode token: QPK query heads share each
@@ -132,37 +130,88 @@ __global__ __launch_bounds__(kGlueThreads) void attention_decode_kernel(AttnArgs
   const int n_heads = a.n_kv * QPK;
   const int t0 = c * kChunk;
   const int t1 = min(t0 + kChunk, a.pos + 1);
-  const _Float16* qh = a.qkv + static_cast<size_t>(h) * QPK * HD;
-  const _Float16* kx = a.qkv + static_cast<size_t>(n_heads) * HD + static_cast<size_t>(h) * HD;
-  const _Float16* vx = kx + static_cast<size_t>(a.n_kv) * HD;
   const size_t row0 = static_cast<size_t>(h) * a.max_seq;  // cache row of token 0
   const int g16 = tid >> 4;
   const int j = tid & 15;
 
+  // Every load of the prologue is issued before any of them is used, so the
+  // prologue costs one memory round trip: this thread's q elements with their
+  // rotary partners and cos / sin, the new token's k and v, then the cached
+  // rows (issued last: the rotary work waits only for the loads before them).
+  // Buffer loads without branches: a lane with nothing to load passes an
+  // offset beyond the resource (it reads zero), and without rotary tables the
+  // cos / sin resources are empty.
+  constexpr int QE = (QPK * HD + kGlueThreads - 1) / kGlueThreads;  // q elements per thread
+  const bool rope = a.rope_cos != nullptr;
+  const uint32_t rope_bytes = rope ? static_cast<uint32_t>(a.max_seq) * kRopeHalf * 4u : 0u;
+  const auto rq = make_rsrc(a.qkv, static_cast<uint32_t>(n_heads + 2 * a.n_kv) * HD * 2u);
+  const auto rcos = make_rsrc(a.rope_cos, rope_bytes);
+  const auto rsin = make_rsrc(a.rope_sin, rope_bytes);
+  const uint32_t rope_row = static_cast<uint32_t>(a.pos) * kRopeHalf * 4u;
+  const bool writer = t1 == a.pos + 1 && tid < HD;  // writes the new token's k and v
+  auto ld16 = [&](uint32_t off) {
+    return __builtin_bit_cast(_Float16, __builtin_amdgcn_raw_buffer_load_b16(rq, off, 0, 0));
+  };
+  auto ld32 = [](__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+  };
+  _Float16 qx[QE], qp[QE];
+  float qc[QE], qn[QE];
+#pragma unroll
+  for (int u = 0; u < QE; ++u) {
+    const int e = tid + u * kGlueThreads;
+    const int d = e % HD;
+    const uint32_t base = e < QPK * HD ? static_cast<uint32_t>(h * QPK * HD + e - d) * 2u
+                                       : kOutOfRange;
+    const uint32_t rot = e < QPK * HD ? rope_row + static_cast<uint32_t>(d & (kRopeHalf - 1)) * 4u
+                                      : kOutOfRange;
+    qx[u] = ld16(base + static_cast<uint32_t>(d) * 2u);
+    qp[u] = ld16(base + static_cast<uint32_t>(d ^ kRopeHalf) * 2u);
+    qc[u] = ld32(rcos, rot);
+    qn[u] = ld32(rsin, rot);
+  }
+  const uint32_t kbase = writer ? static_cast<uint32_t>((n_heads + h) * HD) * 2u : kOutOfRange;
+  const uint32_t vbase = writer ? static_cast<uint32_t>((n_heads + a.n_kv + h) * HD) * 2u
+                                : kOutOfRange;
+  const uint32_t krot = writer ? rope_row + static_cast<uint32_t>(tid & (kRopeHalf - 1)) * 4u
+                               : kOutOfRange;
+  const _Float16 kx0 = ld16(kbase + static_cast<uint32_t>(tid) * 2u);
+  const _Float16 kxp = ld16(kbase + static_cast<uint32_t>(tid ^ kRopeHalf) * 2u);
+  const _Float16 vx0 = ld16(vbase + static_cast<uint32_t>(tid) * 2u);
+  const float kc = ld32(rcos, krot);
+  const float kn_s = ld32(rsin, krot);
+  // This kv head's cache rows (max_seq x 128 fp16 each, under 2^31 bytes:
+  // max_seq is bounded on the host); rows outside the chunk and the current
+  // token's (not written yet) read as zero.
+  const uint32_t head_bytes = static_cast<uint32_t>(a.max_seq) * HD * 2u;
+  const auto rk = make_rsrc(a.k_cache + row0 * HD, head_bytes);
+  const auto rv = make_rsrc(a.v_cache + row0 * HD, head_bytes);
   h8_t kr[TPG], vr[TPG];
 #pragma unroll
   for (int u = 0; u < TPG; ++u) {
     const int t = t0 + g16 + 16 * u;
-    kr[u] = h8_t{};
-    vr[u] = h8_t{};
-    if (t < t1 && t != a.pos) {
-      const size_t off = (row0 + t) * HD + 8 * j;
-      kr[u] = *reinterpret_cast<const h8_t*>(a.k_cache + off);
-      vr[u] = *reinterpret_cast<const h8_t*>(a.v_cache + off);
-    }
+    const uint32_t off = t < t1 && t != a.pos ? static_cast<uint32_t>(t * HD + 8 * j) * 2u
+                                              : kOutOfRange;
+    kr[u] = __builtin_bit_cast(h8_t, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
+    vr[u] = __builtin_bit_cast(h8_t, __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0));
   }
 
-  for (int e = tid; e < QPK * HD; e += kGlueThreads) {
-    const int hq = e / HD, d = e % HD;
-    qs[hq][d] = rope_at(qh + hq * HD, d, a) * kScale;
+#pragma unroll
+  for (int u = 0; u < QE; ++u) {
+    const int e = tid + u * kGlueThreads;
+    if (e < QPK * HD) {
+      const int hq = e / HD, d = e % HD;
+      const float v = rope ? rotate_half(qx[u], qp[u], qc[u], qn[u], d) : static_cast<float>(qx[u]);
+      qs[hq][d] = v * kScale;
+    }
   }
-  if (t1 == a.pos + 1 && tid < HD) {
-    const _Float16 kn = static_cast<_Float16>(rope_at(kx, tid, a));
-    const _Float16 vn = vx[tid];
+  if (writer) {
+    const _Float16 kn = static_cast<_Float16>(
+        rope ? rotate_half(kx0, kxp, kc, kn_s, tid) : static_cast<float>(kx0));
     knew[tid] = kn;
-    vnew[tid] = vn;
+    vnew[tid] = vx0;
     a.k_cache[(row0 + a.pos) * HD + tid] = kn;
-    a.v_cache[(row0 + a.pos) * HD + tid] = vn;
+    a.v_cache[(row0 + a.pos) * HD + tid] = vx0;
   }
   __syncthreads();
 
