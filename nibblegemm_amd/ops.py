@@ -463,7 +463,14 @@ def matmul_swiglu(X: torch.Tensor, qw: QuantizedWeight) -> torch.Tensor:
     return torch.nn.functional.silu(gate) * up
 
 
-NORM_FUSED_MAX_M = 8
+#: Largest batch ``rmsnorm_matmul`` runs as one launch.  The kernels take the
+#: RMSNorm prologue up to 8 rows, but from 4 rows the two launches are faster
+#: (MI355X, strip-major weights, graph replay, fused vs composed): 4096 x 6144
+#: M = 1 / 3 / 4 / 8 5.9 / 7.1 / 7.6 / 9.9 us vs 6.8 / 7.2 / 7.4 / 7.7;
+#: 4096 x 28672 SwiGLU M = 1 / 4 / 8 12.0 / 15.4 / 30.0 vs 14.4 / 15.0 /
+#: 15.5 (at 8 rows the staged norm weight leaves room for one workgroup per
+#: CU instead of two).
+NORM_FUSED_MAX_M = 3
 NORM_FUSED_MAX_K = 16384
 
 
@@ -473,10 +480,10 @@ def rmsnorm_matmul(X: torch.Tensor, norm_weight: torch.Tensor, qw: QuantizedWeig
     """``matmul(rmsnorm(X, norm_weight, eps), qw)``, optionally through the
     bias or SwiGLU epilogue (:func:`matmul_bias`, :func:`matmul_swiglu`).
 
-    For M <= 8 and K <= 16384 (the normalised rows fitting 64 KiB) this is one
+    For M <= 3 and K <= 16384 (the normalised rows fitting 64 KiB) this is one
     launch: the streaming kernel normalises the rows itself, with the
     RMSNorm kernel's arithmetic, so the result has the bits of the two-step
-    composition, which runs otherwise."""
+    composition, which runs otherwise (:data:`NORM_FUSED_MAX_M`)."""
     _check_2d(X, qw)
     if bias is not None and swiglu:
         raise ValueError("bias and swiglu epilogues are exclusive")

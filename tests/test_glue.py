@@ -304,6 +304,9 @@ def test_rmsnorm_matmul_fused_is_the_two_step_bits(M, K, N, epi):
     w = (1 + 0.1 * torch.randn(K, generator=g)).half().to(dev)
     bias = torch.randn(N, generator=g).half().to(dev) if epi == "bias" else None
     fused = ops.rmsnorm_matmul(x, w, qw, 1e-5, bias=bias, swiglu=epi == "swiglu")
+    # the one-launch form directly, also where rmsnorm_matmul composes (M > 3)
+    code = 2 if epi == "swiglu" else 1 if epi == "bias" else 0
+    direct = ops._fused(x, qw, code, bias, N // 2 if epi == "swiglu" else N, (w, 1e-5))
     a = glue.rmsnorm(x, w, 1e-5)
     if epi == "swiglu":
         ref = ops.matmul_swiglu(a, qw)
@@ -312,6 +315,7 @@ def test_rmsnorm_matmul_fused_is_the_two_step_bits(M, K, N, epi):
     else:
         ref = ops.matmul(a, qw)
     assert torch.equal(fused, ref)
+    assert torch.equal(direct, ref)
     W = ng.dequant(qw).float()
     if epi == "none":
         assert err_rms(fused, (a.float() @ W).half()) <= 1e-2
@@ -322,7 +326,7 @@ def test_rmsnorm_matmul_beyond_the_fused_limits_composes():
     from nibblegemm_amd import ops
     g = torch.Generator().manual_seed(4)
     qw = ng.quantize(torch.randn((1024, 256), generator=g) * 0.02, 128).to(dev)
-    x = torch.randn((12, 1024), generator=g).half().to(dev)  # M > 8: two launches
+    x = torch.randn((12, 1024), generator=g).half().to(dev)  # M > 3: two launches
     w = (1 + 0.1 * torch.randn(1024, generator=g)).half().to(dev)
     assert torch.equal(ops.rmsnorm_matmul(x, w, qw), ops.matmul(glue.rmsnorm(x, w), qw))
 

@@ -215,9 +215,13 @@ def test_rmsnorm_prologue_is_the_two_step_composition(M, K, N, sw):
     _, _, _, Xd, _, sm = strip_case(M, K, N, 128, sw, seed=5)
     w = (torch.rand(K, generator=torch.Generator().manual_seed(K)) + 0.5).half().cuda()
     fused = ng.rmsnorm_matmul(Xd, w, sm, 1e-5)
+    # the one-launch form directly (rmsnorm_matmul composes from M = 4)
+    direct = ops._strip_gemv(Xd, sm, 0, None, N, (w, 1e-5))
     from nibblegemm_amd.glue import rmsnorm  # noqa: PLC0415
 
-    assert torch.equal(fused, ng.matmul(rmsnorm(Xd, w, 1e-5), sm))
+    two_step = ng.matmul(rmsnorm(Xd, w, 1e-5), sm)
+    assert torch.equal(fused, two_step)
+    assert torch.equal(direct, two_step)
 
 
 @pytest.mark.gpu
