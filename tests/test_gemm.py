@@ -303,13 +303,16 @@ def test_gemm_under_aligned_weights(M, K_, N):
     assert rms_err(host(y_off), oracle_y(X, packed, scales, K_, 128)) <= RMS_TOL
 
 
-def test_split_k_gemm_replays_in_a_graph():
+@pytest.mark.parametrize("M,K_,N", [(160, 14336, 512), (64, 14336, 4096), (129, 4096, 4096)])
+def test_split_k_gemm_replays_in_a_graph(M, K_, N):
     """The producer/consumer kernel's K split (counters reset by the kernel
     itself, no memset) is graph-capturable; every replay matches eager, with
-    eager work between replays."""
-    X, packed, scales, Xd, qw = synthetic(160, 14336, 512, 128, seed=11)
+    eager work between replays.  Shapes: 128-row tiles split 4 ways over a
+    long K; a small batch on 64-row tiles split 8 ways; 4096 <= K < 8192 with
+    few tiles, split 4 ways."""
+    X, packed, scales, Xd, qw = synthetic(M, K_, N, 128, seed=11)
     ext = ng.extension()
-    assert ext.gemm_workspace_bytes(160, 14336, 512, 128, 6, None)[1] > 0  # this plan splits K
+    assert ext.gemm_workspace_bytes(M, K_, N, 128, 6, None)[1] > 0  # this plan splits K
     eager = ng.gemm(Xd, qw)
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -326,7 +329,7 @@ def test_split_k_gemm_replays_in_a_graph():
         assert torch.equal(out, eager)
         ng.gemm(Xd, qw)
         torch.cuda.synchronize()
-    assert rms_err(host(eager), oracle_y(X, packed, scales, 14336, 128)) <= RMS_TOL
+    assert rms_err(host(eager), oracle_y(X, packed, scales, K_, 128)) <= RMS_TOL
 
 
 def test_split_k_sum_into_under_aligned_output():
