@@ -150,14 +150,16 @@ def test_small_batch_handover(M, K_, N, g):
         assert rel_err(y, ref) < REL_TOL, version
 
 
-@pytest.mark.parametrize("M", [33, 64, 100, 128])
-@pytest.mark.parametrize("K_,N", [(4096, 14336), (14336, 4096), (8192, 8192)])
+@pytest.mark.parametrize("M,K_,N", [(M, K_, N) for M in (33, 64, 100, 128)
+                                    for K_, N in ((4096, 14336), (14336, 4096), (8192, 8192))]
+                         + [(100, 14336, 4100), (47, 8192, 8200), (65, 4096, 14340)])
 def test_small_batch_tiles(M, K_, N):
     """Batches of 33..128 rows over large weights (32-row weight passes of
     48 MiB or more) take 64-row producer/consumer tiles split over K instead
     of streaming: every output, both versions (the same plan, so the same
     bits), repeated calls bit-identical, against an fp32 product of the
-    dequant kernel's weights on the GPU."""
+    dequant kernel's weights on the GPU.  The last three shapes end in
+    partial row and column tiles."""
     ext = ng.extension()
     assert not ext.gemm_streams(M, K_, N, 128)
     _, _, _, Xd, qw = synthetic(M, K_, N, 128, seed=400 + M + N)
