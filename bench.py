@@ -26,6 +26,9 @@ one ``nibblegemm_amd.gemv`` call (M=1) over one batch of synthetic inputs
   ms_per_step, in GB/s.  ``roofline`` prices the same figure against MI355X's
   8 TB/s; ``cpu_baseline`` times the CPU oracle (dequantize + fp32 matmul,
   the reference's CPU path) on this host on a bounded sample.
+* ``small_batch`` (configs[2]: M = 2..32 through ``matmul``) and ``dequant``
+  (the standalone kernel at the same shape, bit-exact first) are graph-timed
+  over the same kind of rotation.
 
 Prints ONE JSON line.  Only ``--gpus 1`` is supported (one GPU per box).
 """
@@ -107,6 +110,8 @@ def main() -> int:
                     help="skip the Llama-3-8B-shaped decode step")
     ap.add_argument("--skip-prefill", action="store_true",
                     help="skip the M=2048 prefill GEMM points")
+    ap.add_argument("--skip-small-batch", action="store_true",
+                    help="skip the small-batch matmul points and the standalone dequant")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -221,6 +226,38 @@ def main() -> int:
             f"{r['K']}x{r['N']} {r['us']} us {r['TFLOP/s']} TFLOP/s ({r['vs_fp16']}x hipBLASLt fp16)"
             for r in prefill) + f"; {time.perf_counter() - t0:.1f} s")
 
+    small = dequant = None
+    if not args.skip_small_batch:
+        # configs[2]'s small batches through matmul (M <= 8 the decode GEMV,
+        # above it the GEMM's plans), and the standalone dequant at the same
+        # shape, bit-exact against the host dequantize first.
+        from nibblegemm_amd import bench_shapes as BS, quant  # noqa: PLC0415
+
+        torch.cuda.empty_cache()
+        t0 = time.perf_counter()
+        qws, gen = BS._weights(K, N, G, seed=K + N)
+        small = []
+        for m in (2, 4, 8, 16, 32):
+            Xm = torch.randn((m, K), generator=gen).to(torch.float16).cuda()
+            err = BS._check(ng.matmul(Xm, qws[0]), Xm, qws[0], f"matmul {m}x{K}x{N}")
+            t = H.bench_graph(lambda i: ng.matmul(Xm, qws[i]), reps=32, trials=10)
+            nb = H.total_bytes(m, K, N, G, 4)
+            small.append({"M": m, "us": round(t.median_ms * 1e3, 2),
+                          "gbps": round(H.achieved_gbps(nb, t.median_ms), 1),
+                          "max_err_rms": float(f"{err:.2e}")})
+        host = quant.dequantize(qws[0].to("cpu"))
+        if not torch.equal(ng.dequant(qws[0]).cpu().view(torch.int16), host.view(torch.int16)):
+            raise RuntimeError("dequant differs from the host dequantize")
+        t = H.bench_graph(lambda i: ng.dequant(qws[i]), reps=16, trials=10)
+        dq_bytes = K * N // 2 + (K // G) * N * 2 + 2 * K * N
+        dq_gbps = H.achieved_gbps(dq_bytes, t.median_ms)
+        dequant = {"K": K, "N": N, "us": round(t.median_ms * 1e3, 2), "gbps": round(dq_gbps, 1),
+                   "pct_hbm_peak": round(100 * dq_gbps / H.HBM_PEAK_GBPS, 2), "bit_exact": True}
+        del qws
+        log("small batch (matmul): " + "; ".join(f"M={r['M']} {r['us']} us" for r in small)
+            + f"; dequant {dequant['us']} us {dequant['gbps']} GB/s; "
+            f"{time.perf_counter() - t0:.1f} s")
+
     roofline = {
         "bound": "hbm",
         "achieved": round(gbps, 1),
@@ -260,6 +297,8 @@ def main() -> int:
         "cpu_baseline": cpu,
         "decode_8b": decode,
         "prefill_2048": prefill,
+        "small_batch": small,
+        "dequant": dequant,
         **extras,
     }
     print(json.dumps(line), flush=True)
