@@ -227,6 +227,20 @@ def test_attention_long_context_and_repeat(n_heads):
 
 
 @pytest.mark.gpu
+def test_attention_combine_repeats_its_bits():
+    """1024 tokens (8 chunks per kv head, combined by the last workgroup to
+    arrive), 300 calls back to back: identical bits each time."""
+    n_heads, n_kv, pos, max_seq = 32, 8, 1023, 1024
+    qkv, kc, vc = _attn_case(n_heads, n_kv, pos, max_seq, seed=13)
+    rope = glue.rope_tables(max_seq)
+    first = glue.attention_decode(qkv, kc, vc, pos, rope)
+    outs = [glue.attention_decode(qkv, kc, vc, pos, rope) for _ in range(300)]
+    torch.cuda.synchronize()
+    for y in outs:
+        assert torch.equal(y, first)
+
+
+@pytest.mark.gpu
 def test_attention_single_token_is_v():
     """At position 0 the softmax has one entry: the output is v itself
     (each query head reading its kv head)."""
