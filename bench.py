@@ -15,17 +15,21 @@ one ``nibblegemm_amd.gemv`` call (M=1) over one batch of synthetic inputs
   step is served from the 256 MiB Infinity Cache or the L2s.
 * ``--warmup W`` eager steps run untimed, then the K timed steps are captured
   into one HIP graph (capture executes nothing), replayed untimed for ~0.25 s
-  so the timed replay starts at the loaded shader clock, and replayed once
-  timed between events on the replay stream, bracketed by
-  ``torch.cuda.synchronize()``.  ``ms_per_step`` = elapsed / K.  The default
-  K = 5000 makes the timed region ~36 ms, long enough for the sysfs clock /
-  power sampler (10 ms period) to see it: ``clock`` holds the shader clock
-  at its start and end, min / mean / max over it, and the reference's
-  ``throttled`` test (the clock moving by more than 5%).
+  so the timed window starts at the loaded shader clock, and then replayed
+  R times back to back between two events on the replay stream, bracketed by
+  ``torch.cuda.synchronize()``.  R is the smallest count whose window lasts
+  at least ``--min-window-ms`` (30 ms), whatever K is, so the figure does not
+  depend on K and the sysfs clock / power sampler (10 ms period) sees the
+  window: ``ms_per_step`` = window / (R * K), and ``timed_replays`` = R.
+  ``clock`` holds the shader clock at the window's start and end, min /
+  mean / max over it, and the reference's ``throttled`` test (the clock
+  moving by more than 5%).
 * ``value`` = algorithmic bytes per step (K*N/2 + (K/128)*N*2 + 2K + 2N) /
   ms_per_step, in GB/s.  ``roofline`` prices the same figure against MI355X's
   8 TB/s; ``cpu_baseline`` times the CPU oracle (dequantize + fp32 matmul,
-  the reference's CPU path) on this host on a bounded sample.
+  the reference's CPU path) on this host on a bounded sample, and its
+  ``per_shape`` table the same path at every other shape the line reports
+  (decode sweep, small batches, prefill, dequant) on all of the job's cores.
 * ``small_batch`` (configs[2]: M = 2..32 through ``matmul``) and ``dequant``
   (the standalone kernel at the same shape, bit-exact first) are graph-timed
   over the same kind of rotation.
@@ -63,16 +67,47 @@ def _cpu_model() -> str:
     return "unknown"
 
 
-def cpu_baseline(target_s: float) -> dict:
+#: Shapes whose reference CPU path the line reports beside the GPU figures:
+#: (M, K, N).  The decode sweep (configs[0..1]), the small batches
+#: and the prefill points.
+CPU_SHAPES = ([(1, k, n) for k, n in ((4096, 14336), (14336, 4096), (8192, 8192), (4096, 4096),
+                                      (4096, 1024), (4096, 6144))]
+              + [(m, 4096, 14336) for m in (2, 4, 8, 16, 32)]
+              + [(m, k, n) for m in (128, 512, 2048) for k, n in ((4096, 14336), (14336, 4096))])
+#: Rows of X the CPU matmul is timed on at most (scaled by M / rows above it).
+CPU_MAX_ROWS = 32
+
+
+def _threads():
+    affinity = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    omp = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    return (min(affinity, omp) if omp > 0 else affinity), affinity, omp
+
+
+def cpu_per_shape(O, threads: int) -> list:
+    """The reference CPU path at every shape of CPU_SHAPES: the oracle's
+    dequantize (whole) and fp32 matmul (on at most CPU_MAX_ROWS rows, scaled
+    linearly to M), median of 3 after a warm-up, all of the job's cores."""
+    rows = []
+    for m, k, n in CPU_SHAPES:
+        r = O.time_reference_path(m, k, n, G, reps=3, threads=threads, max_rows=CPU_MAX_ROWS)
+        nb = k * n // 2 + (k // G) * n * 2 + m * k * 2 + m * n * 2
+        rows.append({"M": m, "K": k, "N": n, "ms": round(r["total_s"] * 1e3, 2),
+                     "dequant_ms": round(r["dequant_s"] * 1e3, 2),
+                     "matmul_ms": round(r["matmul_s"] * 1e3, 2), "rows_timed": r["rows_timed"],
+                     "gbps": round(nb / r["total_s"] / 1e9, 3),
+                     "tflops": round(2 * m * k * n / r["total_s"] / 1e12, 4)})
+    return rows
+
+
+def cpu_baseline(target_s: float, per_shape: bool = True) -> dict:
     """The reference's CPU path (dequantize + fp32 matmul), via the CPU oracle,
     on this host's cores: as many threads as the job's CPU share allows (the
     affinity mask, capped by OMP_NUM_THREADS where the box sets it)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O  # noqa: PLC0415  (cpu_baseline leg only)
 
-    affinity = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
-    omp = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
-    threads = min(affinity, omp) if omp > 0 else affinity
+    threads, affinity, omp = _threads()
     one = O.time_reference_path(M, K, N, G, reps=1, threads=threads)
     reps = int(max(5, min(60, target_s / max(one["total_s"], 1e-3))))
     r = O.time_reference_path(M, K, N, G, reps=reps, threads=threads)
@@ -94,6 +129,7 @@ def cpu_baseline(target_s: float) -> dict:
         "affinity_cores": affinity,
         "omp_num_threads": omp or None,
         "cpu_model": _cpu_model(),
+        "per_shape": cpu_per_shape(O, threads) if per_shape else None,
     }
 
 
@@ -104,6 +140,10 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--min-window-ms", type=float, default=30.0,
+                    help="shortest timed window; the K-step graph is replayed until it is reached")
+    ap.add_argument("--no-cpu-shapes", action="store_true",
+                    help="time the CPU path at the headline shape only")
     ap.add_argument("--skip-extras", action="store_true",
                     help="skip the copy-bandwidth, hipBLASLt and eager side measurements")
     ap.add_argument("--skip-decode-step", action="store_true",
@@ -139,11 +179,10 @@ def main() -> int:
     qweight = torch.from_numpy(ng.pack_nibbles(qu)).to(dev)
     scales = (torch.rand((K // G, N), generator=gen) * 0.018 + 0.002).to(torch.float16).to(dev)
     X = torch.randn((M, K), generator=gen).to(torch.float16).to(dev)
-    rot_w = H.Rotation(qweight)
-    rot_s = [scales] + [scales.clone() for _ in range(rot_w.count - 1)]
-    variants = H.Cycle(ng.QuantizedWeight(rot_w[i], rot_s[i], G, K, N) for i in range(rot_w.count))
+    variants = H.weight_ring(ng.QuantizedWeight(qweight, scales, G, K, N))
     nbytes = H.total_bytes(M, K, N, G, 4)
-    log(f"rotation: {rot_w.count} copies, {rot_w.total_bytes / 2**30:.2f} GiB of packed weights")
+    log(f"rotation: {len(variants)} copies, {H.ring_bytes(variants) / 2**30:.2f} GiB of packed "
+        "weights and scales")
 
     # ---- warmup (untimed, eager) ---------------------------------------------
     for i in range(warmup):
@@ -154,7 +193,7 @@ def main() -> int:
     runner = H.GraphRunner(lambda i: ng.gemv(X, variants[i]), reps=steps, warmup=0)
     runner.graph.replay()  # untimed: first replay uploads the graph
     torch.cuda.synchronize()
-    ms_per_step, clocks = runner.time_once(warm_s=0.25)
+    ms_per_step, replays, clocks = runner.time_window(min_ms=args.min_window_ms, warm_s=0.25)
     torch.cuda.synchronize()
     gbps = H.achieved_gbps(nbytes, ms_per_step)
     log(f"gemv M=1 {K}x{N}: {ms_per_step * 1e3:.2f} us/step, {gbps:.0f} GB/s "
@@ -172,7 +211,7 @@ def main() -> int:
         extras["pct_of_read_bw"] = round(100 * gbps / read["read_gbps"], 1)
         torch.backends.cuda.matmul.allow_tf32 = False
         w16 = (torch.randn((K, N), generator=gen) * 0.02).to(torch.float16).to(dev)
-        rot16 = H.Rotation(w16)
+        rot16 = H.tensor_ring(w16)
         fp16 = H.bench_graph(lambda i: torch.mm(X, rot16[i]), reps=64, trials=10)
         extras["hipblaslt_fp16_us"] = round(fp16.median_ms * 1e3, 2)
         extras["speedup_vs_hipblaslt_fp16"] = round(fp16.median_ms / ms_per_step, 2)
@@ -181,7 +220,7 @@ def main() -> int:
         del rot16, w16
         # The same GEMV on strip-major copies of the rotation (the decode
         # kernel's contiguous-strip layout; same bytes per call).
-        sm = H.Cycle([ng.to_strip_major(variants[i]) for i in range(rot_w.count)])
+        sm = variants.map(ng.to_strip_major)
         smt = H.bench_graph(lambda i: ng.matmul(X, sm[i]), reps=64, trials=10)
         extras["strip_major"] = {
             "strip_cols": sm[0].strip_cols, "us": round(smt.median_ms * 1e3, 2),
@@ -196,7 +235,7 @@ def main() -> int:
     if not args.skip_decode_step:
         from nibblegemm_amd import decode_step  # noqa: PLC0415
 
-        del variants, rot_w, rot_s
+        del variants
         torch.cuda.empty_cache()
         t0 = time.perf_counter()
         decode = decode_step.run(32)
@@ -270,7 +309,7 @@ def main() -> int:
     cpu = None
     if not args.no_cpu_baseline:
         t0 = time.perf_counter()
-        cpu = cpu_baseline(args.cpu_seconds)
+        cpu = cpu_baseline(args.cpu_seconds, per_shape=not args.no_cpu_shapes)
         log(f"cpu baseline {cpu['value']} GB/s on {cpu['cores']} threads "
             f"({time.perf_counter() - t0:.1f} s)")
 
@@ -281,6 +320,8 @@ def main() -> int:
         "n_gpus": 1,
         "steps": steps,
         "warmup": warmup,
+        "timed_replays": replays,
+        "timed_window_ms": round(ms_per_step * replays * steps, 3),
         "ms_per_step": round(ms_per_step, 6),
         "higher_is_better": True,
         "scaling": "weak",

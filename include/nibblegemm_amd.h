@@ -108,7 +108,10 @@ NIBBLE_API int nibble_gemv_w4a16(const void* X, int64_t x_rows, int64_t x_cols,
  * fp32 partials [splits, M, N]); a request needing more than that fails with
  * NIBBLE_ERR_UNSUPPORTED before anything is launched.  Every call on a GPU
  * shares that GPU's array: calls that overlap on one GPU (other streams or
- * threads) race and must be serialised by the caller.
+ * threads) race and must be serialised by the caller.  The first split-K
+ * call on a GPU clears the counters and waits for that to finish, so it
+ * cannot itself be captured into a graph: under capture it fails with
+ * NIBBLE_ERR_UNSUPPORTED (make one such call before capturing).
  */
 NIBBLE_API int nibble_gemv_w4a16_noalloc(const void* X, int64_t x_rows, int64_t x_cols,
                       const void* Wq, int64_t wq_rows, int64_t wq_cols,
@@ -286,21 +289,6 @@ NIBBLE_API size_t nibble_attention_decode_workspace_bytes(int64_t n_heads, int64
 NIBBLE_API size_t nibble_attention_decode_counter_bytes(int64_t n_heads, int64_t n_kv_heads,
                                                         int64_t head_dim, int64_t max_seq,
                                                         int64_t pos, void* stream);
-
-/*
- * GPTQ's column loop over one quantisation group (replaces the per-channel
- * PyTorch loop of gptq_quantize, python/nibblegemm/gptq.py:103-122).
- * W: fp32 rows of the group's G input channels for N output rows (row n at
- * W + n * ldw; the [out, in] orientation GPTQ works in).  U: the group's
- * G x G block of the upper Cholesky factor of H^-1 (row stride ldu).
- * Writes, per row n: Q[n * ldq + i] = q + 8 (uint8, 0..15), E[n * G + i] =
- * the compensation residual err_i, and scales[n] (fp32).  W and U are only
- * read.  G must be 64 or 128.  Arithmetic as the reference's ops, each
- * rounded on its own; see nibblegemm_amd/csrc/gptq.hip.
- */
-NIBBLE_API int nibble_gptq_group_f32(const void* W, int64_t ldw, int64_t N, int64_t G,
-                                     const void* U, int64_t ldu, void* Q, int64_t ldq, void* E,
-                                     void* scales, void* stream);
 
 /*
  * Measurement: a streaming read of `bytes` (a positive multiple of 16) from

@@ -6,15 +6,14 @@ Drop-in for the Python surface of arvindcr4/nibblegemm
 kernel entry points, the batch-size dispatch and ``QuantLinear``.  The kernels
 are hand-written HIP behind the C ABI in ``include/nibblegemm_amd.h``.
 
-The reference's GPTQ quantiser is here too (``gptq_quantize``,
-``quantize_model_gptq``, ``HessianAccumulator``, ``find_decoder_blocks``, in
-:mod:`nibblegemm_amd.gptq`, its column loop a kernel of this library);
-symmetric GPTQ / AWQ 4-bit checkpoints are converted by
-:mod:`nibblegemm_amd.convert`.  The reference's Triton baseline is not.
+Symmetric GPTQ / AWQ 4-bit checkpoints are converted into the packed format
+by :mod:`nibblegemm_amd.convert`.  The reference's offline GPTQ quantiser
+(python/nibblegemm/gptq.py) is not part of this library: its names are kept
+as stubs that raise ``NotImplementedError``, so ``from nibblegemm_amd import
+*`` keeps the reference package's namespace.  Its Triton baseline is absent.
 """
 
-from . import convert, gptq
-from .gptq import HessianAccumulator, find_decoder_blocks, gptq_quantize, quantize_model_gptq
+from . import convert
 from .ops import (DECODE_MAX_M, QuantLinear, dequant, extension, gemm, gemv, matmul, matmul_bias,
                   matmul_swiglu, rmsnorm_matmul, strip_major_cols, to_strip_major)
 from .quant import (
@@ -37,7 +36,6 @@ __all__ = [
     "QuantizedWeight",
     "concat_columns",
     "convert",
-    "gptq",
     "gptq_quantize",
     "dequant",
     "dequantize",
@@ -61,3 +59,22 @@ __all__ = [
     "unpack_nibbles",
 ]
 __version__ = "0.1.0"
+
+
+def _not_built(name: str):
+    msg = (f"{name} is the reference's offline GPTQ quantiser (python/nibblegemm/gptq.py), "
+           "which nibblegemm_amd does not provide; quantise with nibblegemm_amd.quantize "
+           "(RTN) or convert a GPTQ checkpoint with nibblegemm_amd.convert.from_gptq")
+
+    def stub(*_args, **_kwargs):
+        raise NotImplementedError(msg)
+
+    stub.__name__ = stub.__qualname__ = name
+    stub.__doc__ = msg
+    return stub
+
+
+gptq_quantize = _not_built("gptq_quantize")
+quantize_model_gptq = _not_built("quantize_model_gptq")
+find_decoder_blocks = _not_built("find_decoder_blocks")
+HessianAccumulator = _not_built("HessianAccumulator")

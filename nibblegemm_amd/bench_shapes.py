@@ -47,15 +47,12 @@ def _weights(K: int, N: int, G: int, seed: int):
     qu = torch.randint(0, 16, (K, N), generator=gen, dtype=torch.uint8).numpy()
     qweight = torch.from_numpy(pack_nibbles(qu)).cuda()
     scales = (torch.rand((K // G, N), generator=gen) * 0.018 + 0.002).to(torch.float16).cuda()
-    rot = H.Rotation(qweight)
-    srot = [scales] + [scales.clone() for _ in range(rot.count - 1)]
-    qws = H.Cycle(QuantizedWeight(rot[i], srot[i], G, K, N) for i in range(rot.count))
-    return qws, gen
+    return H.weight_ring(QuantizedWeight(qweight, scales, G, K, N)), gen
 
 
 def _fp16_baseline(qw: QuantizedWeight):
     """fp16 copies of the same (dequantized) weight, rotated through >= 1 GiB."""
-    return H.Rotation(ops.dequant(qw))
+    return H.tensor_ring(ops.dequant(qw))
 
 
 def _check(y: torch.Tensor, X: torch.Tensor, qw: QuantizedWeight, what: str) -> float:
@@ -125,7 +122,7 @@ def decode(args, rows):
     for K, N in DECODE_SHAPES:
         qws, gen = _weights(K, N, args.group_size, seed=K + N)
         w16 = _fp16_baseline(qws[0])
-        sms = H.Cycle(ops.to_strip_major(qw) for qw in qws.items)
+        sms = qws.map(ops.to_strip_major)
         H.spin_up(0.2)  # host-side setup above let the clock drop
         for M in args.M or [1, 2, 4, 8]:
             X = torch.randn((M, K), generator=gen).to(torch.float16).cuda()

@@ -232,20 +232,6 @@ static PyObject* py_attention_ws(PyObject* self, PyObject* const* a, Py_ssize_t 
   return Py_BuildValue("(nn)", (Py_ssize_t)ws, (Py_ssize_t)cb);
 }
 
-/* gptq_group(W, ldw, N, G, U, ldu, Q, ldq, E, scales, stream) */
-static PyObject* py_gptq_group(PyObject* self, PyObject* const* a, Py_ssize_t n) {
-  (void)self;
-  if (!nargs_is(n, 11, "gptq_group")) return NULL;
-  void *W, *U, *Q, *E, *S, *stream;
-  long long ldw, N, G, ldu, ldq;
-  if (!take_ptr(a[0], &W) || !take_i64(a[1], &ldw) || !take_i64(a[2], &N) ||
-      !take_i64(a[3], &G) || !take_ptr(a[4], &U) || !take_i64(a[5], &ldu) ||
-      !take_ptr(a[6], &Q) || !take_i64(a[7], &ldq) || !take_ptr(a[8], &E) ||
-      !take_ptr(a[9], &S) || !take_ptr(a[10], &stream))
-    return NULL;
-  return PyLong_FromLong(nibble_gptq_group_f32(W, ldw, N, G, U, ldu, Q, ldq, E, S, stream));
-}
-
 /* dequant(Wq, wr, wc, S, sr, sc, g, fast, W, stream) */
 static PyObject* py_dequant(PyObject* self, PyObject* const* a, Py_ssize_t n) {
   (void)self;
@@ -298,8 +284,6 @@ static PyMethodDef kMethods[] = {
      "nibble_attention_decode_f16"},
     {"attention_workspace_bytes", (PyCFunction)(void (*)(void))py_attention_ws, METH_FASTCALL,
      "(nibble_attention_decode_workspace_bytes, nibble_attention_decode_counter_bytes)"},
-    {"gptq_group", (PyCFunction)(void (*)(void))py_gptq_group, METH_FASTCALL,
-     "nibble_gptq_group_f32"},
     {"last_error", py_last_error, METH_NOARGS, "nibble_last_error"},
     {"abi_version", py_abi_version, METH_NOARGS, "nibble_abi_version"},
     {NULL, NULL, 0, NULL}};

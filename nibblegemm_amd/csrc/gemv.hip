@@ -1521,17 +1521,29 @@ __global__ void zero_words_kernel(uint32_t* __restrict__ p, uint32_t n) {
 // The device address of `scratch` on `device` (which must be current), set
 // up on the device's first use: the address comes from the runtime (in host
 // code the array's name only stands for the symbol), and the counter region
-// is cleared by a kernel on `stream`, ahead of the call that asked.
+// is cleared by a kernel on `stream` that completes before the address is
+// published, so every later call on any stream of the device finds it zero.
+// That first use cannot be captured into a graph (the clearing would exist
+// only inside the graph): it is refused while `stream` is capturing.
 int scratch_on(int device, hipStream_t stream, void** addr) {
   if (device < 0 || device >= kScratchDevices)
     return fail(NIBBLE_ERR_UNSUPPORTED, "no-alloc scratch: device %d out of range", device);
   std::lock_guard<std::mutex> lock(g_scratch_mutex);
   if (g_scratch_addr[device] == nullptr) {
+    hipStreamCaptureStatus capturing = hipStreamCaptureStatusNone;
+    NIBBLE_HIP(hipStreamIsCapturing(stream, &capturing));
+    if (capturing != hipStreamCaptureStatusNone)
+      return fail(NIBBLE_ERR_UNSUPPORTED,
+                  "nibble_gemv_w4a16_noalloc: the first split-K call on device %d sets up the "
+                  "static scratch and cannot run under graph capture; make one such call "
+                  "outside the capture first",
+                  device);
     void* p = nullptr;
     NIBBLE_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
     const uint32_t words = static_cast<uint32_t>(kScratchCounterBytes / 4);
     zero_words_kernel<<<(words + 255) / 256, 256, 0, stream>>>(static_cast<uint32_t*>(p), words);
     NIBBLE_HIP(hipGetLastError());
+    NIBBLE_HIP(hipStreamSynchronize(stream));
     g_scratch_addr[device] = p;
   }
   *addr = g_scratch_addr[device];

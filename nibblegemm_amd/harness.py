@@ -26,7 +26,7 @@ import statistics
 import threading
 import time
 from dataclasses import dataclass, field
-from typing import Callable, Dict, List, Optional, Sequence
+from typing import Callable, Dict, List, Optional, Sequence, Tuple
 
 import torch
 
@@ -172,55 +172,74 @@ class ClockMonitor:
         return out
 
 
-@dataclass
+@dataclass(frozen=True)
 class Timing:
-    median_ms: float
-    p05_ms: float
-    p95_ms: float
-    trials: int
+    """One measurement: the per-call time of each timed window, in ms.
+
+    A window spans ``reps`` calls between two events; ``windows_ms`` holds
+    each window's elapsed time divided by ``reps``.  Quantiles interpolate
+    linearly between the sorted windows (numpy's default definition)."""
+
+    windows_ms: Tuple[float, ...]
     reps: int
-    samples: Sequence[float] = field(default_factory=list, repr=False)
     clocks: Dict[str, object] = field(default_factory=dict)
 
     @property
-    def spread_pct(self) -> float:
-        return 100.0 * (self.p95_ms - self.p05_ms) / self.median_ms if self.median_ms else 0.0
+    def trials(self) -> int:
+        return len(self.windows_ms)
+
+    def quantile_ms(self, q: float) -> float:
+        xs = sorted(self.windows_ms)
+        if not xs:
+            return float("nan")
+        pos = q * (len(xs) - 1)
+        lo = int(math.floor(pos))
+        hi = min(lo + 1, len(xs) - 1)
+        return xs[lo] + (pos - lo) * (xs[hi] - xs[lo])
+
+    @property
+    def median_ms(self) -> float:
+        return self.quantile_ms(0.5)
+
+    @property
+    def p05_ms(self) -> float:
+        return self.quantile_ms(0.05)
+
+    @property
+    def p95_ms(self) -> float:
+        return self.quantile_ms(0.95)
 
     @property
     def throttled(self) -> bool:
         return bool(self.clocks.get("throttled", False))
 
 
-def _summarise(samples: List[float], trials: int, reps: int,
-               clocks: Optional[Dict[str, object]] = None) -> Timing:
-    samples = sorted(samples)
-    return Timing(
-        median_ms=statistics.median(samples),
-        p05_ms=samples[max(0, int(0.05 * len(samples)) - 1)],
-        p95_ms=samples[min(len(samples) - 1, int(0.95 * len(samples)))],
-        trials=trials, reps=reps, samples=samples, clocks=clocks or {},
-    )
+def _new_event() -> "torch.cuda.Event":
+    return torch.cuda.Event(enable_timing=True)
 
 
 def bench(fn: Callable[[int], object], *, reps: int = 32, trials: int = 20,
           warmup: int = 5) -> Timing:
-    """Eager: one event pair spans ``reps`` back-to-back calls of ``fn(i)``."""
+    """Eager timing of ``fn(i)``.  Every window's event pair is recorded up
+    front on the current stream, the calls are issued back to back (their
+    index keeps counting across windows, so a rotation advances through all
+    of its copies), and one synchronisation at the end collects the windows:
+    no host round trip sits between windows."""
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    samples = []
+    marks = [(_new_event(), _new_event()) for _ in range(trials)]
     mon = ClockMonitor().start()
-    for _ in range(trials):
-        torch.cuda.synchronize()
-        start.record()
-        for r in range(reps):
-            fn(r)
-        end.record()
-        torch.cuda.synchronize()
-        samples.append(start.elapsed_time(end) / reps)
-    return _summarise(samples, trials, reps, mon.stop())
+    call = 0
+    for first, last in marks:
+        first.record()
+        for _ in range(reps):
+            fn(call)
+            call += 1
+        last.record()
+    torch.cuda.synchronize()
+    clocks = mon.stop()
+    return Timing(tuple(a.elapsed_time(b) / reps for a, b in marks), reps, clocks)
 
 
 class GraphRunner:
@@ -263,34 +282,43 @@ class GraphRunner:
             self.graph.replay()
         time.sleep(max(0.0, (n - 1) * per))
 
-    def time_once(self, warm_s: float = 0.25):
-        """One timed replay after :meth:`warm`; returns (ms per call, clock
-        summary).  The clock monitor starts while the GPU is still busy with
-        the warm-up, so its first sample is the clock the timed replay starts
-        at and its last the clock it ends at."""
-        self.warm(warm_s)
-        mon = ClockMonitor().start()
-        start = torch.cuda.Event(enable_timing=True)
-        end = torch.cuda.Event(enable_timing=True)
-        start.record()
-        self.graph.replay()
-        end.record()
-        end.synchronize()
-        return start.elapsed_time(end) / self.reps, mon.stop()
-
     def time(self, trials: int = 20, warm_s: float = 0.05) -> Timing:
-        start = torch.cuda.Event(enable_timing=True)
-        end = torch.cuda.Event(enable_timing=True)
+        """``trials`` windows of one replay each, back to back after
+        :meth:`warm` (one synchronisation at the end)."""
         self.warm(warm_s)
-        samples = []
+        marks = [(_new_event(), _new_event()) for _ in range(trials)]
         mon = ClockMonitor().start()
-        for _ in range(trials):
-            start.record()
+        for first, last in marks:
+            first.record()
             self.graph.replay()
-            end.record()
-            end.synchronize()
-            samples.append(start.elapsed_time(end) / self.reps)
-        return _summarise(samples, trials, self.reps, mon.stop())
+            last.record()
+        torch.cuda.synchronize()
+        clocks = mon.stop()
+        return Timing(tuple(a.elapsed_time(b) / self.reps for a, b in marks), self.reps, clocks)
+
+    def time_window(self, min_ms: float = 20.0, warm_s: float = 0.25):
+        """One timed window of whole replays lasting at least ``min_ms``.
+
+        The replay count comes from an untimed replay's duration, so the
+        window's length does not depend on how many calls the graph holds.
+        Returns (ms per call, replays, clock summary); ms per call is the
+        window over replays x calls per replay."""
+        first, last = _new_event(), _new_event()
+        first.record()
+        self.graph.replay()
+        last.record()
+        last.synchronize()
+        per_replay = max(first.elapsed_time(last), 1e-4)
+        replays = max(1, math.ceil(min_ms / per_replay))
+        self.warm(warm_s)
+        mon = ClockMonitor().start()
+        first.record()
+        for _ in range(replays):
+            self.graph.replay()
+        last.record()
+        last.synchronize()
+        clocks = mon.stop()
+        return first.elapsed_time(last) / (replays * self.reps), replays, clocks
 
 
 def bench_graph(fn: Callable[[int], object], *, reps: int = 32, trials: int = 20,
@@ -306,21 +334,19 @@ def bench_graph_pair(fn_a: Callable[[int], object], fn_b: Callable[[int], object
     other would charge that to whichever runs second.  Returns (Timing a,
     Timing b)."""
     runners = (GraphRunner(fn_a, reps, warmup), GraphRunner(fn_b, reps, warmup))
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
     for r in runners:
         r.warm(0.025)
-    samples = ([], [])
+    marks = [[(_new_event(), _new_event()) for _ in range(trials)] for _ in runners]
     mon = ClockMonitor().start()
-    for _ in range(trials):
-        for r, out in zip(runners, samples):
-            start.record()
+    for t in range(trials):
+        for r, m in zip(runners, marks):
+            m[t][0].record()
             r.graph.replay()
-            end.record()
-            end.synchronize()
-            out.append(start.elapsed_time(end) / reps)
+            m[t][1].record()
+    torch.cuda.synchronize()
     clocks = mon.stop()
-    return tuple(_summarise(s, trials, reps, clocks) for s in samples)
+    return tuple(Timing(tuple(a.elapsed_time(b) / reps for a, b in m), reps, clocks)
+                 for m in marks)
 
 
 def spin_up(seconds: float = 0.3) -> None:
@@ -396,29 +422,58 @@ def measured_read_gbps(size_bytes: int = 2 << 30, workgroups=(2048, 4096, 8192))
     return {"read_gbps": round(best[0], 1), "read_workgroups": best[1]}
 
 
-class Rotation:
-    """Copies of a tensor spanning at least ``min_total_bytes`` in total."""
+class Ring:
+    """A fixed tuple of objects indexed modulo its length: ``ring[i]`` for any
+    call index ``i``.  Timed loops index rings of weight copies this way so
+    that consecutive calls read different copies."""
 
-    def __init__(self, proto: torch.Tensor, min_total_bytes: int = ROTATION_BYTES, cap: int = 512):
-        nbytes = proto.numel() * proto.element_size()
-        count = max(1, min(cap, -(-min_total_bytes // max(nbytes, 1))))
-        self.buffers = [proto] + [proto.clone() for _ in range(count - 1)]
-        self.count = len(self.buffers)
-        self.total_bytes = self.count * nbytes
-
-    def __getitem__(self, i: int) -> torch.Tensor:
-        return self.buffers[i % self.count]
-
-
-class Cycle:
     def __init__(self, items):
-        self.items = list(items)
+        self.items = tuple(items)
+        if not self.items:
+            raise ValueError("a ring needs at least one item")
+
+    def __len__(self) -> int:
+        return len(self.items)
 
     def __getitem__(self, i: int):
         return self.items[i % len(self.items)]
 
-    def __len__(self) -> int:
-        return len(self.items)
+    def map(self, fn: Callable[[object], object]) -> "Ring":
+        return Ring(fn(x) for x in self.items)
+
+
+def copies_for(nbytes: int, min_total_bytes: int = ROTATION_BYTES, cap: int = 512) -> int:
+    """How many copies of an ``nbytes`` object together span
+    ``min_total_bytes`` (at least one, at most ``cap``)."""
+    if nbytes <= 0:
+        return 1
+    return max(1, min(cap, math.ceil(min_total_bytes / nbytes)))
+
+
+def tensor_ring(proto: torch.Tensor, min_total_bytes: int = ROTATION_BYTES,
+                cap: int = 512) -> Ring:
+    """``proto`` and clones of it, enough to span ``min_total_bytes``."""
+    n = copies_for(proto.numel() * proto.element_size(), min_total_bytes, cap)
+    return Ring([proto, *(proto.clone() for _ in range(n - 1))])
+
+
+def weight_ring(qw, min_total_bytes: int = ROTATION_BYTES, cap: int = 512) -> Ring:
+    """Copies of a packed weight (``QuantizedWeight``: its int32 words and its
+    scales cloned together) spanning ``min_total_bytes``: each call of a
+    timed loop then streams its weights from HBM, not from the 256 MiB
+    Infinity Cache."""
+    n = copies_for(qw.weight_bytes, min_total_bytes, cap)
+    same = type(qw)
+    return Ring([qw, *(same(qw.qweight.clone(), qw.scales.clone(), qw.group_size, qw.K, qw.N)
+                       for _ in range(n - 1))])
+
+
+def ring_bytes(ring: Ring) -> int:
+    """Total bytes held by a ring of tensors or packed weights."""
+    total = 0
+    for x in ring.items:
+        total += x.weight_bytes if hasattr(x, "weight_bytes") else x.numel() * x.element_size()
+    return total
 
 
 # --------------------------------------------------------------------------
@@ -448,7 +503,12 @@ def tflops(M: int, K: int, N: int, ms: float) -> float:
 
 
 def markdown_table(rows: Sequence[dict], columns: Sequence[str]) -> str:
-    head = "| " + " | ".join(columns) + " |"
-    rule = "|" + "|".join("---" for _ in columns) + "|"
-    body = ["| " + " | ".join(str(r.get(c, "")) for c in columns) + " |" for r in rows]
-    return "\n".join([head, rule, *body])
+    """A GitHub table of ``rows`` (dicts; missing keys left blank), with every
+    column padded to its widest cell so the text lines up as well."""
+    grid = [list(map(str, columns))] + [["" if r.get(c) is None else str(r.get(c))
+                                         for c in columns] for r in rows]
+    width = [max(len(line[j]) for line in grid) for j in range(len(columns))]
+    text = ["| " + " | ".join(cell.ljust(w) for cell, w in zip(line, width)) + " |"
+            for line in grid]
+    text.insert(1, "| " + " | ".join("-" * w for w in width) + " |")
+    return "\n".join(text)

@@ -451,12 +451,18 @@ def matmul_bias(X: torch.Tensor, qw: QuantizedWeight, bias: torch.Tensor) -> tor
 def matmul_swiglu(X: torch.Tensor, qw: QuantizedWeight) -> torch.Tensor:
     """``silu(X @ W_gate) * (X @ W_up)`` for ``qw = interleave_swiglu(gate,
     up)``, with the fp16 roundings of the unfused ops (the two products,
-    silu, then the product).  M <= 128 runs as one launch."""
+    silu, then the product).  M <= 128 runs as one launch; so does a
+    strip-major weight whose strips hold whole gate|up block pairs (at least
+    32 columns), while narrower strips compose the same arithmetic from the
+    plain product."""
     _check_2d(X, qw)
     if qw.N % (2 * SWIGLU_BLOCK):
         raise ValueError(f"N={qw.N} is not an interleaved gate|up weight (multiple of 32)")
     if isinstance(qw, StripMajorWeight):
-        return _strip_gemv(X, qw, 2, None, qw.N // 2)
+        if qw.strip_cols >= 2 * SWIGLU_BLOCK:
+            return _strip_gemv(X, qw, 2, None, qw.N // 2)
+        gate, up = split_swiglu(_strip_gemv(X, qw, 0, None, qw.N))
+        return torch.nn.functional.silu(gate) * up
     if _fusable(X, qw):
         return _fused(X, qw, 2, None, qw.N // 2)
     gate, up = split_swiglu(matmul(X, qw))
@@ -493,6 +499,8 @@ def rmsnorm_matmul(X: torch.Tensor, norm_weight: torch.Tensor, qw: QuantizedWeig
     mt = 1 if M <= 1 else 2 if M <= 2 else 4 if M <= 4 else 8
     strip = isinstance(qw, StripMajorWeight)
     fusable = (X.dim() == 2 and X.is_cuda and X.is_contiguous()) if strip else _fusable(X, qw)
+    if swiglu and strip and qw.strip_cols < 2 * SWIGLU_BLOCK:
+        fusable = False  # the SwiGLU epilogue needs whole gate|up block pairs per strip
     if (fusable and M <= NORM_FUSED_MAX_M and K <= NORM_FUSED_MAX_K and mt * K * 2 <= 65536
             and norm_weight.dtype == torch.float16 and norm_weight.is_contiguous()
             and norm_weight.device == X.device and norm_weight.numel() == K

@@ -35,9 +35,7 @@ def _weights(K: int, N: int, G: int, dev):
     qu = torch.randint(0, 16, (K, N), generator=gen, dtype=torch.uint8).numpy()
     qweight = torch.from_numpy(pack_nibbles(qu)).to(dev)
     scales = (torch.rand((K // G, N), generator=gen) * 0.018 + 0.002).to(torch.float16).to(dev)
-    rot = H.Rotation(qweight)
-    rs = [scales] + [scales.clone() for _ in range(rot.count - 1)]
-    return H.Cycle(QuantizedWeight(rot[i], rs[i], G, K, N) for i in range(rot.count)), gen
+    return H.weight_ring(QuantizedWeight(qweight, scales, G, K, N)), gen
 
 
 def main(argv=None) -> int:
@@ -66,7 +64,7 @@ def main(argv=None) -> int:
     elif args.kernel == "fp16mm":
         qws, gen = _weights(args.K, args.N, args.G, dev)
         X = torch.randn((args.M, args.K), generator=gen).to(torch.float16).to(dev)
-        w16 = H.Rotation(ops.dequant(qws[0]))
+        w16 = H.tensor_ring(ops.dequant(qws[0]))
         torch.backends.cuda.matmul.allow_tf32 = False
         torch.cuda.synchronize()
         for i in range(args.calls):

@@ -266,16 +266,18 @@ def strip_major(qw: QuantizedWeight, strip_cols: int) -> StripMajorWeight:
 
 def pack_nibbles(qu: np.ndarray) -> np.ndarray:
     """Codes ``[K, N]`` (values 0..15) to packed words ``int32 [K // 8, N]``
-    (reference quant.py:164-182).  Each code is shifted to its nibble slot and
-    the eight of a word are OR-ed in uint32 (no sign to overflow into); the
-    words are returned viewed as int32, the dtype the kernels take."""
+    (reference quant.py:164-182).  Each code is masked to its low four bits
+    (as the reference does, so a negative signed code wraps into its own
+    nibble: -1 packs as 15), shifted to its nibble slot, and the eight of a
+    word are OR-ed in uint32 (no sign to overflow into); the words are
+    returned viewed as int32, the dtype the kernels take."""
     qu = np.asarray(qu)
     K, N = qu.shape
     if K % PACK_FACTOR:
         raise ValueError(f"K={K} must be divisible by {PACK_FACTOR}")
     if qu.max(initial=0) > 15:
         raise ValueError("quantised values must fit in 4 bits")
-    codes = qu.reshape(K // PACK_FACTOR, PACK_FACTOR, N).astype(np.uint32)
+    codes = qu.reshape(K // PACK_FACTOR, PACK_FACTOR, N).astype(np.uint32) & np.uint32(0xF)
     words = np.bitwise_or.reduce(codes << _SHIFTS[None, :, None], axis=1)
     return np.ascontiguousarray(words, dtype=np.uint32).view(np.int32)
 

@@ -12,7 +12,6 @@
  *   nibble_oracle_pack            python/nibblegemm/quant.py:164-182
  *   nibble_oracle_unpack          python/nibblegemm/quant.py:185-196
  *   nibble_oracle_quantize_rtn    python/nibblegemm/quant.py:127-161 (clip_search=False)
- *   nibble_oracle_gptq_group      python/nibblegemm/gptq.py:103-122 (one group's column loop)
  *   nibble_oracle_dequantize      python/nibblegemm/quant.py:199-204
  *   nibble_oracle_matmul_f32      python/nibblegemm/quant.py:207-215
  *   nibble_oracle_matmul_f64      (brute-force double-precision check, no counterpart)
@@ -239,57 +238,6 @@ void nibble_oracle_matmul_f64(const uint16_t* X, const uint16_t* W, int64_t M, i
       Y[m * N + n] = acc;
     }
   }
-}
-
-/* ------------------------------------------------------------------------- */
-/* GPTQ: one quantisation group's column loop                                 */
-/* ------------------------------------------------------------------------- */
-/* python/nibblegemm/gptq.py:103-122.  W holds the group's G input channels of
- * N output rows, row n at W + n * ldw (GPTQ's [out, in] orientation); U is the
- * group's G x G block of the upper Cholesky factor of H^-1.  Per row, in
- * float32 with every operation rounded on its own (this file is compiled
- * with -ffp-contract=off):
- *   scale = max(amax(row) * (1/7 rounded to float), 1e-8);  inv = 1 / scale
- *     (the reference divides a GPU tensor by the Python int 7, which PyTorch
- *      evaluates as a multiply by the float reciprocal)
- *   for i in 0..G-1: q = clamp(rint(w_i * inv), -8, 7)
- *                    err = (w_i - q * scale) / U[i][i]
- *                    w_j = w_j - err * U[i][j]  for j > i
- * Outputs q + 8, err and scale.  G is any positive size here (tests use tiny
- * groups to check the recurrence by hand). */
-int nibble_oracle_gptq_group(const float* W, int64_t ldw, int64_t N, int64_t G, const float* U,
-                             int64_t ldu, uint8_t* Q, int64_t ldq, float* E, float* scales) {
-  if (G <= 0 || ldw < G || ldu < G || ldq < G) return -1;
-  const float inv7 = 1.0f / 7.0f;
-  float* w = (float*)malloc((size_t)G * sizeof(float));
-  if (w == NULL) return -2;
-  for (int64_t n = 0; n < N; ++n) {
-    float amax = 0.0f;
-    for (int64_t j = 0; j < G; ++j) {
-      w[j] = W[n * ldw + j];
-      const float a = fabsf(w[j]);
-      if (a > amax) amax = a;
-    }
-    float scale = amax * inv7;
-    if (scale < 1e-8f) scale = 1e-8f;
-    const float inv = 1.0f / scale;
-    for (int64_t i = 0; i < G; ++i) {
-      float q = nearbyintf(w[i] * inv); /* FE_TONEAREST: ties to even, as torch.round */
-      if (q < -8.0f) q = -8.0f;
-      if (q > 7.0f) q = 7.0f;
-      const float qs = q * scale;
-      const float err = (w[i] - qs) / U[i * ldu + i];
-      Q[n * ldq + i] = (uint8_t)((int)q + 8);
-      E[n * G + i] = err;
-      for (int64_t j = i + 1; j < G; ++j) {
-        const float d = err * U[i * ldu + j];
-        w[j] = w[j] - d;
-      }
-    }
-    scales[n] = scale;
-  }
-  free(w);
-  return 0;
 }
 
 int nibble_oracle_max_threads(void) {

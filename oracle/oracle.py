@@ -15,8 +15,6 @@ Reference lines each function follows:
 ``pack_nibbles``       python/nibblegemm/quant.py:164-182
 ``unpack_nibbles``     python/nibblegemm/quant.py:185-196
 ``quantize_rtn``       python/nibblegemm/quant.py:127-161 (clip_search=False)
-``gptq_group``         python/nibblegemm/gptq.py:103-122 (one group's column loop)
-``gptq_quantize``      python/nibblegemm/gptq.py:65-134 given the factor U
 ``dequantize``         python/nibblegemm/quant.py:199-204
 ``reference_matmul``   python/nibblegemm/quant.py:207-215
 ``matmul_f64``         brute-force double-precision product (no counterpart)
@@ -70,8 +68,6 @@ def lib():
         L.nibble_oracle_quantize_rtn.restype = ctypes.c_int
         L.nibble_oracle_quantize_rtn.argtypes = [p, i64, i64, i64, p, p, p]
         L.nibble_oracle_dequantize.argtypes = [p, p, i64, i64, i64, p]
-        L.nibble_oracle_gptq_group.restype = ctypes.c_int
-        L.nibble_oracle_gptq_group.argtypes = [p, i64, i64, i64, p, i64, p, i64, p, p]
         L.nibble_oracle_matmul_f32.argtypes = [p, p, i64, i64, i64, p, p]
         L.nibble_oracle_matmul_f64.argtypes = [p, p, i64, i64, i64, p]
         L.nibble_oracle_max_threads.restype = ctypes.c_int
@@ -153,47 +149,6 @@ def quantize_rtn(W: np.ndarray, group_size: int = 128):
     return qu, s32, s16.view(np.float16)
 
 
-def gptq_group(W1: np.ndarray, U1: np.ndarray):
-    """One group's column loop: W1 float32 [N, G] (rows = output channels),
-    U1 float32 [G, G] (upper factor) -> (qu uint8 [N, G], err float32 [N, G],
-    scales float32 [N])."""
-    W1 = np.ascontiguousarray(W1, dtype=np.float32)
-    U1 = np.ascontiguousarray(U1, dtype=np.float32)
-    N, G = W1.shape
-    assert U1.shape == (G, G)
-    qu = np.empty((N, G), dtype=np.uint8)
-    err = np.empty((N, G), dtype=np.float32)
-    sc = np.empty(N, dtype=np.float32)
-    rc = lib().nibble_oracle_gptq_group(_ptr(W1), G, N, G, _ptr(U1), G, _ptr(qu), G, _ptr(err),
-                                        _ptr(sc))
-    if rc != 0:
-        raise ValueError(f"gptq_group failed ({rc})")
-    return qu, err, sc
-
-
-def gptq_quantize(W: np.ndarray, U: np.ndarray, group_size: int):
-    """GPTQ of W float32 [K, N] given the upper factor U float32 [K, K] of the
-    damped inverse Hessian: groups in order, each group's column loop, then
-    the later channels updated by err @ U[group, later] (a float32 numpy
-    product, whose summation order is BLAS's).  Dead-channel handling and the
-    factorisation are the caller's.  Returns (qu uint8 [K, N], scales float32
-    [K/G, N])."""
-    Wt = np.ascontiguousarray(np.asarray(W, dtype=np.float32).T)
-    U = np.asarray(U, dtype=np.float32)
-    N, K = Wt.shape
-    G = group_size
-    qu = np.empty((N, K), dtype=np.uint8)
-    scales = np.empty((K // G, N), dtype=np.float32)
-    for i1 in range(0, K, G):
-        i2 = i1 + G
-        q, err, sc = gptq_group(Wt[:, i1:i2], U[i1:i2, i1:i2])
-        qu[:, i1:i2] = q
-        scales[i1 // G] = sc
-        if i2 < K:
-            Wt[:, i2:] -= err @ U[i1:i2, i2:]
-    return np.ascontiguousarray(qu.T), scales
-
-
 def dequantize(packed: np.ndarray, scales, K: int, group_size: int) -> np.ndarray:
     """fp16 [K, N] = f16((nibble-8) * f32(scale)) (quant.py:199-204)."""
     p = np.ascontiguousarray(packed).view(np.uint32)
@@ -271,26 +226,32 @@ def synthetic_case(M: int, K: int, N: int, group_size: int = 128, seed: int = 0)
 # CPU baseline timing (reported only)
 # --------------------------------------------------------------------------
 def time_reference_path(M: int, K: int, N: int, group_size: int = 128, reps: int = 5,
-                        threads: int = 0, seed: int = 0) -> dict:
-    """Time dequantize + reference matmul on this host's cores (median of reps)."""
+                        threads: int = 0, seed: int = 0, max_rows: int = 0) -> dict:
+    """Time dequantize + reference matmul on this host's cores (median of reps).
+
+    ``max_rows`` > 0 bounds the sample: the matmul runs on the first
+    ``min(M, max_rows)`` rows of X and its time is scaled by M / rows (the
+    fp32 product's work is linear in M; the dequantize runs whole).  The
+    result says how many rows were timed."""
     L = lib()
     if threads > 0:
         L.nibble_oracle_set_threads(threads)
-    X, packed, scales = synthetic_case(M, K, N, group_size, seed)
+    rows = M if max_rows <= 0 else min(M, max_rows)
+    X, packed, scales = synthetic_case(rows, K, N, group_size, seed)
     p = np.ascontiguousarray(packed).view(np.uint32)
     s = _as_u16(scales)
     x = _as_u16(X)
     W = np.empty((K, N), dtype=np.uint16)
-    Y = np.empty((M, N), dtype=np.uint16)
+    Y = np.empty((rows, N), dtype=np.uint16)
     dq, mm = [], []
     for _ in range(reps + 1):
         t0 = time.perf_counter()
         L.nibble_oracle_dequantize(_ptr(p), _ptr(s), K, N, group_size, _ptr(W))
         t1 = time.perf_counter()
-        L.nibble_oracle_matmul_f32(_ptr(x), _ptr(W), M, K, N, _ptr(Y), None)
+        L.nibble_oracle_matmul_f32(_ptr(x), _ptr(W), rows, K, N, _ptr(Y), None)
         t2 = time.perf_counter()
         dq.append(t1 - t0)
-        mm.append(t2 - t1)
+        mm.append((t2 - t1) * M / rows)
     dq, mm = sorted(dq[1:]), sorted(mm[1:])
     tot = sorted(a + b for a, b in zip(dq, mm))
     return {
@@ -299,4 +260,5 @@ def time_reference_path(M: int, K: int, N: int, group_size: int = 128, reps: int
         "total_s": tot[len(tot) // 2],
         "threads": L.nibble_oracle_max_threads(),
         "reps": reps,
+        "rows_timed": rows,
     }

@@ -280,6 +280,24 @@ def test_library_loads_only_one_hip_runtime():
     assert len(paths) <= 1, paths
 
 
+REFERENCE_NAMES = ("DECODE_MAX_M", "QuantLinear", "QuantizedWeight", "dequant", "dequantize",
+                   "HessianAccumulator", "extension", "find_decoder_blocks", "gptq_quantize",
+                   "quantize_model_gptq", "gemm", "gemv", "matmul", "pack_nibbles", "quantize",
+                   "reference_matmul", "unpack_nibbles")
+
+
+def test_package_keeps_the_reference_namespace():
+    """Every name the reference package exports (python/nibblegemm/__init__.py:
+    19-37) is exported here; the offline GPTQ quantiser's four names are
+    stubs that refuse with NotImplementedError instead of computing."""
+    assert set(REFERENCE_NAMES) <= set(ng.__all__)
+    assert all(hasattr(ng, n) for n in ng.__all__)
+    for name in ("gptq_quantize", "quantize_model_gptq", "find_decoder_blocks",
+                 "HessianAccumulator"):
+        with pytest.raises(NotImplementedError, match="GPTQ"):
+            getattr(ng, name)(None)
+
+
 def test_extension_exposes_the_reference_module_functions():
     """``extension()`` offers the reference module's tensor-level functions
     (csrc/bindings.cpp:11-22) with the same argument names and defaults."""

@@ -66,6 +66,21 @@ def test_high_codes_at_k7_make_negative_words():
     assert words[15] == -(1 << 31) + (7 << 28)
 
 
+def test_negative_signed_codes_wrap_into_their_own_nibble():
+    """A signed input passes the > 15 check with negative codes; each one is
+    masked to its low four bits before the shift (the reference's ``& 0xF``,
+    python/nibblegemm/quant.py:177), so -c packs as 16 - c in its own slot and
+    leaves every other nibble of the word untouched."""
+    for k in range(8):
+        qu = np.zeros((8, 8), np.int8)
+        qu[k, :] = -np.arange(1, 9, dtype=np.int8)
+        words = ng.pack_nibbles(qu).view(np.uint32)[0]
+        assert words.tolist() == [(16 - c) << (4 * SLOT_TABLE[k]) for c in range(1, 9)]
+    rng = np.random.default_rng(5)
+    codes = rng.integers(-8, 8, size=(64, 9)).astype(np.int8)
+    assert np.array_equal(ng.pack_nibbles(codes), ng.pack_nibbles((codes & 0xF).astype(np.uint8)))
+
+
 def _bad_pack_value():
     qu = np.zeros((16, 3), np.uint8)
     qu[9, 1] = 200

@@ -209,6 +209,28 @@ def test_swiglu_epilogue_is_the_fp16_composition(M, K, Nh, sw):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("M,K,Nh", [(1, 4096, 1024), (3, 4096, 512)])
+def test_swiglu_on_default_16_column_strips_composes(M, K, Nh):
+    """A gate|up weight whose recommended strip width is 16 columns (N <= 2048)
+    cannot take the SwiGLU epilogue (a strip holds half a gate|up block pair);
+    matmul_swiglu and rmsnorm_matmul(swiglu=True) compose the same fp16
+    arithmetic from the plain strip-major product instead of refusing."""
+    _, _, _, Xd, gate = synthetic(M, K, Nh, 128, seed=3)
+    _, _, _, _, up = synthetic(M, K, Nh, 128, seed=4)
+    sm = ng.to_strip_major(ng.interleave_swiglu(gate, up))
+    assert sm.strip_cols == 16
+    gate_y, up_y = quant.split_swiglu(ng.matmul(Xd, sm))
+    want = torch.nn.functional.silu(gate_y) * up_y
+    assert torch.equal(ng.matmul_swiglu(Xd, sm), want)
+    w = (torch.rand(K, generator=torch.Generator().manual_seed(9)) + 0.5).half().cuda()
+    from nibblegemm_amd.glue import rmsnorm  # noqa: PLC0415
+
+    g2, u2 = quant.split_swiglu(ng.matmul(rmsnorm(Xd, w, 1e-5), sm))
+    assert torch.equal(ng.rmsnorm_matmul(Xd, w, sm, 1e-5, swiglu=True),
+                       torch.nn.functional.silu(g2) * u2)
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("M,K,N,sw", [(1, 4096, 6144, 32), (4, 4096, 1024, 16), (8, 2048, 28672, 64),
                                       (1, 14336, 4096, 16), (8, 4096, 6144, 32), (3, 8192, 512, 64)])
 def test_rmsnorm_prologue_is_the_two_step_composition(M, K, N, sw):

@@ -93,6 +93,45 @@ def test_graph_replays_match_eager():
         assert torch.equal(out, eager)
 
 
+def test_first_split_call_under_capture_is_refused_in_a_fresh_process():
+    """The scratch of a GPU is set up by its first split-K call (counters
+    cleared, then the address published); that call cannot be recorded into a
+    graph, so in a process that has made none, a capture of one is refused
+    with a clear error, and an eager call afterwards sets up and computes
+    the workspace entry point's bits.  Runs in a child process: this one has
+    set its scratch up already."""
+    import os  # noqa: PLC0415
+    import subprocess  # noqa: PLC0415
+    import sys  # noqa: PLC0415
+
+    code = r"""
+import sys, torch
+sys.path[:0] = [sys.argv[1], sys.argv[2]]
+import test_zz_no_alloc as T
+import nibblegemm_amd as ng
+X, qw = T.case(2, 14336, 4096, seed=5)
+side = torch.cuda.Stream()
+side.wait_stream(torch.cuda.current_stream())
+g = torch.cuda.CUDAGraph()
+refused = False
+try:
+    with torch.cuda.graph(g, stream=side):
+        T.noalloc(X, qw)
+except RuntimeError as e:
+    refused = "graph capture" in str(e)
+torch.cuda.synchronize()
+got = T.noalloc(X, qw)
+ok = torch.equal(got, ng.gemv(X, qw))
+print("RESULT", refused, ok, flush=True)
+"""
+    tests_dir = os.path.dirname(os.path.abspath(__file__))
+    root = os.path.dirname(tests_dir)
+    r = subprocess.run([sys.executable, "-c", code, tests_dir, root], capture_output=True,
+                       text=True, timeout=110)
+    assert r.returncode == 0, r.stderr[-2000:]
+    assert "RESULT True True" in r.stdout, (r.stdout[-500:], r.stderr[-2000:])
+
+
 def test_rejects_plans_beyond_the_scratch():
     X, qw = case(8, 4096, 8192, seed=7)
     with pytest.raises(RuntimeError, match="static scratch"):
