@@ -50,7 +50,7 @@
 extern "C" {
 #endif
 
-#define NIBBLE_ABI_VERSION 9
+#define NIBBLE_ABI_VERSION 10
 
 #if defined(__GNUC__) || defined(__clang__)
 #define NIBBLE_API __attribute__((visibility("default")))
@@ -289,6 +289,55 @@ NIBBLE_API size_t nibble_attention_decode_workspace_bytes(int64_t n_heads, int64
 NIBBLE_API size_t nibble_attention_decode_counter_bytes(int64_t n_heads, int64_t n_kv_heads,
                                                         int64_t head_dim, int64_t max_seq,
                                                         int64_t pos, void* stream);
+
+/*
+ * Persistent decode chain: a list of strip-major decode GEMVs ("stages") run
+ * by ONE launch, each stage optionally waiting for an earlier one.  No
+ * counterpart in the reference, whose decode step is one launch per
+ * projection (bench/bench_model.py:70-86) and whose optimisation log names
+ * fewer launches as the fix for the launch-bound small projections
+ * (docs/OPTIMIZATION_LOG.md:159-163).  Every output has the bits of
+ * nibble_gemv_w4a16_strip_major with the same operands and epilogue.
+ *
+ * A stage is Y = X @ W (epilogue 0), fp16(fp16(X @ W) + bias) (1) or the
+ * SwiGLU of an interleave_swiglu weight (2, strips of >= 32 columns), with
+ * X [M, K] fp16, W strip-major (nibble_pack_strip_major at `strip_cols`),
+ * Y [M, N] fp16 ([M, N / 2] for SwiGLU).  `after` names an earlier stage
+ * (index) that must have finished before this one reads its X and bias, or
+ * is -1.  Whatever a stage reads that another stage writes, and whatever two
+ * stages both write, must be ordered by `after` links (directly or through a
+ * chain of them); nibble_chain_create checks this, and that no stage writes
+ * weights.  All stages share M (1..8) and group_size.
+ */
+typedef struct nibble_chain_stage {
+  const void* X;
+  const void* Wt;
+  const void* St;
+  void* Y;
+  const void* bias;
+  int64_t K, N, group_size, strip_cols, epilogue;
+  int64_t after;
+} nibble_chain_stage;
+
+/* Validates the stages, plans the launch (one workgroup per CU; every
+ * workgroup gets an ordered list of strips, balanced by bytes) and copies
+ * the plan to the device of `stream` (allocates; not for graph capture).
+ * The pointers are recorded: the buffers must outlive the chain. */
+NIBBLE_API int nibble_chain_create(const nibble_chain_stage* stages, int64_t n_stages, int64_t M,
+                                   void* stream, void** chain);
+/* One run of every stage on `stream` (allocates nothing; graph-capturable).
+ * Runs of one chain must not overlap (they share its counters).
+ * `timestamps`: NULL, or n_stages + 1 uint64 the caller has set to 0 (and
+ * the last to UINT64_MAX): per stage the s_memrealtime (100 MHz) tick at
+ * which its last round ended, and the tick the first workgroup started. */
+NIBBLE_API int nibble_chain_run(void* chain, void* timestamps, void* stream);
+/* Synchronises `stream`, then reports whether a run gave up waiting for a
+ * stage (bounded waits; e.g. when not every workgroup could be resident):
+ * NIBBLE_ERR_HIP with a message if so (the flag is then cleared). */
+NIBBLE_API int nibble_chain_check(void* chain, void* stream);
+/* 0: workgroups, 1: rounds, 2: dynamic LDS bytes, 3: stages; -1 otherwise. */
+NIBBLE_API int64_t nibble_chain_info(void* chain, int64_t what);
+NIBBLE_API int nibble_chain_destroy(void* chain);
 
 /*
  * Measurement: a streaming read of `bytes` (a positive multiple of 16) from

@@ -29,7 +29,7 @@ OBJ = os.path.join(PKG, "_build")
 LIBDIR = os.path.join(PKG, "lib")
 LIB = os.path.join(LIBDIR, "libnibblegemm_amd.so")
 
-HIP_SOURCES = ["abi.hip", "dequant.hip", "gemv.hip", "gemm.hip", "glue.hip", "probe.hip"]
+HIP_SOURCES = ["abi.hip", "dequant.hip", "gemv.hip", "gemm.hip", "glue.hip", "chain.hip", "probe.hip"]
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [

@@ -247,6 +247,76 @@ static PyObject* py_dequant(PyObject* self, PyObject* const* a, Py_ssize_t n) {
   return PyLong_FromLong(rc);
 }
 
+/* chain_create(stages: bytes of n packed nibble_chain_stage, n, M, stream) -> (status, handle) */
+static PyObject* py_chain_create(PyObject* self, PyObject* const* a, Py_ssize_t n) {
+  (void)self;
+  if (!nargs_is(n, 4, "chain_create")) return NULL;
+  long long count, M;
+  void* stream;
+  if (!PyBytes_Check(a[0])) {
+    PyErr_SetString(PyExc_TypeError, "chain_create: stages must be bytes");
+    return NULL;
+  }
+  if (!take_i64(a[1], &count) || !take_i64(a[2], &M) || !take_ptr(a[3], &stream)) return NULL;
+  if (count < 0 || (size_t)PyBytes_GET_SIZE(a[0]) != (size_t)count * sizeof(nibble_chain_stage)) {
+    PyErr_Format(PyExc_ValueError, "chain_create: %lld stages need %zu bytes, got %zd", count,
+                 (size_t)count * sizeof(nibble_chain_stage), PyBytes_GET_SIZE(a[0]));
+    return NULL;
+  }
+  void* chain = NULL;
+  int rc = nibble_chain_create((const nibble_chain_stage*)PyBytes_AS_STRING(a[0]), count, M,
+                               stream, &chain);
+  PyObject* handle = NULL;
+  if (rc == 0) {
+    handle = PyLong_FromVoidPtr(chain);
+    if (handle == NULL) {
+      nibble_chain_destroy(chain);
+      return NULL;
+    }
+  } else {
+    Py_INCREF(Py_None);
+    handle = Py_None;
+  }
+  return Py_BuildValue("(iN)", rc, handle);
+}
+
+/* chain_run(handle, timestamps, stream) */
+static PyObject* py_chain_run(PyObject* self, PyObject* const* a, Py_ssize_t n) {
+  (void)self;
+  if (!nargs_is(n, 3, "chain_run")) return NULL;
+  void *chain, *stamps, *stream;
+  if (!take_ptr(a[0], &chain) || !take_ptr(a[1], &stamps) || !take_ptr(a[2], &stream)) return NULL;
+  return PyLong_FromLong(nibble_chain_run(chain, stamps, stream));
+}
+
+/* chain_check(handle, stream) */
+static PyObject* py_chain_check(PyObject* self, PyObject* const* a, Py_ssize_t n) {
+  (void)self;
+  if (!nargs_is(n, 2, "chain_check")) return NULL;
+  void *chain, *stream;
+  if (!take_ptr(a[0], &chain) || !take_ptr(a[1], &stream)) return NULL;
+  return PyLong_FromLong(nibble_chain_check(chain, stream));
+}
+
+/* chain_info(handle, what) */
+static PyObject* py_chain_info(PyObject* self, PyObject* const* a, Py_ssize_t n) {
+  (void)self;
+  if (!nargs_is(n, 2, "chain_info")) return NULL;
+  void* chain;
+  long long what;
+  if (!take_ptr(a[0], &chain) || !take_i64(a[1], &what)) return NULL;
+  return PyLong_FromLongLong(nibble_chain_info(chain, what));
+}
+
+/* chain_destroy(handle) */
+static PyObject* py_chain_destroy(PyObject* self, PyObject* const* a, Py_ssize_t n) {
+  (void)self;
+  if (!nargs_is(n, 1, "chain_destroy")) return NULL;
+  void* chain;
+  if (!take_ptr(a[0], &chain)) return NULL;
+  return PyLong_FromLong(nibble_chain_destroy(chain));
+}
+
 static PyObject* py_last_error(PyObject* self, PyObject* unused) {
   (void)self;
   (void)unused;
@@ -284,6 +354,14 @@ static PyMethodDef kMethods[] = {
      "nibble_attention_decode_f16"},
     {"attention_workspace_bytes", (PyCFunction)(void (*)(void))py_attention_ws, METH_FASTCALL,
      "(nibble_attention_decode_workspace_bytes, nibble_attention_decode_counter_bytes)"},
+    {"chain_create", (PyCFunction)(void (*)(void))py_chain_create, METH_FASTCALL,
+     "nibble_chain_create"},
+    {"chain_run", (PyCFunction)(void (*)(void))py_chain_run, METH_FASTCALL, "nibble_chain_run"},
+    {"chain_check", (PyCFunction)(void (*)(void))py_chain_check, METH_FASTCALL,
+     "nibble_chain_check"},
+    {"chain_info", (PyCFunction)(void (*)(void))py_chain_info, METH_FASTCALL, "nibble_chain_info"},
+    {"chain_destroy", (PyCFunction)(void (*)(void))py_chain_destroy, METH_FASTCALL,
+     "nibble_chain_destroy"},
     {"last_error", py_last_error, METH_NOARGS, "nibble_last_error"},
     {"abi_version", py_abi_version, METH_NOARGS, "nibble_abi_version"},
     {NULL, NULL, 0, NULL}};

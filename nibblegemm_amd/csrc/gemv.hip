@@ -39,6 +39,7 @@
 
 #include "nibble_common.h"
 #include "nibble_decode.h"
+#include "nibble_epilogue.h"
 #include "nibble_reduce.h"
 #include "stream_matmul.h"
 
@@ -73,24 +74,6 @@ struct GemvArgs {
   // w_strip = 4 SW K / 8, s_row = 2 SW, s_strip = 2 SW K / G.
   uint32_t w_row, w_strip, s_row, s_strip;
 };
-
-// Output epilogues of the streaming kernel (fused forms of what a caller
-// would otherwise run as separate elementwise kernels on the fp16 result).
-constexpr int kEpilogueNone = 0;
-constexpr int kEpilogueBias = 1;    // Y = fp16(fp16(X W) + bias)
-constexpr int kEpilogueSwiglu = 2;  // W = [gate | up] in 16-column blocks; Y = silu(G) * U
-constexpr int kSwigluBlock = 16;    // columns of one gate or up block of that layout
-
-// The fp16 arithmetic of the unfused composition, step by step: the two
-// products rounded to fp16, silu(g) = g / (1 + e^-g) evaluated in fp32 and
-// rounded, then the fp32 product of the two fp16 values (rounded at the
-// store).
-__device__ __forceinline__ float silu_mul(float g, float u) {
-  const float g16 = static_cast<float>(static_cast<_Float16>(g));
-  const float u16 = static_cast<float>(static_cast<_Float16>(u));
-  const float s16 = static_cast<float>(static_cast<_Float16>(g16 / (1.0f + expf(-g16))));
-  return s16 * u16;
-}
 
 __device__ __forceinline__ f4_t mfma16(h8_t a, h8_t b, f4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);

@@ -40,6 +40,18 @@ launch), so a layer is 5 launches.  This is the per-token forward of
 the reference's model decode (bench/bench_model.py:177-188) without the
 embedding lookup and the fp16 lm_head, which are not W4A16.
 
+``persistent`` runs the fused strip-major step as ONE launch: a
+:class:`~nibblegemm_amd.chain.DecodeChain` of the 128 projections, each still
+reading its fixed activation (the reference's semantics), whose workgroups
+stream weights across projection boundaries; the outputs are bit-identical to
+``fused_strips``.  ``dataflow`` is the real data flow of a decoder layer
+without attention and norms, one launch per projection on strip-major
+weights: the q|k|v product, o on its q part with the layer input added as
+the residual, gate|up through the SwiGLU epilogue, and down with o's output
+added, whose result is the next layer's input.  ``persistent_dataflow`` runs
+that same dependent sequence as one chain (every stage waits for the one
+before it) with the same bits.
+
 ``--tp N`` builds every layer at one GPU's share of an N-way tensor-parallel
 split instead (:func:`projection_shapes`): q, k, v, gate and up split by
 columns (N / tp each), o and down by rows (K / tp, whole quant groups).  It
@@ -62,6 +74,7 @@ from typing import Dict, List, Tuple
 import torch
 
 from . import harness as H
+from .chain import DecodeChain, stage
 from .glue import attention_bytes, attention_decode, rmsnorm, rope_tables
 from .ops import (matmul, matmul_bias, matmul_swiglu, rmsnorm_matmul, strip_major_cols,
                   to_strip_major)
@@ -167,6 +180,100 @@ class DecodeStep:
         return len(self.calls)
 
 
+def chain_stages(layers: List[Dict[str, QuantizedWeight]], acts: Dict[int, torch.Tensor]) -> list:
+    """The projections of ``layers`` (strip-major weights) as independent
+    chain stages, each reading its fixed activation ``acts[K]`` (the
+    reference's decode-step semantics) and writing its own output."""
+    out = []
+    for layer in layers:
+        for name, w in layer.items():
+            out.append(stage(acts[w.K], w, swiglu=name == "gate_up_swiglu"))
+    return out
+
+
+class ChainStep:
+    """A decode step run as one :class:`DecodeChain` launch."""
+
+    def __init__(self, chain: DecodeChain, nbytes: int):
+        self.chain = chain
+        self.nbytes = nbytes
+
+    def __call__(self, _i: int = 0) -> None:
+        self.chain.run()
+
+    def outputs(self) -> List[torch.Tensor]:
+        self.chain.run()
+        return [y.clone() for y in self.chain.outputs()]
+
+    @property
+    def launches(self) -> int:
+        return 1
+
+
+class DataflowStep:
+    """The data flow of a decoder layer without attention and norms, one
+    launch per projection: ``qkv = x W_qkv``; ``h = q W_o + x`` (q the first
+    ``hidden`` columns of qkv; the residual add as the fused bias);
+    ``g = silu(h W_gate) * (h W_up)``; ``x' = g W_down + h``.  ``layers`` are
+    ``fuse(layer, swiglu=True)`` sets (strip-major or packed).  A call makes
+    the launches alone (outputs from the caching allocator, as any
+    ``matmul``); :meth:`as_chain` builds the same step as one chain writing
+    into buffers allocated once here."""
+
+    def __init__(self, layers: List[Dict[str, QuantizedWeight]], cfg=LLAMA3_8B, device="cuda",
+                 seed: int = 3):
+        gen = torch.Generator(device=device).manual_seed(seed)
+        h, inter = cfg["hidden"], cfg["intermediate"]
+        self.layers = layers
+        self.hidden = h
+        self.x0 = torch.randn((1, h), generator=gen, device=device).to(torch.float16)
+        self.bufs = []
+        for layer in layers:
+            nqkv = layer["qkv"].N
+            self.bufs.append({"qkv": torch.empty((1, nqkv), dtype=torch.float16, device=device),
+                              "h": torch.empty((1, h), dtype=torch.float16, device=device),
+                              "g": torch.empty((1, inter), dtype=torch.float16, device=device),
+                              "x": torch.empty((1, h), dtype=torch.float16, device=device)})
+
+    def __call__(self, _i: int = 0) -> None:
+        self.step_outputs()
+
+    def step_outputs(self) -> List[torch.Tensor]:
+        """One step's four activations of every layer, in order."""
+        out, x = [], self.x0
+        for layer in self.layers:
+            qkv = matmul(x, layer["qkv"])
+            hh = matmul_bias(qkv[:, :self.hidden], layer["o"], x.view(-1))
+            g = matmul_swiglu(hh, layer["gate_up_swiglu"])
+            x = matmul_bias(g, layer["down"], hh.view(-1))
+            out += [qkv, hh, g, x]
+        return out
+
+    outputs = step_outputs
+
+    def as_chain(self) -> DecodeChain:
+        """The same step as one chain writing the same buffers: every stage
+        waits for the one before it."""
+        stages, x, prev = [], self.x0, -1
+        for layer, b in zip(self.layers, self.bufs):
+            stages.append(stage(x, layer["qkv"], after=prev, Y=b["qkv"]))
+            stages.append(stage(b["qkv"][:, :self.hidden], layer["o"], bias=x.view(-1),
+                                after=len(stages) - 1, Y=b["h"]))
+            stages.append(stage(b["h"], layer["gate_up_swiglu"], swiglu=True,
+                                after=len(stages) - 1, Y=b["g"]))
+            stages.append(stage(b["g"], layer["down"], bias=b["h"].view(-1),
+                                after=len(stages) - 1, Y=b["x"]))
+            x, prev = b["x"], len(stages) - 1
+        return DecodeChain(stages)
+
+    def buffers(self) -> List[torch.Tensor]:
+        return [b[k] for b in self.bufs for k in ("qkv", "h", "g", "x")]
+
+    @property
+    def launches(self) -> int:
+        return 4 * len(self.layers)
+
+
 class GlueDecodeStep:
     """One batch-1 token step of a Llama-shaped decoder at position ``pos``.
 
@@ -231,48 +338,115 @@ class GlueDecodeStep:
         return weight_bytes(self.layers) + len(self.layers) * per_layer
 
 
-def measure_glue(layers: List[Dict[str, QuantizedWeight]], pos: int = 1023, trials: int = 10,
-                 warmup: int = 3) -> dict:
-    step = GlueDecodeStep(layers, pos=pos)
-    eager = H.bench(step, reps=1, trials=trials, warmup=warmup)
-    graph = H.bench_graph(step, reps=1, trials=trials, warmup=warmup)
-    nbytes = step.step_bytes()
-    return {
-        "launches": step.launches,
-        "context": pos + 1,
-        "step_gib": round(nbytes / 2**30, 3),
-        "eager_ms": round(eager.median_ms, 4),
-        "graph_ms": round(graph.median_ms, 4),
-        "tok_s": round(1000.0 / eager.median_ms, 1),
-        "graph_tok_s": round(1000.0 / graph.median_ms, 1),
-        "graph_gbps": round(nbytes / (graph.median_ms * 1e-3) / 1e9, 1),
-        "clock_mhz": graph.clocks.get("clock_mean_mhz"),
-        "throttled": graph.clocks.get("throttled"),
-    }
+def outputs_of(step) -> List[torch.Tensor]:
+    """The tensors one call of ``step`` produces, in order."""
+    if hasattr(step, "outputs"):
+        return step.outputs()
+    return [step()]
 
 
-def measure(layers: List[Dict[str, QuantizedWeight]], trials: int = 10, warmup: int = 3) -> dict:
+def graph_matches_eager(step) -> bool:
+    """Captures one call of ``step`` into a HIP graph, replays it, and
+    compares every output with an eager call's, bit for bit."""
+    eager = [t.clone() for t in outputs_of(step)]
+    torch.cuda.synchronize()
+    kept: List[torch.Tensor] = []
+
+    def body(_i):
+        kept[:] = outputs_of(step)
+
+    runner = H.GraphRunner(body, reps=1, warmup=1)
+    runner.graph.replay()
+    torch.cuda.synchronize()
+    same = _same(kept, eager)
+    del runner, kept
+    return same
+
+
+def measure_step(step, nbytes: int, trials: int = 10, warmup: int = 3, **extra) -> dict:
     """Eager and graph-replayed time of one step, as the reference reports it
-    (bench_model.py:100-113)."""
-    step = DecodeStep(layers)
+    (bench_model.py:100-113), after checking that a graph replay gives the
+    eager call's outputs bit for bit (raises otherwise)."""
+    if not graph_matches_eager(step):
+        raise RuntimeError(f"{type(step).__name__}: graph replay differs from the eager step")
     eager = H.bench(step, reps=1, trials=trials, warmup=warmup)
     graph = H.bench_graph(step, reps=1, trials=trials, warmup=warmup)
-    nbytes = weight_bytes(layers)
     return {
         "launches": step.launches,
+        **extra,
         "weights_gib": round(nbytes / 2**30, 3),
         "eager_ms": round(eager.median_ms, 4),
         "graph_ms": round(graph.median_ms, 4),
         "tok_s": round(1000.0 / eager.median_ms, 1),
         "graph_tok_s": round(1000.0 / graph.median_ms, 1),
         "graph_gbps": round(nbytes / (graph.median_ms * 1e-3) / 1e9, 1),
+        "graph_equals_eager": True,
         "clock_mhz": graph.clocks.get("clock_mean_mhz"),
         "throttled": graph.clocks.get("throttled"),
     }
 
 
+def measure_glue(layers: List[Dict[str, QuantizedWeight]], pos: int = 1023, trials: int = 10,
+                 warmup: int = 3) -> dict:
+    step = GlueDecodeStep(layers, pos=pos)
+    r = measure_step(step, step.step_bytes(), trials, warmup, context=pos + 1)
+    r["step_gib"] = r.pop("weights_gib")
+    return r
+
+
+def measure(layers: List[Dict[str, QuantizedWeight]], trials: int = 10, warmup: int = 3) -> dict:
+    return measure_step(DecodeStep(layers), weight_bytes(layers), trials, warmup)
+
+
+def _same(a: List[torch.Tensor], b: List[torch.Tensor]) -> bool:
+    """Bit-for-bit equality of two lists of fp16 tensors (NaNs included)."""
+    return len(a) == len(b) and all(
+        x.shape == y.shape and torch.equal(x.view(torch.int16), y.view(torch.int16))
+        for x, y in zip(a, b))
+
+
+def measure_persistent(layers_sm: List[Dict[str, QuantizedWeight]], trials: int = 10,
+                       warmup: int = 3) -> dict:
+    """The step of ``layers_sm`` (strip-major) as one chain launch with the
+    reference's semantics, after checking its outputs against the
+    per-projection launches bit for bit (raises otherwise)."""
+    launches = DecodeStep(layers_sm)
+    chain = DecodeChain(chain_stages(layers_sm, launches.acts))
+    step = ChainStep(chain, weight_bytes(layers_sm))
+    if not _same(step.outputs(), launches.outputs()):
+        raise RuntimeError("persistent chain differs from the per-projection launches")
+    chain.check()
+    r = measure_step(step, step.nbytes, trials, warmup, stages=len(chain.stages),
+                     workgroups=chain.workgroups, rounds=chain.rounds,
+                     equals_per_projection_launches=True)
+    chain.check()
+    return r
+
+
+def measure_dataflow(layers_sm: List[Dict[str, QuantizedWeight]], trials: int = 10,
+                     warmup: int = 3, persistent: bool = True) -> Dict[str, dict]:
+    """The layer data flow (:class:`DataflowStep`) one launch per projection,
+    and (``persistent``) as one chain, after checking the chain's outputs
+    against the launches' bit for bit (raises otherwise)."""
+    df = DataflowStep(layers_sm)
+    nbytes = weight_bytes(layers_sm)
+    out = {"dataflow_strips": measure_step(df, nbytes, trials, warmup)}
+    if persistent:
+        chain = df.as_chain()
+        step = ChainStep(chain, nbytes)
+        if not _same(step.outputs(), df.step_outputs()):
+            raise RuntimeError("persistent data-flow chain differs from the per-projection launches")
+        chain.check()
+        out["persistent_dataflow"] = measure_step(
+            step, nbytes, trials, warmup, stages=len(chain.stages), workgroups=chain.workgroups,
+            rounds=chain.rounds, equals_per_projection_launches=True)
+        chain.check()
+    return out
+
+
 VARIANTS = ("projections", "fused", "fused_swiglu", "glue", "projections_strips", "fused_strips",
-            "fused_swiglu_strips", "glue_strips")
+            "fused_swiglu_strips", "glue_strips", "persistent", "dataflow_strips",
+            "persistent_dataflow")
 
 
 def run(n_layers: int = 32, group_size: int = 128, trials: int = 10, glue_pos: int = 1023,
@@ -291,27 +465,37 @@ def run(n_layers: int = 32, group_size: int = 128, trials: int = 10, glue_pos: i
         res["projections"] = measure(layers, trials)
     if "projections_strips" in want:
         res["projections_strips"] = measure(strips(layers), trials)
-    if want & {"fused", "fused_strips"}:
+    if want & {"fused", "fused_strips", "persistent"}:
         fused = [fuse(layer) for layer in layers]
         if "fused" in want:
             res["fused"] = measure(fused, trials)
-        if "fused_strips" in want:
-            res["fused_strips"] = measure(strips(fused), trials)
+        if want & {"fused_strips", "persistent"}:
+            fs = strips(fused)
+            if "fused_strips" in want:
+                res["fused_strips"] = measure(fs, trials)
+            if "persistent" in want:
+                res["persistent"] = measure_persistent(fs, trials)
+            del fs
         del fused
-    if want & {"fused_swiglu", "glue", "fused_swiglu_strips", "glue_strips"}:
+    swiglu_want = {"fused_swiglu", "glue", "fused_swiglu_strips", "glue_strips",
+                   "dataflow_strips", "persistent_dataflow"}
+    if want & swiglu_want:
         swiglu = [fuse(layer, swiglu=True) for layer in layers]
         del layers
         if "fused_swiglu" in want:
             res["fused_swiglu"] = measure(swiglu, trials)
         if "glue" in want and glue_pos >= 0:
             res["glue"] = measure_glue(swiglu, glue_pos, trials)
-        if want & {"fused_swiglu_strips", "glue_strips"}:
+        if want & (swiglu_want - {"fused_swiglu", "glue"}):
             swiglu_strips = strips(swiglu)
             del swiglu
             if "fused_swiglu_strips" in want:
                 res["fused_swiglu_strips"] = measure(swiglu_strips, trials)
             if "glue_strips" in want and glue_pos >= 0:
                 res["glue_strips"] = measure_glue(swiglu_strips, glue_pos, trials)
+            if want & {"dataflow_strips", "persistent_dataflow"}:
+                res.update(measure_dataflow(swiglu_strips, trials,
+                                            persistent="persistent_dataflow" in want))
     return res
 
 

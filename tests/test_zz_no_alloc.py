@@ -106,7 +106,7 @@ def test_first_split_call_under_capture_is_refused_in_a_fresh_process():
 
     code = r"""
 import sys, torch
-sys.path[:0] = [sys.argv[1], sys.argv[2]]
+sys.path[:0] = sys.argv[1:4]  # tests/, oracle/ (before the root: its module, not the folder), root
 import test_zz_no_alloc as T
 import nibblegemm_amd as ng
 X, qw = T.case(2, 14336, 4096, seed=5)
@@ -126,8 +126,8 @@ print("RESULT", refused, ok, flush=True)
 """
     tests_dir = os.path.dirname(os.path.abspath(__file__))
     root = os.path.dirname(tests_dir)
-    r = subprocess.run([sys.executable, "-c", code, tests_dir, root], capture_output=True,
-                       text=True, timeout=110)
+    r = subprocess.run([sys.executable, "-c", code, tests_dir, os.path.join(root, "oracle"), root],
+                       capture_output=True, text=True, timeout=110)
     assert r.returncode == 0, r.stderr[-2000:]
     assert "RESULT True True" in r.stdout, (r.stdout[-500:], r.stderr[-2000:])
 
