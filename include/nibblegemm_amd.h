@@ -50,7 +50,7 @@
 extern "C" {
 #endif
 
-#define NIBBLE_ABI_VERSION 10
+#define NIBBLE_ABI_VERSION 11
 
 #if defined(__GNUC__) || defined(__clang__)
 #define NIBBLE_API __attribute__((visibility("default")))
@@ -289,6 +289,26 @@ NIBBLE_API size_t nibble_attention_decode_workspace_bytes(int64_t n_heads, int64
 NIBBLE_API size_t nibble_attention_decode_counter_bytes(int64_t n_heads, int64_t n_kv_heads,
                                                         int64_t head_dim, int64_t max_seq,
                                                         int64_t pos, void* stream);
+
+/*
+ * Strip-major weights for every batch size (no counterpart in the
+ * reference): nibble_gemm_w4a16 and nibble_dequant_w4 on the strip-major
+ * copy (Wt, St) of a weight, so that a model can keep that one copy.
+ * nibble_gemm_w4a16_strip_major takes batches of more than 8 rows (at most 8
+ * take nibble_gemv_w4a16_strip_major) and runs the packed call's plans and
+ * kernels, so it returns the packed call's bits and needs the same
+ * workspace (nibble_gemm_workspace_bytes / nibble_gemm_counter_bytes).
+ * nibble_dequant_w4_strip_major writes the packed call's [K, N] output.
+ * Wt and St 16-byte aligned; strip_cols 16, 32 or 64 dividing N.
+ */
+NIBBLE_API int nibble_gemm_w4a16_strip_major(const void* X, int64_t x_rows, int64_t x_cols,
+                                             const void* Wt, const void* St, int64_t K, int64_t N,
+                                             int64_t group_size, int64_t strip_cols,
+                                             int64_t version, void* Y, void* workspace,
+                                             size_t workspace_bytes, void* stream);
+NIBBLE_API int nibble_dequant_w4_strip_major(const void* Wt, const void* St, int64_t K, int64_t N,
+                                             int64_t group_size, int64_t strip_cols, int fast,
+                                             void* W, void* stream);
 
 /*
  * Persistent decode chain: a list of strip-major decode GEMVs ("stages") run

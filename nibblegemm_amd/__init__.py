@@ -21,6 +21,7 @@ from .quant import (
     StripMajorWeight,
     concat_columns,
     dequantize,
+    from_strip_major,
     interleave_swiglu,
     pack_nibbles,
     quantize,
@@ -41,6 +42,7 @@ __all__ = [
     "dequantize",
     "extension",
     "find_decoder_blocks",
+    "from_strip_major",
     "gemm",
     "gemv",
     "interleave_swiglu",

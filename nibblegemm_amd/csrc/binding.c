@@ -247,6 +247,35 @@ static PyObject* py_dequant(PyObject* self, PyObject* const* a, Py_ssize_t n) {
   return PyLong_FromLong(rc);
 }
 
+/* gemm_strip_major(X, xr, xc, Wt, St, K, N, g, sw, version, Y, ws, ws_bytes, stream) */
+static PyObject* py_sm_gemm(PyObject* self, PyObject* const* a, Py_ssize_t n) {
+  (void)self;
+  if (!nargs_is(n, 14, "gemm_strip_major")) return NULL;
+  void *X, *Wt, *St, *Y, *ws, *stream;
+  long long xr, xc, K, N, g, sw, ver, wsb;
+  if (!take_ptr(a[0], &X) || !take_i64(a[1], &xr) || !take_i64(a[2], &xc) ||
+      !take_ptr(a[3], &Wt) || !take_ptr(a[4], &St) || !take_i64(a[5], &K) ||
+      !take_i64(a[6], &N) || !take_i64(a[7], &g) || !take_i64(a[8], &sw) ||
+      !take_i64(a[9], &ver) || !take_ptr(a[10], &Y) || !take_ptr(a[11], &ws) ||
+      !take_i64(a[12], &wsb) || !take_ptr(a[13], &stream))
+    return NULL;
+  return PyLong_FromLong(nibble_gemm_w4a16_strip_major(X, xr, xc, Wt, St, K, N, g, sw, ver, Y, ws,
+                                                       (size_t)(wsb < 0 ? 0 : wsb), stream));
+}
+
+/* dequant_strip_major(Wt, St, K, N, g, sw, fast, W, stream) */
+static PyObject* py_sm_dequant(PyObject* self, PyObject* const* a, Py_ssize_t n) {
+  (void)self;
+  if (!nargs_is(n, 9, "dequant_strip_major")) return NULL;
+  void *Wt, *St, *W, *stream;
+  long long K, N, g, sw, fast;
+  if (!take_ptr(a[0], &Wt) || !take_ptr(a[1], &St) || !take_i64(a[2], &K) ||
+      !take_i64(a[3], &N) || !take_i64(a[4], &g) || !take_i64(a[5], &sw) ||
+      !take_i64(a[6], &fast) || !take_ptr(a[7], &W) || !take_ptr(a[8], &stream))
+    return NULL;
+  return PyLong_FromLong(nibble_dequant_w4_strip_major(Wt, St, K, N, g, sw, (int)fast, W, stream));
+}
+
 /* chain_create(stages: bytes of n packed nibble_chain_stage, n, M, stream) -> (status, handle) */
 static PyObject* py_chain_create(PyObject* self, PyObject* const* a, Py_ssize_t n) {
   (void)self;
@@ -349,6 +378,10 @@ static PyMethodDef kMethods[] = {
      "nibble_pack_strip_major"},
     {"gemv_strip_major", (PyCFunction)(void (*)(void))py_sm_gemv, METH_FASTCALL,
      "nibble_gemv_w4a16_strip_major"},
+    {"gemm_strip_major", (PyCFunction)(void (*)(void))py_sm_gemm, METH_FASTCALL,
+     "nibble_gemm_w4a16_strip_major"},
+    {"dequant_strip_major", (PyCFunction)(void (*)(void))py_sm_dequant, METH_FASTCALL,
+     "nibble_dequant_w4_strip_major"},
     {"rmsnorm", (PyCFunction)(void (*)(void))py_rmsnorm, METH_FASTCALL, "nibble_rmsnorm_f16"},
     {"attention", (PyCFunction)(void (*)(void))py_attention, METH_FASTCALL,
      "nibble_attention_decode_f16"},

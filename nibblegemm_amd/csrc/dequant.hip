@@ -15,6 +15,7 @@
 
 #include "nibble_common.h"
 #include "nibble_decode.h"
+#include "stream_matmul.h"
 
 namespace nibble {
 
@@ -31,10 +32,13 @@ constexpr int kDequantThreads = 64;
 // and the host either way once the kernel completes.
 constexpr int kStoreAux = 1 | 2 | 16;
 
-template <int COLS, bool FAST, bool BUFFER_STORES>
+// STRIPS: the weights are in a strip-major layout `L` (strips of at least 16
+// columns, so a thread's 8 columns lie in one strip; every offset below
+// 2^31, host-checked); otherwise in the packed [K / 8, N] layout.
+template <int COLS, bool FAST, bool BUFFER_STORES, bool STRIPS = false>
 __global__ __launch_bounds__(kDequantThreads) void dequant_kernel(
     const uint32_t* __restrict__ Wq, const _Float16* __restrict__ S, _Float16* __restrict__ out,
-    int N, int group_size) {
+    int N, int group_size, WeightLayout L = WeightLayout()) {
   const int col_chunk = blockIdx.x * kDequantThreads + threadIdx.x;
   const int n0 = col_chunk * COLS;
   const int r8 = blockIdx.y;  // packed row
@@ -46,7 +50,22 @@ __global__ __launch_bounds__(kDequantThreads) void dequant_kernel(
 
   uint32_t q[COLS];
   _Float16 sc[COLS];
-  if constexpr (COLS == 8) {
+  if constexpr (STRIPS) {
+    static_assert(COLS == 8, "strip-major weights are read 8 columns at a time");
+    const char* wp = reinterpret_cast<const char*>(Wq) + r8 * L.w_row + L.wcol(n0);
+    const char* sp = reinterpret_cast<const char*>(S) + ((r8 * 8) / group_size) * L.s_row +
+                     L.scol(n0);
+    const u4_t a = *reinterpret_cast<const u4_t*>(wp);
+    const u4_t b = *reinterpret_cast<const u4_t*>(wp + 16);
+    const h8_t s = *reinterpret_cast<const h8_t*>(sp);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      q[c] = a[c];
+      q[4 + c] = b[c];
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c) sc[c] = s[c];
+  } else if constexpr (COLS == 8) {
     const u4_t a = *reinterpret_cast<const u4_t*>(Wq + in_off);
     const u4_t b = *reinterpret_cast<const u4_t*>(Wq + in_off + 4);
     const h8_t s = *reinterpret_cast<const h8_t*>(S + s_off);
@@ -187,5 +206,50 @@ extern "C" int nibble_dequant_w4(const void* Wq, int64_t wq_rows, int64_t wq_col
   else
     e = launch<1>(w, s, o, wq_rows, N, group_size, fast != 0, stream);
   if (e != hipSuccess) return hip_fail(e, "dequant kernel launch");
+  return ok();
+}
+
+// dequant_w4 of strip-major weights (no counterpart in the reference): the
+// same [K, N] fp16 output, bit for bit, as the packed call on the weight the
+// strips were packed from.
+extern "C" int nibble_dequant_w4_strip_major(const void* Wt, const void* St, int64_t K, int64_t N,
+                                             int64_t group_size, int64_t strip_cols, int fast,
+                                             void* W, void* stream_) {
+  using namespace nibble;
+  NIBBLE_CHECK(K >= 0 && N >= 0 && K % 8 == 0, "bad dimension (K a multiple of 8)");
+  NIBBLE_CHECK(strip_cols == 16 || strip_cols == 32 || strip_cols == 64,
+               "strip_cols must be 16, 32 or 64, got %lld", (long long)strip_cols);
+  NIBBLE_CHECK(N % strip_cols == 0, "N=%lld is not a multiple of strip_cols=%lld", (long long)N,
+               (long long)strip_cols);
+  int rc = validate_dequant(Wt, K / 8, N, St, group_size > 0 ? K / group_size : 0, N, group_size,
+                            W);
+  if (rc != NIBBLE_OK) return rc;
+  NIBBLE_CHECK(group_size == 64 || group_size == 128, "group_size must be 64 or 128");
+  NIBBLE_CHECK(strip_cols != 16 || group_size == 128, "16-column strips need group_size 128");
+  NIBBLE_CHECK(K / 8 * N * 4 < (int64_t(1) << 31), "weights beyond 32-bit offsets");
+  if (K == 0 || N == 0) return ok();
+  NIBBLE_CHECK(aligned(Wt, 16) && aligned(St, 16) && aligned(W, 16),
+               "strip-major dequant needs 16-byte aligned weights, scales and output");
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  DeviceGuard guard;
+  int dev = 0;
+  NIBBLE_HIP(guard.enter(stream, &dev));
+  const WeightLayout L = strip_major_layout(K, N, group_size, strip_cols);
+  const auto* w = static_cast<const uint32_t*>(Wt);
+  const auto* s = static_cast<const _Float16*>(St);
+  auto* o = static_cast<_Float16*>(W);
+  const dim3 grid(static_cast<unsigned>(ceil_div(N / 8, kDequantThreads)),
+                  static_cast<unsigned>(K / 8));
+  const bool bufs = 16 * N < (int64_t(1) << 31);
+  if (fast && bufs)
+    dequant_kernel<8, true, true, true><<<grid, kDequantThreads, 0, stream>>>(w, s, o, (int)N, (int)group_size, L);
+  else if (fast)
+    dequant_kernel<8, true, false, true><<<grid, kDequantThreads, 0, stream>>>(w, s, o, (int)N, (int)group_size, L);
+  else if (bufs)
+    dequant_kernel<8, false, true, true><<<grid, kDequantThreads, 0, stream>>>(w, s, o, (int)N, (int)group_size, L);
+  else
+    dequant_kernel<8, false, false, true><<<grid, kDequantThreads, 0, stream>>>(w, s, o, (int)N, (int)group_size, L);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, "strip-major dequant kernel launch");
   return ok();
 }

@@ -135,6 +135,7 @@ struct TileArgs {
   int M, K, N;
   int steps_per_split;  // 32-k steps per K split
   int splits;
+  WeightLayout L;       // where a column's words and scales live (packed or strip-major)
 };
 
 // Last-arriver sum of a split output tile [m0, m0 + BM) x [n0, n0 + BN) by
@@ -256,10 +257,11 @@ gemm_tile_kernel(TileArgs args) {
   // This workgroup's K split: steps [step0, step0 + ntiles) of 32 k.
   const int step0 = blockIdx.z * args.steps_per_split;
   const int ntiles = min(args.steps_per_split, K / BK - step0);
-  const uint32_t row_bytes = static_cast<uint32_t>(N) * 4u;
+  const uint32_t row_bytes = args.L.w_row;
   const __amdgpu_buffer_rsrc_t rx =
       make_rsrc(X, static_cast<uint32_t>(M) * static_cast<uint32_t>(K) * 2u);
-  const __amdgpu_buffer_rsrc_t rw = make_rsrc(Wq, static_cast<uint32_t>(K / 8) * row_bytes);
+  const __amdgpu_buffer_rsrc_t rw =
+      make_rsrc(Wq, static_cast<uint32_t>(K / 8) * static_cast<uint32_t>(N) * 4u);
   const __amdgpu_buffer_rsrc_t rsc =
       make_rsrc(S, static_cast<uint32_t>(K / GROUP) * static_cast<uint32_t>(N) * 2u);
   uint32_t voff_a[C::A_ITERS];
@@ -270,8 +272,8 @@ gemm_tile_kernel(TileArgs args) {
     voff_a[it] = gm < M ? (static_cast<uint32_t>(gm) * K + (e & 3) * 8) * 2u : kOutOfRange;
   }
   const bool b_ok = b_col < N;
-  const uint32_t voff_b = b_ok ? b_row * row_bytes + static_cast<uint32_t>(b_col) * 4u : kOutOfRange;
-  const uint32_t voff_s = b_ok ? static_cast<uint32_t>(b_col) * 2u : kOutOfRange;
+  const uint32_t voff_b = b_ok ? b_row * row_bytes + args.L.wcol(b_col) : kOutOfRange;
+  const uint32_t voff_s = b_ok ? args.L.scol(b_col) : kOutOfRange;
 
   // Loads of step `step`, clamped to the last step: a prefetch past the end
   // re-reads it (an L2 hit) rather than being skipped, so the loads are the
@@ -282,7 +284,7 @@ gemm_tile_kernel(TileArgs args) {
     for (int it = 0; it < C::A_ITERS; ++it)
       st.a[it] = __builtin_bit_cast(h8_t, __builtin_amdgcn_raw_buffer_load_b128(rx, voff_a[it], k0 * 2u, 0));
     st.b = BWords<VB>::load_w(rw, voff_b, (k0 / 8) * row_bytes);
-    st.s = BWords<VB>::load_s(rsc, voff_s, (k0 / GROUP) * static_cast<uint32_t>(N) * 2u);
+    st.s = BWords<VB>::load_s(rsc, voff_s, (k0 / GROUP) * args.L.s_row);
   };
   // LDS offsets (fp16 elements).  Rows 64 apart share the swizzle of their
   // low 5 bits, so each offset is a per-thread constant plus a row multiple.
@@ -574,10 +576,11 @@ __global__ __launch_bounds__((CWAVES + 4) * 64) void gemm_pc64_kernel(TileArgs a
     };
     const int prow = tid >> 5;
     const int b_col = n0 + 4 * (tid & 31);
-    const uint32_t row_bytes = static_cast<uint32_t>(N) * 4u;
+    const uint32_t row_bytes = args.L.w_row;
     const __amdgpu_buffer_rsrc_t rx =
         make_rsrc(args.X, static_cast<uint32_t>(M) * static_cast<uint32_t>(K) * 2u);
-    const __amdgpu_buffer_rsrc_t rw = make_rsrc(args.Wq, static_cast<uint32_t>(K / 8) * row_bytes);
+    const __amdgpu_buffer_rsrc_t rw =
+        make_rsrc(args.Wq, static_cast<uint32_t>(K / 8) * static_cast<uint32_t>(N) * 4u);
     const __amdgpu_buffer_rsrc_t rsc =
         make_rsrc(args.S, static_cast<uint32_t>(K / GROUP) * static_cast<uint32_t>(N) * 2u);
     uint32_t voff_a[A_IT];
@@ -590,8 +593,8 @@ __global__ __launch_bounds__((CWAVES + 4) * 64) void gemm_pc64_kernel(TileArgs a
       a_st[it] = lds_unit64(row, tid & 7) * 8;
     }
     const bool b_ok = b_col < N;  // N % 4 == 0: the quad is wholly inside or outside
-    const uint32_t voff_b = b_ok ? prow * row_bytes + static_cast<uint32_t>(b_col) * 4u : kOutOfRange;
-    const uint32_t voff_s = b_ok ? static_cast<uint32_t>(b_col) * 2u : kOutOfRange;
+    const uint32_t voff_b = b_ok ? prow * row_bytes + args.L.wcol(b_col) : kOutOfRange;
+    const uint32_t voff_s = b_ok ? args.L.scol(b_col) : kOutOfRange;
     int b_st[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) b_st[j] = lds_unit64(4 * (tid & 31) + j, prow) * 8;
@@ -605,7 +608,7 @@ __global__ __launch_bounds__((CWAVES + 4) * 64) void gemm_pc64_kernel(TileArgs a
           u4_t, __builtin_amdgcn_raw_buffer_load_b128(rw, voff_b, (k0 / 8) * row_bytes, 0));
       st.s = __builtin_bit_cast(
           h4_t, __builtin_amdgcn_raw_buffer_load_b64(
-                    rsc, voff_s, (k0 / GROUP) * static_cast<uint32_t>(N) * 2u, 0));
+                    rsc, voff_s, (k0 / GROUP) * args.L.s_row, 0));
     };
     auto store_step = [&](const Stage& st, int buf) {
 #pragma unroll
@@ -751,10 +754,11 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_big_kernel(TileArgs args) {
     u4_t b[B_IT];
     h4_t s;
   };
-  const uint32_t row_bytes = static_cast<uint32_t>(N) * 4u;
+  const uint32_t row_bytes = args.L.w_row;
   const __amdgpu_buffer_rsrc_t rx =
       make_rsrc(args.X, static_cast<uint32_t>(M) * static_cast<uint32_t>(K) * 2u);
-  const __amdgpu_buffer_rsrc_t rw = make_rsrc(args.Wq, static_cast<uint32_t>(K / 8) * row_bytes);
+  const __amdgpu_buffer_rsrc_t rw =
+      make_rsrc(args.Wq, static_cast<uint32_t>(K / 8) * static_cast<uint32_t>(N) * 4u);
   const __amdgpu_buffer_rsrc_t rsc =
       make_rsrc(args.S, static_cast<uint32_t>(K / GROUP) * static_cast<uint32_t>(N) * 2u);
   uint32_t voff_a[A_IT];
@@ -774,11 +778,11 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_big_kernel(TileArgs args) {
 #pragma unroll
   for (int it = 0; it < B_IT; ++it) {
     const int pr = tid / QUADS + PR_STEP * it;
-    voff_b[it] = b_ok ? pr * row_bytes + static_cast<uint32_t>(b_col) * 4u : kOutOfRange;
+    voff_b[it] = b_ok ? pr * row_bytes + args.L.wcol(b_col) : kOutOfRange;
 #pragma unroll
     for (int j = 0; j < 4; ++j) b_st[it][j] = lds_unit64(4 * quad + j, pr) * 8;
   }
-  const uint32_t voff_s = b_ok ? static_cast<uint32_t>(b_col) * 2u : kOutOfRange;
+  const uint32_t voff_s = b_ok ? args.L.scol(b_col) : kOutOfRange;
 
   auto load_step = [&](Stage& st, int step) {
     const uint32_t k0 = static_cast<uint32_t>((step0 + min(step, ntiles - 1)) * PBK);
@@ -792,7 +796,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_big_kernel(TileArgs args) {
           u4_t, __builtin_amdgcn_raw_buffer_load_b128(rw, voff_b[it], (k0 / 8) * row_bytes, 0));
     st.s = __builtin_bit_cast(
         h4_t, __builtin_amdgcn_raw_buffer_load_b64(
-                  rsc, voff_s, (k0 / GROUP) * static_cast<uint32_t>(N) * 2u, 0));
+                  rsc, voff_s, (k0 / GROUP) * args.L.s_row, 0));
   };
   auto store_step = [&](const Stage& st, int buf) {
 #pragma unroll
@@ -1169,14 +1173,16 @@ extern "C" size_t nibble_gemm_counter_bytes(int64_t M, int64_t K, int64_t N, int
   return counters;
 }
 
-extern "C" int nibble_gemm_w4a16(const void* X, int64_t x_rows, int64_t x_cols, const void* Wq,
-                                 int64_t wq_rows, int64_t wq_cols, const void* S, int64_t s_rows,
-                                 int64_t s_cols, int64_t group_size, int64_t version, void* Y,
-                                 void* workspace, size_t workspace_bytes, void* stream_) {
-  int rc = validate_gemm(X, x_rows, x_cols, Wq, wq_rows, wq_cols, S, s_rows, s_cols, group_size,
-                         version, Y);
-  if (rc != NIBBLE_OK) return rc;
-  const int64_t M = x_rows, K = x_cols, N = wq_cols;
+namespace {
+// The body of nibble_gemm_w4a16 for validated operands, the weights in the
+// packed layout (strip_cols 0) or the strip-major layout of that width: the
+// plans depend on (M, K, N, group_size, version) and pointer alignment only,
+// so both layouts run the same kernels in the same order and give the same
+// bits.
+int gemm_run(const void* X, int64_t M, int64_t K, int64_t N, const void* Wq, const void* S,
+             int64_t group_size, int64_t version, void* Y, void* workspace,
+             size_t workspace_bytes, void* stream_, int64_t strip_cols) {
+  int rc = NIBBLE_OK;
   if (M == 0 || N == 0) return ok();
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   DeviceGuard guard;
@@ -1191,7 +1197,7 @@ extern "C" int nibble_gemm_w4a16(const void* X, int64_t x_rows, int64_t x_cols, 
     rc = plan_stream(M, K, N, group_size, true, 0, 0, &p);
     if (rc != NIBBLE_OK) return rc;
     rc = launch_stream(X, Wq, S, Y, M, K, N, group_size, p, workspace, workspace_bytes, stream,
-                       "gemm (streaming) kernel launch");
+                       "gemm (streaming) kernel launch", 0, nullptr, nullptr, 0.0f, strip_cols);
     return rc == NIBBLE_OK ? ok() : rc;
   }
   const auto* x = static_cast<const _Float16*>(X);
@@ -1232,6 +1238,7 @@ extern "C" int nibble_gemm_w4a16(const void* X, int64_t x_rows, int64_t x_cols, 
   a.partial = p.splits > 1
                   ? reinterpret_cast<float*>(static_cast<char*>(workspace) + p.counter_bytes)
                   : nullptr;
+  a.L = layout_for(K, N, group_size, strip_cols);
   hipError_t e = hipSuccess;
   for (int64_t m0 = 0; m0 < M && e == hipSuccess; m0 += rows_max) {
     a.X = x + m0 * K;
@@ -1241,4 +1248,47 @@ extern "C" int nibble_gemm_w4a16(const void* X, int64_t x_rows, int64_t x_cols, 
   }
   if (e != hipSuccess) return hip_fail(e, "gemm kernel launch");
   return ok();
+}
+}  // namespace
+
+extern "C" int nibble_gemm_w4a16(const void* X, int64_t x_rows, int64_t x_cols, const void* Wq,
+                                 int64_t wq_rows, int64_t wq_cols, const void* S, int64_t s_rows,
+                                 int64_t s_cols, int64_t group_size, int64_t version, void* Y,
+                                 void* workspace, size_t workspace_bytes, void* stream_) {
+  const int rc = validate_gemm(X, x_rows, x_cols, Wq, wq_rows, wq_cols, S, s_rows, s_cols,
+                               group_size, version, Y);
+  if (rc != NIBBLE_OK) return rc;
+  return gemm_run(X, x_rows, x_cols, wq_cols, Wq, S, group_size, version, Y, workspace,
+                  workspace_bytes, stream_, 0);
+}
+
+// nibble_gemm_w4a16 for batches of 9 rows and more on strip-major weights
+// (no counterpart in the reference): the same plans, kernels and bits as the
+// packed call; batches of at most 8 rows take the strip-major GEMV.
+extern "C" int nibble_gemm_w4a16_strip_major(const void* X, int64_t x_rows, int64_t x_cols,
+                                             const void* Wt, const void* St, int64_t K, int64_t N,
+                                             int64_t group_size, int64_t strip_cols,
+                                             int64_t version, void* Y, void* workspace,
+                                             size_t workspace_bytes, void* stream) {
+  NIBBLE_CHECK(x_cols == K, "activation columns (%lld) disagree with K=%lld", (long long)x_cols,
+               (long long)K);
+  NIBBLE_CHECK(K > 0 && N > 0, "bad dimension (K and N must be positive)");
+  NIBBLE_CHECK(group_size == 64 || group_size == 128, "group_size must be 64 or 128");
+  NIBBLE_CHECK(K % group_size == 0, "K=%lld is not a multiple of group_size=%lld", (long long)K,
+               (long long)group_size);
+  NIBBLE_CHECK(strip_cols == 16 || strip_cols == 32 || strip_cols == 64,
+               "strip_cols must be 16, 32 or 64, got %lld", (long long)strip_cols);
+  NIBBLE_CHECK(N % strip_cols == 0, "N=%lld is not a multiple of strip_cols=%lld", (long long)N,
+               (long long)strip_cols);
+  NIBBLE_CHECK(strip_cols != 16 || group_size == 128, "16-column strips need group_size 128");
+  NIBBLE_CHECK(x_rows == 0 || x_rows > 8,
+               "batches of at most 8 rows take nibble_gemv_w4a16_strip_major (got M=%lld)",
+               (long long)x_rows);
+  NIBBLE_CHECK(Wt == nullptr || (aligned(Wt, 16) && aligned(St, 16)),
+               "strip-major weights and scales must be 16-byte aligned");
+  const int rc = validate_gemm(X, x_rows, x_cols, Wt, K / 8, N, St, K / group_size, N, group_size,
+                               version, Y);
+  if (rc != NIBBLE_OK) return rc;
+  return gemm_run(X, x_rows, K, N, Wt, St, group_size, version, Y, workspace, workspace_bytes,
+                  stream, strip_cols);
 }

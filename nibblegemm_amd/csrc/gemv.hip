@@ -66,13 +66,8 @@ struct GemvArgs {
   int strips;             // strip kernel: column strips of the launch
   int strips_per_xcd;     // strip kernel: strips run by each XCD's workgroups
   int stage_x;            // strip kernel: copy the activations to LDS (if they fit 64 KiB)
-  // Strip kernel addressing, in bytes.  Word (packed row r, strip column
-  // 4 c + j) of strip s is at s * w_strip + r * w_row + 16 c + 4 j; the scale
-  // of (group g, strip column j) at s * s_strip + g * s_row + 2 j.  The
-  // packed [K / 8, N] layout has w_row = 4 N, w_strip = 4 SW, s_row = 2 N,
-  // s_strip = 2 SW; the strip-major layout has w_row = 4 SW,
-  // w_strip = 4 SW K / 8, s_row = 2 SW, s_strip = 2 SW K / G.
-  uint32_t w_row, w_strip, s_row, s_strip;
+  // Where the weights and scales of a column live (packed or strip-major).
+  WeightLayout L;
 };
 
 __device__ __forceinline__ f4_t mfma16(h8_t a, h8_t b, f4_t c) {
@@ -253,15 +248,16 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs a) {
   const int kb = lane >> 4;  // 8-k block within a 32-k chunk
   const int col = strip * kStripCols + 4 * q;
   const bool col_ok = col < a.N;
-  const uint32_t row_bytes = static_cast<uint32_t>(a.N) * 4u;
+  const uint32_t row_bytes = a.L.w_row;
 
-  const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.Wq, static_cast<uint32_t>(a.K / 8) * row_bytes);
+  const __amdgpu_buffer_rsrc_t rw =
+      make_rsrc(a.Wq, static_cast<uint32_t>(a.K / 8) * static_cast<uint32_t>(a.N) * 4u);
   const __amdgpu_buffer_rsrc_t rx =
       make_rsrc(a.X, static_cast<uint32_t>(a.M) * static_cast<uint32_t>(a.K) * 2u);
   const __amdgpu_buffer_rsrc_t rs =
       make_rsrc(a.S, static_cast<uint32_t>(a.K / GROUP) * static_cast<uint32_t>(a.N) * 2u);
-  const uint32_t voff_w = col_ok ? kb * row_bytes + static_cast<uint32_t>(col) * 4u : kOutOfRange;
-  const uint32_t voff_s = col_ok ? static_cast<uint32_t>(col) * 2u : kOutOfRange;
+  const uint32_t voff_w = col_ok ? kb * row_bytes + a.L.wcol(col) : kOutOfRange;
+  const uint32_t voff_s = col_ok ? a.L.scol(col) : kOutOfRange;
   uint32_t voff_x[TILES];
 #pragma unroll
   for (int t = 0; t < TILES; ++t) {
@@ -298,7 +294,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs a) {
               h8_t, __builtin_amdgcn_raw_buffer_load_b128(rx, voff_x[t], kx + c * 64, 0));
     }
     st.s = __builtin_bit_cast(
-        h4_t, __builtin_amdgcn_raw_buffer_load_b64(rs, voff_s, static_cast<uint32_t>(g) * a.N * 2u,
+        h4_t, __builtin_amdgcn_raw_buffer_load_b64(rs, voff_s, static_cast<uint32_t>(g) * a.L.s_row,
                                                    kWPolicy));
 #pragma unroll
     for (int c = 0; c < CPG; ++c)
@@ -559,12 +555,12 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_strip_kernel(GemvArgs a) {
   const uint32_t c = lane % LPR, r = lane / LPR;
   const uint32_t col = strip * SW + 4 * c;
   const bool col_ok = strip < static_cast<uint32_t>(a.strips) && col < N;
-  const uint32_t row_bytes = a.w_row, s_row = a.s_row;
+  const uint32_t row_bytes = a.L.w_row, s_row = a.L.s_row;
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.Wq, (K / 8) * N * 4u);
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.X, static_cast<uint32_t>(a.M) * K * 2u);
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.S, total_groups * N * 2u);
-  const uint32_t voff_w = col_ok ? strip * a.w_strip + r * row_bytes + 16u * c : kOutOfRange;
-  const uint32_t voff_s = col_ok ? strip * a.s_strip + 8u * c : kOutOfRange;
+  const uint32_t voff_w = col_ok ? r * row_bytes + a.L.wcol(col) : kOutOfRange;
+  const uint32_t voff_s = col_ok ? a.L.scol(col) : kOutOfRange;
   // A side: lane (m', kb) holds row m' = RPT p + mm of each tile at k block
   // kb, i.e. the 8 k of packed row P kb + p of a wave load.
   const uint32_t mq = lane & 15u, kb = lane >> 4;
@@ -613,9 +609,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_strip_kernel(GemvArgs a) {
       if (ch < chunks)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
             rs, (lds_ptr)(s_lds + blk * 512), 16,
-            strip < static_cast<uint32_t>(a.strips) && scol < N
-                ? strip * a.s_strip + g * s_row + 16u * part
-                : kOutOfRange,
+            strip < static_cast<uint32_t>(a.strips) && scol < N ? a.L.scol(scol) + g * s_row
+                                                                : kOutOfRange,
             0, 0, 0);
     }
     // Rows past M read as zeros from LDS (no masking in the loop).
@@ -1158,7 +1153,7 @@ bool stream_supported(const void* X, const void* Wq, const void* S, const void* 
 int launch_stream(const void* X, const void* Wq, const void* S, void* Y, int64_t M, int64_t K,
                   int64_t N, int64_t G, const StreamPlan& p, void* workspace,
                   size_t workspace_bytes, hipStream_t stream, const char* who, int epilogue,
-                  const void* bias, const void* norm_w, float norm_eps) {
+                  const void* bias, const void* norm_w, float norm_eps, int64_t strip_cols) {
   if (p.workspace_bytes > 0) {
     if (workspace == nullptr || workspace_bytes < p.workspace_bytes)
       return fail(NIBBLE_ERR_WORKSPACE, "%s needs %zu bytes of workspace, got %zu", who,
@@ -1170,16 +1165,16 @@ int launch_stream(const void* X, const void* Wq, const void* S, void* Y, int64_t
   void* partials =
       p.workspace_bytes > 0 ? static_cast<char*>(workspace) + p.counter_bytes : nullptr;
   return launch_stream_split(X, Wq, S, Y, M, K, N, G, p, counters, partials, stream, who,
-                             epilogue, bias, norm_w, norm_eps);
+                             epilogue, bias, norm_w, norm_eps, strip_cols);
 }
 
 int launch_stream_split(const void* X, const void* Wq, const void* S, void* Y, int64_t M,
                         int64_t K, int64_t N, int64_t G, const StreamPlan& p, void* counters,
                         void* partials, hipStream_t stream, const char* who, int epilogue,
-                        const void* bias, const void* norm_w, float norm_eps, bool strip_major) {
-  if (strip_major && p.kernel != kStripKernel)
-    return fail(NIBBLE_ERR_UNSUPPORTED, "%s: strip-major weights need the strip kernel", who);
+                        const void* bias, const void* norm_w, float norm_eps,
+                        int64_t strip_cols) {
   GemvArgs a;
+  a.L = layout_for(K, N, G, strip_cols);
   a.X = static_cast<const _Float16*>(X);
   a.Wq = static_cast<const uint32_t*>(Wq);
   a.S = static_cast<const _Float16*>(S);
@@ -1199,19 +1194,7 @@ int launch_stream_split(const void* X, const void* Wq, const void* S, void* Y, i
   if (p.kernel == kStripKernel) {
     a.strips = p.strips;
     a.strips_per_xcd = static_cast<int>(ceil_div(p.strips, 8));
-    const uint32_t sw = static_cast<uint32_t>(p.strip_cols);
     a.stage_x = p.stage_x ? 1 : 0;
-    if (strip_major) {
-      a.w_row = sw * 4u;
-      a.w_strip = static_cast<uint32_t>(K / 8) * sw * 4u;
-      a.s_row = sw * 2u;
-      a.s_strip = static_cast<uint32_t>(K / G) * sw * 2u;
-    } else {
-      a.w_row = static_cast<uint32_t>(N) * 4u;
-      a.w_strip = sw * 4u;
-      a.s_row = static_cast<uint32_t>(N) * 2u;
-      a.s_strip = sw * 2u;
-    }
     e = G == 128 ? launch_strip_group<128>(a, p, stream) : launch_strip_group<64>(a, p, stream);
   } else {
     e = G == 128 ? launch_group<128>(a, p, stream) : launch_group<64>(a, p, stream);
@@ -1713,6 +1696,6 @@ extern "C" int nibble_gemv_w4a16_strip_major(const void* X, int64_t x_rows, int6
   NIBBLE_HIP(guard.enter(stream, &dev));
   rc = launch_stream_split(X, Wt, St, Y, M, K, N, group_size, p, nullptr, nullptr, stream,
                            "strip-major gemv kernel launch", static_cast<int>(epilogue), bias,
-                           norm_weight, norm_eps, true);
+                           norm_weight, norm_eps, strip_cols);
   return rc == NIBBLE_OK ? ok() : rc;
 }

@@ -10,6 +10,55 @@ namespace nibble {
 
 constexpr int kStreamMaxM = 128;
 
+// Where column n's packed words and scales live, for either weight layout
+// (byte offsets within the words / scales):
+//   packed [K / 8, N] (the reference's format): word (r, n) at r w_row + 4 n
+//     with w_row = 4 N, scale (g, n) at g s_row + 2 n with s_row = 2 N --
+//     one strip (strip_shift 31);
+//   strip-major of width SW = 2^strip_shift (nibble_pack_strip_major): the
+//     words of strip n / SW are one run of w_strip bytes, row r of it at
+//     r w_row (w_row = 4 SW), column n % SW at 4 (n % SW) within the row;
+//     the scales likewise (s_strip, s_row = 2 SW).
+// Every kernel reading weights computes a lane's column offset once with
+// wcol / scol and steps along K by w_row / s_row, so it reads either layout
+// and loads the same values from both.
+struct WeightLayout {
+  uint32_t strip_shift = 31;
+  uint32_t w_row = 0, w_strip = 0;
+  uint32_t s_row = 0, s_strip = 0;
+  __host__ __device__ uint32_t wcol(uint32_t n) const {
+    return (n >> strip_shift) * w_strip + (n & ((1u << strip_shift) - 1u)) * 4u;
+  }
+  __host__ __device__ uint32_t scol(uint32_t n) const {
+    return (n >> strip_shift) * s_strip + (n & ((1u << strip_shift) - 1u)) * 2u;
+  }
+};
+
+inline WeightLayout packed_layout(int64_t N) {
+  WeightLayout l;
+  l.strip_shift = 31;
+  l.w_row = static_cast<uint32_t>(N) * 4u;
+  l.s_row = static_cast<uint32_t>(N) * 2u;
+  return l;
+}
+
+// SW must be 16, 32 or 64 (the caller checks).
+inline WeightLayout strip_major_layout(int64_t K, int64_t N, int64_t G, int64_t SW) {
+  (void)N;
+  WeightLayout l;
+  l.strip_shift = SW == 16 ? 4u : SW == 32 ? 5u : 6u;
+  l.w_row = static_cast<uint32_t>(SW) * 4u;
+  l.w_strip = static_cast<uint32_t>(K / 8 * SW * 4);
+  l.s_row = static_cast<uint32_t>(SW) * 2u;
+  l.s_strip = static_cast<uint32_t>(K / G * SW * 2);
+  return l;
+}
+
+// The layout of a call: packed when strip_cols is 0, else strip-major.
+inline WeightLayout layout_for(int64_t K, int64_t N, int64_t G, int64_t strip_cols) {
+  return strip_cols > 0 ? strip_major_layout(K, N, G, strip_cols) : packed_layout(N);
+}
+
 // Two kernels serve the plan.  kSplitKernel: 64-column strips, K split
 // across workgroups when a wave would stream too many groups, partials
 // reduced by the last workgroup of a strip (any M up to kStreamMaxM).
@@ -70,18 +119,18 @@ int launch_stream(const void* X, const void* Wq, const void* S, void* Y, int64_t
                   int64_t N, int64_t G, const StreamPlan& p, void* workspace,
                   size_t workspace_bytes, hipStream_t stream, const char* who, int epilogue = 0,
                   const void* bias = nullptr, const void* norm_w = nullptr,
-                  float norm_eps = 0.0f);
+                  float norm_eps = 0.0f, int64_t strip_cols = 0);
 
 // launch_stream with the split-K workspace given as its two parts: the
 // counter region (zero on entry, left zero) and the fp32 partials.  The plan
-// must fit whatever those point at; no checks are made here.  `strip_major`
-// reads Wq and S in the strip-major layout of the plan's strip width (strip
-// kernel plans only).
+// must fit whatever those point at; no checks are made here.  A non-zero
+// `strip_cols` reads Wq and S in the strip-major layout of that width (any
+// plan; the plan's geometry, and so the bits, are the packed layout's).
 int launch_stream_split(const void* X, const void* Wq, const void* S, void* Y, int64_t M,
                         int64_t K, int64_t N, int64_t G, const StreamPlan& p, void* counters,
                         void* partials, hipStream_t stream, const char* who, int epilogue = 0,
                         const void* bias = nullptr, const void* norm_w = nullptr,
-                        float norm_eps = 0.0f, bool strip_major = false);
+                        float norm_eps = 0.0f, int64_t strip_cols = 0);
 
 // Strip width recommended for strip-major weights of this shape (0: none
 // fits), and the strip kernel's plan for a strip-major weight of width SW.

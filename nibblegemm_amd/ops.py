@@ -32,8 +32,8 @@ from typing import Dict, Optional, Tuple
 import torch
 
 from . import _native
-from .quant import (SWIGLU_BLOCK, QuantizedWeight, StripMajorWeight, quantize,  # noqa: F401
-                    split_swiglu)
+from .quant import (SWIGLU_BLOCK, QuantizedWeight, StripMajorWeight,  # noqa: F401
+                    from_strip_major, quantize, split_swiglu)
 
 #: Batch sizes at or below this go to the bandwidth-bound decode kernel
 #: (reference ops.py:30).
@@ -218,9 +218,20 @@ def _gemm_workspace(ext, device: torch.device, stream: int, M: int, K: int, N: i
 
 def dequant(qw: QuantizedWeight, fast: bool = True) -> torch.Tensor:
     """Expand packed INT4 to a dense ``[K, N]`` fp16 matrix on the device
-    (reference ops.py:59-61 -> csrc/dequant_kernel.cu:48-74)."""
+    (reference ops.py:59-61 -> csrc/dequant_kernel.cu:48-74).  A
+    :class:`StripMajorWeight` gives the same matrix as the packed weight it
+    was made from."""
     ext = _bind()
     Wq, S = qw.qweight, qw.scales
+    if isinstance(qw, StripMajorWeight):
+        _check_strip_weight(qw)
+        out = torch.empty((qw.K, qw.N), dtype=torch.float16, device=Wq.device)
+        rc = ext.dequant_strip_major(Wq.data_ptr(), S.data_ptr(), qw.K, qw.N, qw.group_size,
+                                     qw.strip_cols, 1 if fast else 0, out.data_ptr(),
+                                     _stream(Wq.device))
+        if rc:
+            _raise(rc, ext)
+        return out
     if not (Wq.is_cuda and S.is_cuda):
         raise RuntimeError("tensors must live on the GPU")
     if Wq.dtype != torch.int32:
@@ -273,7 +284,11 @@ def gemv(X: torch.Tensor, qw: QuantizedWeight, version: int = 4, splits: int = 0
 def gemm(X: torch.Tensor, qw: QuantizedWeight, version: int = 6) -> torch.Tensor:
     """Prefill-regime matmul on MFMA (reference ops.py:77-86).  ``version`` 6
     (default) or 7 select two tile shapes with identical numerics; batches of
-    M <= 128 run the GEMV's weight-streaming kernel whatever the version."""
+    M <= 128 run the GEMV's weight-streaming kernel whatever the version.  A
+    :class:`StripMajorWeight` runs the same plans and kernels (the same bits
+    as its packed weight) from 9 rows, the strip-major GEMV below."""
+    if isinstance(qw, StripMajorWeight):
+        return _strip_gemm(X, qw, version)
     ext = _bind()
     Wq, S = qw.qweight, qw.scales
     _check_matmul_inputs(X, Wq, S)
@@ -301,7 +316,8 @@ def to_strip_major(qw: QuantizedWeight, strip_cols: int = 0) -> StripMajorWeight
     """A device copy of ``qw`` in the strip-major layout of the decode GEMV
     (one permutation kernel on the current stream; same bytes again).
     ``strip_cols`` 0 picks :func:`strip_major_cols`.  The result serves
-    :func:`matmul` and the fused decode ops for batches of at most 8 rows."""
+    :func:`matmul`, :func:`gemm`, :func:`dequant` and the fused ops at every
+    batch size (the fused epilogues run in the kernel up to 8 rows)."""
     ext = _bind()
     Wq, S = qw.qweight, qw.scales
     if not (Wq.is_cuda and S.is_cuda):
@@ -325,6 +341,44 @@ def to_strip_major(qw: QuantizedWeight, strip_cols: int = 0) -> StripMajorWeight
     if rc:
         _raise(rc, ext)
     return StripMajorWeight(Wt, St, qw.group_size, qw.K, qw.N, sw)
+
+
+def _check_strip_weight(w: StripMajorWeight) -> None:
+    Wt, St = w.qweight, w.scales
+    if not (Wt.is_cuda and St.is_cuda):
+        raise RuntimeError("tensors must live on the GPU")
+    if Wt.dtype != torch.int32 or St.dtype != torch.float16:
+        raise RuntimeError("strip-major weights must be int32 and scales fp16")
+    if not (Wt.is_contiguous() and St.is_contiguous()):
+        raise RuntimeError("inputs must be contiguous")
+
+
+def _strip_gemm(X: torch.Tensor, w: StripMajorWeight, version: int = 6) -> torch.Tensor:
+    """``X @ W`` on strip-major weights: at most 8 rows through the strip-major
+    GEMV, more through the packed layout's GEMM plans."""
+    if X.dim() == 2 and X.size(0) <= DECODE_MAX_M:
+        return _strip_gemv(X, w, 0, None, w.N)
+    ext = _bind()
+    _check_strip_weight(w)
+    if not X.is_cuda:
+        raise RuntimeError("all tensors must live on the GPU")
+    if X.dtype != torch.float16:
+        raise RuntimeError("activations must be fp16")
+    if not X.is_contiguous() or X.dim() != 2:
+        raise RuntimeError("activations must be a contiguous 2-D matrix")
+    if X.device != w.qweight.device:
+        raise RuntimeError("all tensors must live on the same device")
+    M, K = X.shape
+    dev = X.device
+    stream = _stream(dev)
+    Y = torch.empty((M, w.N), dtype=torch.float16, device=dev)
+    ws, ws_bytes = _gemm_workspace(ext, dev, stream, M, w.K, w.N, w.group_size, version)
+    rc = ext.gemm_strip_major(X.data_ptr(), M, K, w.qweight.data_ptr(), w.scales.data_ptr(), w.K,
+                              w.N, w.group_size, w.strip_cols, version, Y.data_ptr(),
+                              ws.data_ptr() if ws is not None else None, ws_bytes, stream)
+    if rc:
+        _raise(rc, ext)
+    return Y
 
 
 def _strip_gemv(X: torch.Tensor, w: StripMajorWeight, epilogue: int,
@@ -370,7 +424,7 @@ def matmul(X: torch.Tensor, qw, splits: int = 0, block_threads: int = 0) -> torc
     if isinstance(qw, StripMajorWeight):
         if splits or block_threads:
             raise ValueError("strip-major weights take no splits / block_threads override")
-        return _strip_gemv(X, qw, 0, None, qw.N)
+        return _strip_gemm(X, qw)
     if X.size(0) <= DECODE_MAX_M:
         return gemv(X, qw, version=4, splits=splits, block_threads=block_threads)
     return gemm(X, qw)
@@ -441,7 +495,7 @@ def matmul_bias(X: torch.Tensor, qw: QuantizedWeight, bias: torch.Tensor) -> tor
     fp16_bias = (bias.dtype == torch.float16 and bias.dim() == 1 and bias.numel() == qw.N
                  and bias.device == X.device and bias.is_contiguous())
     if isinstance(qw, StripMajorWeight):
-        if fp16_bias:
+        if fp16_bias and X.size(0) <= DECODE_MAX_M:
             return _strip_gemv(X, qw, 1, bias, qw.N)
     elif fp16_bias and _fusable(X, qw):
         return _fused(X, qw, 1, bias, qw.N)
@@ -459,9 +513,9 @@ def matmul_swiglu(X: torch.Tensor, qw: QuantizedWeight) -> torch.Tensor:
     if qw.N % (2 * SWIGLU_BLOCK):
         raise ValueError(f"N={qw.N} is not an interleaved gate|up weight (multiple of 32)")
     if isinstance(qw, StripMajorWeight):
-        if qw.strip_cols >= 2 * SWIGLU_BLOCK:
+        if qw.strip_cols >= 2 * SWIGLU_BLOCK and X.size(0) <= DECODE_MAX_M:
             return _strip_gemv(X, qw, 2, None, qw.N // 2)
-        gate, up = split_swiglu(_strip_gemv(X, qw, 0, None, qw.N))
+        gate, up = split_swiglu(_strip_gemm(X, qw))
         return torch.nn.functional.silu(gate) * up
     if _fusable(X, qw):
         return _fused(X, qw, 2, None, qw.N // 2)
@@ -530,10 +584,15 @@ class QuantLinear(torch.nn.Module):
     matmul's output stage where the kernel supports it (same bits as a
     separate fp16 add).
 
-    :meth:`prepare_decode` adds a strip-major copy of the weight (not part of
-    the state dict) that batches of at most 8 rows then multiply with; it
-    costs the weight's bytes again and is rebuilt when a state dict is
-    loaded."""
+    :meth:`prepare_decode` converts the weight, in place, to the strip-major
+    layout (:func:`to_strip_major`), which every batch size reads: at most 8
+    rows through the strip-major GEMV (the fast decode path), more through
+    the same GEMM plans as the packed weight (the same bits).  The module
+    then holds that one copy -- ``qweight`` ``[out/SW, in/8, SW]``,
+    ``scales`` ``[out/SW, in/G, SW]``, ``strip_cols`` = SW -- and converts at
+    the state-dict boundary: ``state_dict()`` returns the packed tensors and
+    ``load_state_dict()`` takes packed tensors.  :meth:`release_decode`
+    converts back."""
 
     def __init__(self, qw: QuantizedWeight, bias: Optional[torch.Tensor] = None):
         super().__init__()
@@ -543,26 +602,51 @@ class QuantLinear(torch.nn.Module):
         for name, tensor in (("qweight", qw.qweight), ("scales", qw.scales), ("bias", bias)):
             self.register_buffer(name, tensor)
         self.strip_cols = 0
-        self.register_buffer("qweight_strips", None, persistent=False)
-        self.register_buffer("scales_strips", None, persistent=False)
-        self.register_load_state_dict_post_hook(QuantLinear._refresh_decode_copy)
 
     def prepare_decode(self, strip_cols: int = 0) -> "QuantLinear":
-        """Build the strip-major copy of the weight on its GPU (``strip_cols``
-        0 picks :func:`strip_major_cols`); returns the module."""
+        """Convert the weight to the strip-major layout on its GPU, in place
+        (``strip_cols`` 0 picks :func:`strip_major_cols`); returns the
+        module.  The packed copy is released once converted."""
+        if self.strip_cols:
+            if strip_cols in (0, self.strip_cols):
+                return self
+            self.release_decode()
         sm = to_strip_major(self._qw(), strip_cols)
-        self.qweight_strips, self.scales_strips, self.strip_cols = sm.qweight, sm.scales, sm.strip_cols
+        self.qweight, self.scales, self.strip_cols = sm.qweight, sm.scales, sm.strip_cols
         return self
 
-    def release_decode(self) -> None:
-        """Drop the strip-major copy."""
-        self.qweight_strips = self.scales_strips = None
-        self.strip_cols = 0
+    def release_decode(self) -> "QuantLinear":
+        """Convert a strip-major weight back to the packed layout, in place."""
+        if self.strip_cols:
+            qw = self._packed()
+            self.qweight, self.scales, self.strip_cols = qw.qweight, qw.scales, 0
+        return self
 
-    @staticmethod
-    def _refresh_decode_copy(module: "QuantLinear", incompatible_keys) -> None:
-        if module.qweight_strips is not None:
-            module.prepare_decode(module.strip_cols)
+    def _packed(self) -> QuantizedWeight:
+        """The packed form of the weight (a converted copy when strip-major)."""
+        if not self.strip_cols:
+            return self._qw()
+        return from_strip_major(self._qw())
+
+    def _save_to_state_dict(self, destination, prefix, keep_vars):
+        super()._save_to_state_dict(destination, prefix, keep_vars)
+        if self.strip_cols:
+            qw = self._packed()
+            destination[prefix + "qweight"] = qw.qweight
+            destination[prefix + "scales"] = qw.scales
+
+    def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys,
+                              unexpected_keys, error_msgs):
+        qk, sk = prefix + "qweight", prefix + "scales"
+        if self.strip_cols and qk in state_dict and sk in state_dict:
+            packed = QuantizedWeight(state_dict[qk].to(self.qweight.device).contiguous(),
+                                     state_dict[sk].to(self.scales.device).contiguous(),
+                                     self.group_size, self.K, self.N)
+            sm = to_strip_major(packed, self.strip_cols)
+            state_dict = dict(state_dict)
+            state_dict[qk], state_dict[sk] = sm.qweight, sm.scales
+        super()._load_from_state_dict(state_dict, prefix, local_metadata, strict, missing_keys,
+                                      unexpected_keys, error_msgs)
 
     @classmethod
     def from_linear(cls, linear: torch.nn.Linear, group_size: int = 128) -> "QuantLinear":
@@ -573,18 +657,15 @@ class QuantLinear(torch.nn.Module):
         bias = None if linear.bias is None else linear.bias.detach().clone()
         return cls(quantize(weight_kn, group_size).to(linear.weight.device), bias)
 
-    def _qw(self) -> QuantizedWeight:
+    def _qw(self):
+        if self.strip_cols:
+            return StripMajorWeight(self.qweight, self.scales, self.group_size, self.K, self.N,
+                                    self.strip_cols)
         return QuantizedWeight(self.qweight, self.scales, self.group_size, self.K, self.N)
-
-    def _weight_for(self, m: int):
-        if self.qweight_strips is not None and 0 < m <= DECODE_MAX_M:
-            return StripMajorWeight(self.qweight_strips, self.scales_strips, self.group_size,
-                                    self.K, self.N, self.strip_cols)
-        return self._qw()
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         lead = x.shape[:-1]
         rows = x.reshape(-1, x.shape[-1]).contiguous()
-        w = self._weight_for(rows.shape[0])
+        w = self._qw()
         y = matmul(rows, w) if self.bias is None else matmul_bias(rows, w, self.bias)
         return y.reshape(*lead, self.N)

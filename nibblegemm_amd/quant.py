@@ -227,9 +227,9 @@ class StripMajorWeight:
     whole: ``qweight`` int32 ``[N / strip_cols, K / 8, strip_cols]`` and
     ``scales`` fp16 ``[N / strip_cols, K / group_size, strip_cols]`` hold the
     words and scales of the packed layout, permuted (:func:`strip_major`).  A
-    decode workgroup then reads one contiguous run per strip.  Serves batches
-    of at most 8 rows (:func:`nibblegemm_amd.ops.to_strip_major` makes one on
-    the device)."""
+    decode workgroup then reads one contiguous run per strip.  Serves every
+    batch size (:func:`nibblegemm_amd.ops.to_strip_major` makes one on the
+    device; :func:`from_strip_major` restores the packed weight)."""
 
     qweight: torch.Tensor
     scales: torch.Tensor
@@ -262,6 +262,17 @@ def strip_major(qw: QuantizedWeight, strip_cols: int) -> StripMajorWeight:
         return t.reshape(rows, n // strip_cols, strip_cols).permute(1, 0, 2).contiguous()
 
     return StripMajorWeight(cut(qw.qweight), cut(qw.scales), qw.group_size, qw.K, qw.N, strip_cols)
+
+
+def from_strip_major(sm: StripMajorWeight) -> QuantizedWeight:
+    """The packed weight a strip-major one was made from (the inverse
+    permutation of :func:`strip_major`, on its own device)."""
+
+    def join(t: torch.Tensor) -> torch.Tensor:
+        strips, rows, sw = t.shape
+        return t.permute(1, 0, 2).reshape(rows, strips * sw).contiguous()
+
+    return QuantizedWeight(join(sm.qweight), join(sm.scales), sm.group_size, sm.K, sm.N)
 
 
 def pack_nibbles(qu: np.ndarray) -> np.ndarray:

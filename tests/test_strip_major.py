@@ -19,6 +19,7 @@ import torch
 
 import nibblegemm_amd as ng
 from nibblegemm_amd import ops, quant
+import oracle as O
 from cases import DECODE_SHAPES, host, oracle_y, rms_err, synthetic
 
 OK, INVALID, UNSUPPORTED = 0, 1, 2
@@ -266,33 +267,92 @@ def test_graph_replay_repeats_eager_bits():
 
 
 @pytest.mark.gpu
-def test_batches_above_8_are_refused():
-    _, _, _, Xd, _, sm = strip_case(9, 256, 64, 128, seed=0)
-    with pytest.raises(ValueError, match="at most 8 rows"):
-        ng.matmul(Xd, sm)
+def test_overrides_are_refused():
+    _, _, _, Xd, _, sm = strip_case(1, 256, 64, 128, seed=0)
     with pytest.raises(ValueError, match="no splits"):
-        ng.matmul(Xd[:1], sm, splits=2)
+        ng.matmul(Xd, sm, splits=2)
 
 
 @pytest.mark.gpu
-def test_quantlinear_decode_copy():
+@pytest.mark.parametrize("K,N", [(4096, 14336), (14336, 4096)])
+@pytest.mark.parametrize("M", [9, 16, 17, 24, 32, 33, 64, 128, 129, 512, 2048])
+def test_batches_above_8_have_the_packed_bits(M, K, N):
+    """From 9 rows a strip-major weight runs the packed weight's plans and
+    kernels (streaming, 64-row tiles with a K split, 128 / 256-row tiles),
+    reading the strip-major layout: the outputs are the packed call's bits,
+    and so as close to the oracle as those (tests/test_gemm.py)."""
+    X, packed, scales, Xd, qw, sm = strip_case(M, K, N, 128, seed=M + K)
+    got = ng.matmul(Xd, sm)
+    assert torch.equal(got, ng.matmul(Xd, qw))
+    if M > 128:
+        assert torch.equal(ng.gemm(Xd, sm, version=7), ng.gemm(Xd, qw, version=7))
+    if M in (17, 129):
+        rows = [0, M // 2, M - 1]
+        ref = O.reference_matmul(np.ascontiguousarray(X[rows]), packed, scales, K, 128)
+        assert rms_err(host(got[rows]), ref.astype(np.float32)) <= RMS_TOL
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,K,N,g,sw", [(9, 1024, 448, 128, 16), (40, 2048, 512, 64, 32),
+                                        (200, 4096, 1024, 128, 16), (100, 1024, 4096, 64, 64),
+                                        (1000, 4096, 4096, 128, 32), (16, 4096, 28672, 128, 64)])
+def test_every_width_above_8_rows_has_the_packed_bits(M, K, N, g, sw):
+    _, _, _, Xd, qw, sm = strip_case(M, K, N, g, sw, seed=sw + M)
+    assert torch.equal(ng.matmul(Xd, sm), ng.matmul(Xd, qw))
+    bias = (torch.randn(N, generator=torch.Generator().manual_seed(2)) * 0.3).half().cuda()
+    assert torch.equal(ng.matmul_bias(Xd, sm, bias), ng.matmul(Xd, qw) + bias)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("K,N,g,sw", [(4096, 14336, 128, 64), (14336, 4096, 128, 16),
+                                      (1024, 448, 64, 32), (256, 96, 128, 32)])
+@pytest.mark.parametrize("fast", [True, False])
+def test_dequant_of_strip_major_weights_is_the_packed_dequant(K, N, g, sw, fast):
+    _, _, _, _, qw, sm = strip_case(1, K, N, g, sw, seed=K + N)
+    a = ng.dequant(sm, fast=fast)
+    assert a.shape == (K, N)
+    assert torch.equal(a.view(torch.int16), ng.dequant(qw, fast=fast).view(torch.int16))
+
+
+def test_strip_major_round_trip_on_the_host():
+    _, packed, scales = O.synthetic_case(1, 256, 96, 128, 3)
+    qw = quant.QuantizedWeight(torch.from_numpy(packed.view(np.int32)),
+                               torch.from_numpy(scales.view(np.float16)), 128, 256, 96)
+    for sw in (16, 32):
+        back = quant.from_strip_major(quant.strip_major(qw, sw))
+        assert torch.equal(back.qweight, qw.qweight) and torch.equal(back.scales, qw.scales)
+
+
+@pytest.mark.gpu
+def test_quantlinear_keeps_one_strip_major_copy():
+    """prepare_decode converts the weight in place: one copy, read by every
+    batch size; the state dict stays the reference's packed format both
+    ways."""
     torch.manual_seed(1)
     lin = torch.nn.Linear(1024, 448).half().cuda()
     ql = ng.QuantLinear.from_linear(lin)
     x = torch.randn(3, 1024, device="cuda").half()
-    before = ql(x)
-    assert ql.prepare_decode() is ql and ql.strip_cols == ng.strip_major_cols(1024, 448, 128)
-    assert set(ql.state_dict()) == {"qweight", "scales", "bias"}
-    sm = ng.StripMajorWeight(ql.qweight_strips, ql.scales_strips, 128, 1024, 448, ql.strip_cols)
+    big = torch.randn(40, 1024, device="cuda").half()
+    packed = {k: v.clone() for k, v in ql.state_dict().items()}
+    before, before_big = ql(x), ql(big)
+    assert ql.prepare_decode() is ql
+    sw = ng.strip_major_cols(1024, 448, 128)
+    assert ql.strip_cols == sw and tuple(ql.qweight.shape) == (448 // sw, 128, sw)
+    assert len(list(ql.buffers())) == 3  # qweight, scales, bias: one copy of the weight
+    sd = ql.state_dict()
+    assert set(sd) == {"qweight", "scales", "bias"}
+    assert all(torch.equal(sd[k], packed[k]) for k in sd)
+    sm = ng.StripMajorWeight(ql.qweight, ql.scales, 128, 1024, 448, sw)
     assert torch.equal(ql(x), ng.matmul(x, sm) + ql.bias)
     assert rms_err(host(ql(x)), host(before)) <= 5e-3
-    big = torch.randn(40, 1024, device="cuda").half()  # above 8 rows: the packed weight
-    assert torch.equal(ql(big), ng.matmul_bias(big, ql._qw(), ql.bias))
-    # loading a state dict rebuilds the copy from the new weight
+    assert torch.equal(ql(big), before_big)  # above 8 rows: the packed weight's bits
+    # a packed state dict loads into the strip-major module
     other = ng.QuantLinear.from_linear(torch.nn.Linear(1024, 448).half().cuda())
     ql.load_state_dict(other.state_dict())
-    other.prepare_decode(ql.strip_cols)
-    assert torch.equal(ql.qweight_strips, other.qweight_strips)
-    assert torch.equal(ql(x), other(x))
+    assert torch.equal(ql.state_dict()["qweight"], other.state_dict()["qweight"])
+    other.prepare_decode(sw)
+    assert torch.equal(ql.qweight, other.qweight) and torch.equal(ql(x), other(x))
     ql.release_decode()
-    assert ql.qweight_strips is None and torch.equal(ql(x), ng.matmul_bias(x, ql._qw(), ql.bias))
+    assert ql.strip_cols == 0 and tuple(ql.qweight.shape) == (128, 448)
+    assert torch.equal(ql.qweight, other.state_dict()["qweight"])
+    assert torch.equal(ql(x), ng.matmul_bias(x, ql._qw(), ql.bias))
