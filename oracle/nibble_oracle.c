@@ -202,9 +202,70 @@ void nibble_oracle_dequantize(const uint32_t* packed, const uint16_t* scales, in
 /* ------------------------------------------------------------------------- */
 
 /* Y fp16 [M, N] = f16( X_f32 @ W_f32 ), X fp16 [M, K], W fp16 [K, N] (the
- * dequantized weight).  Accumulation in binary32, k ascending. */
+ * dequantized weight).  Accumulation in binary32, k ascending: every output
+ * is acc = acc + x[k] * w[k] (a rounded product, then a rounded sum; this
+ * file is built with -ffp-contract=off) for k = 0 .. K - 1.
+ *
+ * As the reference converts the whole weight to binary32 once
+ * (dequantize(qw).float()), so does this: W and X are widened first, then
+ * blocks of 8 rows x 256 columns accumulate together (the per-output order
+ * is unchanged, so is every bit).  Below 4 rows widening the whole weight
+ * costs more than it saves: the rows are done one by one. */
+static void matmul_f32_rows(const uint16_t* X, const uint16_t* W, int64_t M, int64_t K, int64_t N,
+                            uint16_t* Y, float* Yf32);
+
 void nibble_oracle_matmul_f32(const uint16_t* X, const uint16_t* W, int64_t M, int64_t K, int64_t N,
                               uint16_t* Y, float* Yf32) {
+  enum { MB = 8, NB = 256 };
+  if (M < 4) {
+    matmul_f32_rows(X, W, M, K, N, Y, Yf32);
+    return;
+  }
+  float* w32 = (float*)malloc((size_t)(K * N > 0 ? K * N : 1) * sizeof(float));
+  float* x32 = (float*)malloc((size_t)(M * K > 0 ? M * K : 1) * sizeof(float));
+  if (w32 == NULL || x32 == NULL) {
+    free(w32);
+    free(x32);
+    matmul_f32_rows(X, W, M, K, N, Y, Yf32);
+    return;
+  }
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < K * N; ++i) w32[i] = nibble_oracle_f16_to_f32(W[i]);
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < M * K; ++i) x32[i] = nibble_oracle_f16_to_f32(X[i]);
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int64_t mb = 0; mb < M; mb += MB) {
+    for (int64_t nb = 0; nb < N; nb += NB) {
+      float acc[MB][NB];
+      const int64_t rows = (mb + MB < M) ? MB : M - mb;
+      const int64_t cols = (nb + NB < N) ? NB : N - nb;
+      for (int64_t r = 0; r < rows; ++r)
+        for (int64_t c = 0; c < cols; ++c) acc[r][c] = 0.0f;
+      for (int64_t k = 0; k < K; ++k) {
+        const float* wrow = w32 + k * N + nb;
+        for (int64_t r = 0; r < rows; ++r) {
+          const float x = x32[(mb + r) * K + k];
+          float* a = acc[r];
+#pragma omp simd
+          for (int64_t c = 0; c < cols; ++c) a[c] = a[c] + x * wrow[c];
+        }
+      }
+      for (int64_t r = 0; r < rows; ++r)
+        for (int64_t c = 0; c < cols; ++c) {
+          const int64_t o = (mb + r) * N + nb + c;
+          if (Yf32) Yf32[o] = acc[r][c];
+          Y[o] = nibble_oracle_f32_to_f16(acc[r][c]);
+        }
+    }
+  }
+  free(w32);
+  free(x32);
+}
+
+/* The same product without the widened copies (used when they cannot be
+ * allocated): one row at a time, each weight widened as it is read. */
+static void matmul_f32_rows(const uint16_t* X, const uint16_t* W, int64_t M, int64_t K, int64_t N,
+                            uint16_t* Y, float* Yf32) {
   const int64_t NB = 256;
 #pragma omp parallel for collapse(2) schedule(static)
   for (int64_t m = 0; m < M; ++m) {
