@@ -21,15 +21,14 @@ output, multiplied in fp32): max |y - ref| <= 1e-2 * rms(ref), or the sweep
 stops.
 
 One JSON object per line on stdout; ``--markdown`` adds a table on stderr.
+The reference's CPU path at these shapes is timed by ``bench.py``'s
+``cpu_baseline.per_shape`` (the C oracle on all of the job's cores).
 """
 from __future__ import annotations
 
 import argparse
 import json
-import os
-import statistics
 import sys
-import time
 
 import torch
 
@@ -75,50 +74,11 @@ def _clock(t: "H.Timing") -> dict:
     return {"clock_mhz": c.get("clock_mean_mhz"), "throttled": c.get("throttled")}
 
 
-def _host_median_ms(fn, reps: int) -> float:
-    fn()  # warm-up
-    samples = []
-    for _ in range(reps):
-        t0 = time.perf_counter()
-        fn()
-        samples.append((time.perf_counter() - t0) * 1e3)
-    return statistics.median(samples)
-
-
-def cpu_facts() -> dict:
-    """Threads the host leg uses and what it runs on."""
-    model = "unknown"
-    try:
-        with open("/proc/cpuinfo") as fh:
-            model = next((ln.split(":", 1)[1].strip() for ln in fh if ln.startswith("model name")),
-                         model)
-    except OSError:
-        pass
-    # The host dequantize is numpy elementwise work (one thread); the fp32
-    # matmul is torch's (its intra-op thread count).
-    return {"cpu_dequant_threads": 1, "cpu_matmul_threads": torch.get_num_threads(),
-            "host_cpu_count": os.cpu_count(), "cpu_model": model}
-
-
-def cpu_reference_ms(qw: QuantizedWeight, X: torch.Tensor, reps: int = 5) -> dict:
-    """The reference's CPU path on this host (python/nibblegemm/quant.py:199-215,
-    in this package's restatement): ``dequantize`` (unpack, scale, fp16), then
-    the fp32 matmul rounded to fp16; median of ``reps`` after one warm-up,
-    each half separately."""
-    qw_cpu = qw.to("cpu")
-    x = X.cpu()
-    dq = _host_median_ms(lambda: quant.dequantize(qw_cpu), reps)
-    W = quant.dequantize(qw_cpu).float()
-    mm = _host_median_ms(lambda: (x.float() @ W).to(torch.float16), reps)
-    return {"cpu_dequant_ms": round(dq, 2), "cpu_matmul_ms": round(mm, 2),
-            "cpu_ms": round(dq + mm, 2)}
-
-
 def decode(args, rows):
     copy = H.measured_copy_gbps()
     read = H.measured_read_gbps()["read_gbps"]
-    print(json.dumps({"bench": "decode-setup", "copy_gbps": round(copy, 1), "read_gbps": read,
-                      **cpu_facts()}), flush=True)
+    print(json.dumps({"bench": "decode-setup", "copy_gbps": round(copy, 1), "read_gbps": read}),
+          flush=True)
     for K, N in DECODE_SHAPES:
         qws, gen = _weights(K, N, args.group_size, seed=K + N)
         w16 = _fp16_baseline(qws[0])
@@ -146,9 +106,6 @@ def decode(args, rows):
                    "strip_major_%8TB/s": round(100 * H.achieved_gbps(nb, ts.median_ms)
                                                / H.HBM_PEAK_GBPS, 1),
                    "strip_major_err_rms": float(f"{sm_err:.2e}")}
-            if not args.no_cpu:
-                row.update(cpu_reference_ms(qws[0], X))
-                row["vs_cpu"] = round(row["cpu_ms"] / (t.median_ms), 0)
             _emit(rows, row)
         del qws, w16, sms
         torch.cuda.empty_cache()
@@ -188,8 +145,7 @@ def prefill(args, rows):
 
 def dequant(args, rows):
     copy = H.measured_copy_gbps()
-    print(json.dumps({"bench": "dequant-setup", "copy_gbps": round(copy, 1), **cpu_facts()}),
-          flush=True)
+    print(json.dumps({"bench": "dequant-setup", "copy_gbps": round(copy, 1)}), flush=True)
     for K, N in DECODE_SHAPES:
         qws, _ = _weights(K, N, args.group_size, seed=K + N)
         qw_cpu = qws[0].to("cpu")
@@ -204,9 +160,6 @@ def dequant(args, rows):
                "us": round(t.median_ms * 1e3, 2), "GB/s": round(gbps),
                "%8TB/s": round(100 * gbps / H.HBM_PEAK_GBPS, 1),
                "%copy": round(100 * gbps / copy, 1), **_clock(t)}
-        if not args.no_cpu:
-            row["cpu_dequant_ms"] = round(_host_median_ms(lambda: quant.dequantize(qw_cpu), 5), 2)
-            row["vs_cpu"] = round(row["cpu_dequant_ms"] / t.median_ms, 0)
         _emit(rows, row)
         del qws
         torch.cuda.empty_cache()
@@ -347,8 +300,6 @@ def main(argv=None) -> int:
     ap.add_argument("--group-size", type=int, default=128)
     ap.add_argument("--trials", type=int, default=10)
     ap.add_argument("--markdown", action="store_true")
-    ap.add_argument("--no-cpu", action="store_true",
-                    help="skip the host (CPU) timing of the reference path in decode / dequant")
     args = ap.parse_args(argv)
     if not torch.cuda.is_available():
         print("bench_shapes needs a GPU", file=sys.stderr)

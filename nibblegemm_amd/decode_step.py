@@ -40,7 +40,10 @@ launch), so a layer is 5 launches.  This is the per-token forward of
 the reference's model decode (bench/bench_model.py:177-188) without the
 embedding lookup and the fp16 lm_head, which are not W4A16.
 
-``persistent`` runs the fused strip-major step as ONE launch: a
+``persistent_projections`` runs the reference's step itself -- the 224
+separate projections on strip-major weights, each reading its fixed
+activation -- as ONE launch; ``persistent`` runs the fused strip-major step
+the same way: a
 :class:`~nibblegemm_amd.chain.DecodeChain` of the 128 projections, each still
 reading its fixed activation (the reference's semantics), whose workgroups
 stream weights across projection boundaries; the outputs are bit-identical to
@@ -405,8 +408,32 @@ def _same(a: List[torch.Tensor], b: List[torch.Tensor]) -> bool:
         for x, y in zip(a, b))
 
 
+def stage_times(chain: DecodeChain, names: List[str], runs: int = 5) -> dict:
+    """Where a chain's time goes, from the kernel's own timestamps: per
+    projection name (the layer's stages in order), the median over ``runs``
+    of the mean over layers of the time from the end of the stage before it
+    to its own end, in us (its effective time in the step), and the step's
+    total.  Eager runs after a warm-up."""
+    chain.run()
+    chain.check()
+    per = {n: [] for n in names}
+    totals = []
+    for _ in range(runs):
+        t = chain.new_timestamps()
+        chain.run(t)
+        chain.check()
+        ends = DecodeChain.stage_times_us(t)
+        deltas = [ends[0]] + [b - a for a, b in zip(ends, ends[1:])]
+        for j, n in enumerate(names):
+            d = deltas[j::len(names)]
+            per[n].append(sum(d) / len(d))
+        totals.append(max(ends))
+    med = lambda v: sorted(v)[len(v) // 2]  # noqa: E731
+    return {**{n: round(med(v), 2) for n, v in per.items()}, "total_us": round(med(totals), 1)}
+
+
 def measure_persistent(layers_sm: List[Dict[str, QuantizedWeight]], trials: int = 10,
-                       warmup: int = 3) -> dict:
+                       warmup: int = 3, with_stages: bool = False) -> dict:
     """The step of ``layers_sm`` (strip-major) as one chain launch with the
     reference's semantics, after checking its outputs against the
     per-projection launches bit for bit (raises otherwise)."""
@@ -419,12 +446,15 @@ def measure_persistent(layers_sm: List[Dict[str, QuantizedWeight]], trials: int 
     r = measure_step(step, step.nbytes, trials, warmup, stages=len(chain.stages),
                      workgroups=chain.workgroups, rounds=chain.rounds,
                      equals_per_projection_launches=True)
+    if with_stages:
+        r["stage_us"] = stage_times(chain, list(layers_sm[0]))
     chain.check()
     return r
 
 
 def measure_dataflow(layers_sm: List[Dict[str, QuantizedWeight]], trials: int = 10,
-                     warmup: int = 3, persistent: bool = True) -> Dict[str, dict]:
+                     warmup: int = 3, persistent: bool = True,
+                     with_stages: bool = False) -> Dict[str, dict]:
     """The layer data flow (:class:`DataflowStep`) one launch per projection,
     and (``persistent``) as one chain, after checking the chain's outputs
     against the launches' bit for bit (raises otherwise)."""
@@ -440,20 +470,22 @@ def measure_dataflow(layers_sm: List[Dict[str, QuantizedWeight]], trials: int = 
         out["persistent_dataflow"] = measure_step(
             step, nbytes, trials, warmup, stages=len(chain.stages), workgroups=chain.workgroups,
             rounds=chain.rounds, equals_per_projection_launches=True)
+        if with_stages:
+            out["persistent_dataflow"]["stage_us"] = stage_times(chain, list(layers_sm[0]))
         chain.check()
     return out
 
 
 VARIANTS = ("projections", "fused", "fused_swiglu", "glue", "projections_strips", "fused_strips",
-            "fused_swiglu_strips", "glue_strips", "persistent", "dataflow_strips",
-            "persistent_dataflow")
+            "fused_swiglu_strips", "glue_strips", "persistent_projections", "persistent",
+            "dataflow_strips", "persistent_dataflow")
 
 
 def run(n_layers: int = 32, group_size: int = 128, trials: int = 10, glue_pos: int = 1023,
-        variants=VARIANTS, tp: int = 1) -> dict:
+        variants=VARIANTS, tp: int = 1, with_stages: bool = False) -> dict:
     want = set(variants)
-    if tp > 1 and want & {"glue", "glue_strips"}:
-        raise ValueError("the glue variants run the full model only (tp = 1)")
+    if tp > 1 and want & {"glue", "glue_strips", "dataflow_strips", "persistent_dataflow"}:
+        raise ValueError("the glue and data-flow variants run the full model only (tp = 1)")
     layers = build_layers(n_layers, group_size=group_size, tp=tp)
     nbytes = weight_bytes(layers)
     share = "" if tp == 1 else f", one GPU's share of a {tp}-way tensor-parallel split"
@@ -463,8 +495,13 @@ def run(n_layers: int = 32, group_size: int = 128, trials: int = 10, glue_pos: i
            "roofline_tok_s": round(H.HBM_PEAK_GBPS * 1e9 / nbytes, 1)}
     if "projections" in want:
         res["projections"] = measure(layers, trials)
-    if "projections_strips" in want:
-        res["projections_strips"] = measure(strips(layers), trials)
+    if want & {"projections_strips", "persistent_projections"}:
+        ps = strips(layers)
+        if "projections_strips" in want:
+            res["projections_strips"] = measure(ps, trials)
+        if "persistent_projections" in want:
+            res["persistent_projections"] = measure_persistent(ps, trials, with_stages=with_stages)
+        del ps
     if want & {"fused", "fused_strips", "persistent"}:
         fused = [fuse(layer) for layer in layers]
         if "fused" in want:
@@ -474,7 +511,7 @@ def run(n_layers: int = 32, group_size: int = 128, trials: int = 10, glue_pos: i
             if "fused_strips" in want:
                 res["fused_strips"] = measure(fs, trials)
             if "persistent" in want:
-                res["persistent"] = measure_persistent(fs, trials)
+                res["persistent"] = measure_persistent(fs, trials, with_stages=with_stages)
             del fs
         del fused
     swiglu_want = {"fused_swiglu", "glue", "fused_swiglu_strips", "glue_strips",
@@ -495,7 +532,8 @@ def run(n_layers: int = 32, group_size: int = 128, trials: int = 10, glue_pos: i
                 res["glue_strips"] = measure_glue(swiglu_strips, glue_pos, trials)
             if want & {"dataflow_strips", "persistent_dataflow"}:
                 res.update(measure_dataflow(swiglu_strips, trials,
-                                            persistent="persistent_dataflow" in want))
+                                            persistent="persistent_dataflow" in want,
+                                            with_stages=with_stages))
     return res
 
 
@@ -511,8 +549,12 @@ def main(argv=None) -> int:
                     + " (default: all; with --tp > 1 all but the glue variants)")
     ap.add_argument("--tp", type=int, default=1,
                     help="time one GPU's share of a TP-way tensor-parallel split")
+    ap.add_argument("--stage-times", action="store_true",
+                    help="add each persistent chain's per-projection effective times "
+                         "(in-kernel timestamps)")
     args = ap.parse_args(argv)
-    default = VARIANTS if args.tp == 1 else tuple(v for v in VARIANTS if "glue" not in v)
+    default = VARIANTS if args.tp == 1 else tuple(
+        v for v in VARIANTS if "glue" not in v and "dataflow" not in v)
     variants = tuple(v for v in args.variants.split(",") if v) if args.variants else default
     if not set(variants) <= set(VARIANTS):
         ap.error(f"unknown variant in {args.variants!r}")
@@ -520,13 +562,13 @@ def main(argv=None) -> int:
         projection_shapes(tp=args.tp, group_size=args.group_size)
     except ValueError as e:
         ap.error(str(e))
-    if args.tp > 1 and {"glue", "glue_strips"} & set(variants):
-        ap.error("the glue variants run the full model only (tp = 1)")
+    if args.tp > 1 and {"glue", "glue_strips", "dataflow_strips", "persistent_dataflow"} & set(variants):
+        ap.error("the glue and data-flow variants run the full model only (tp = 1)")
     if not torch.cuda.is_available():
         print("decode_step needs a GPU", file=sys.stderr)
         return 1
     print(json.dumps(run(args.layers, args.group_size, args.trials, args.glue_pos, variants,
-                         args.tp)), flush=True)
+                         args.tp, args.stage_times)), flush=True)
     return 0
 
 

@@ -218,28 +218,42 @@ def _new_event() -> "torch.cuda.Event":
     return torch.cuda.Event(enable_timing=True)
 
 
+def _time_windows(issue: Callable[[], None], trials: int, per_window: int):
+    """``trials`` timed windows of ``issue()`` (``per_window`` calls each)
+    between two events on the current stream.  The device is idle when each
+    window opens (a synchronisation first), as for a host loop that waits
+    for each result -- the reference's protocol (bench/harness.py:103-186).
+    Returns (per-call ms of each window, clock summary)."""
+    mon = ClockMonitor().start()
+    out = []
+    for _ in range(trials):
+        first, last = _new_event(), _new_event()
+        torch.cuda.synchronize()
+        first.record()
+        issue()
+        last.record()
+        last.synchronize()
+        out.append(first.elapsed_time(last) / per_window)
+    return tuple(out), mon.stop()
+
+
 def bench(fn: Callable[[int], object], *, reps: int = 32, trials: int = 20,
           warmup: int = 5) -> Timing:
-    """Eager timing of ``fn(i)``.  Every window's event pair is recorded up
-    front on the current stream, the calls are issued back to back (their
-    index keeps counting across windows, so a rotation advances through all
-    of its copies), and one synchronisation at the end collects the windows:
-    no host round trip sits between windows."""
+    """Eager timing of ``fn(i)``: windows of ``reps`` calls issued back to
+    back.  The call index keeps counting across windows, so a rotation of
+    weight copies advances through all of them."""
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
-    marks = [(_new_event(), _new_event()) for _ in range(trials)]
-    mon = ClockMonitor().start()
-    call = 0
-    for first, last in marks:
-        first.record()
+    index = [0]
+
+    def window():
         for _ in range(reps):
-            fn(call)
-            call += 1
-        last.record()
-    torch.cuda.synchronize()
-    clocks = mon.stop()
-    return Timing(tuple(a.elapsed_time(b) / reps for a, b in marks), reps, clocks)
+            fn(index[0])
+            index[0] += 1
+
+    windows, clocks = _time_windows(window, trials, reps)
+    return Timing(windows, reps, clocks)
 
 
 class GraphRunner:
@@ -283,18 +297,10 @@ class GraphRunner:
         time.sleep(max(0.0, (n - 1) * per))
 
     def time(self, trials: int = 20, warm_s: float = 0.05) -> Timing:
-        """``trials`` windows of one replay each, back to back after
-        :meth:`warm` (one synchronisation at the end)."""
+        """``trials`` windows of one replay each, after :meth:`warm`."""
         self.warm(warm_s)
-        marks = [(_new_event(), _new_event()) for _ in range(trials)]
-        mon = ClockMonitor().start()
-        for first, last in marks:
-            first.record()
-            self.graph.replay()
-            last.record()
-        torch.cuda.synchronize()
-        clocks = mon.stop()
-        return Timing(tuple(a.elapsed_time(b) / self.reps for a, b in marks), self.reps, clocks)
+        windows, clocks = _time_windows(self.graph.replay, trials, self.reps)
+        return Timing(windows, self.reps, clocks)
 
     def time_window(self, min_ms: float = 20.0, warm_s: float = 0.25):
         """One timed window of whole replays lasting at least ``min_ms``.
@@ -336,17 +342,16 @@ def bench_graph_pair(fn_a: Callable[[int], object], fn_b: Callable[[int], object
     runners = (GraphRunner(fn_a, reps, warmup), GraphRunner(fn_b, reps, warmup))
     for r in runners:
         r.warm(0.025)
-    marks = [[(_new_event(), _new_event()) for _ in range(trials)] for _ in runners]
-    mon = ClockMonitor().start()
-    for t in range(trials):
-        for r, m in zip(runners, marks):
-            m[t][0].record()
-            r.graph.replay()
-            m[t][1].record()
-    torch.cuda.synchronize()
-    clocks = mon.stop()
-    return tuple(Timing(tuple(a.elapsed_time(b) / reps for a, b in m), reps, clocks)
-                 for m in marks)
+    # Alternate the two graphs window by window: the windows come out a, b,
+    # a, b, ... and are split back by position.
+    turn = [0]
+
+    def one():
+        runners[turn[0] % 2].graph.replay()
+        turn[0] += 1
+
+    windows, clocks = _time_windows(one, 2 * trials, reps)
+    return tuple(Timing(windows[k::2], reps, clocks) for k in (0, 1))
 
 
 def spin_up(seconds: float = 0.3) -> None:
