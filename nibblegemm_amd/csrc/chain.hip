@@ -78,11 +78,7 @@ constexpr int kPolicyNt = 2;              // buffer-load cache policy: non-tempo
 constexpr int kPolicySc1 = 16;            // agent-coherent (misses a stale L2 line)
 constexpr size_t kLdsMax = 160 * 1024;
 
-// s_waitcnt immediates (gfx9 encoding: vmcnt[3:0] and [15:14], expcnt[6:4],
-// lgkmcnt[11:8]); the counters not named are left at their maximum.
-constexpr int waitcnt_vm(int n) { return (n & 0xF) | ((n >> 4) << 14) | 0x70 | 0xF00; }
 constexpr int kWaitRingOldest = waitcnt_vm(kRing - 1);
-constexpr int kWaitLgkm0 = 0xC07F;
 
 // One stage as the kernel reads it (built and checked on the host).
 struct ChainStage {
@@ -140,21 +136,6 @@ using const_ptr = const T*;  // the host pass only parses the kernels
 template <typename T>
 __device__ __forceinline__ const_ptr<T> as_const(const T* p) {
   return (const_ptr<T>)(p);
-}
-
-// A workgroup barrier that orders LDS only: the arriving wave's own LDS
-// accesses are complete (lgkmcnt 0).  __syncthreads() would also wait for
-// every vector-memory access of the wave (vmcnt 0) -- on the compute waves,
-// the whole weight ring, twice a round.  LDS written by LDS-DMA is ordered by
-// explicit vmcnt waits instead: the staging wave waits for its copies before
-// it arrives, and a compute wave for its own ring slot before reading it.
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_sched_barrier(0);
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_sched_barrier(0);
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
 __device__ __forceinline__ f4_t mfma16c(h8_t a, h8_t b, f4_t c) {

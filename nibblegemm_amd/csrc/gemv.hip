@@ -480,6 +480,336 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_mfma_kernel(GemvArgs a) {
     __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// The staging wave's copy of one activation window: COPIES LDS-DMA loads of
+// 16 bytes a lane, load j landing at dst + 1 KiB j.  Lane unit j reads
+// activation k = k0 + dma_k[j] of the row at byte dma_row[j]; rows past M
+// (dma_row[j] == kOutOfRange) and k past K take the out-of-range offset: no
+// memory access.  (The resource is built here from X and its byte extent:
+// the host pass cannot take a buffer resource as a template function's
+// parameter.)
+template <int COPIES>
+__device__ __forceinline__ void copy_window(const void* X, uint32_t xbytes, unsigned char* dst,
+                                            uint32_t k0, uint32_t K, const uint32_t* dma_k,
+                                            const uint32_t* dma_row) {
+  using lds_ptr = __attribute__((address_space(3))) void*;
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(X, xbytes);
+#pragma unroll
+  for (int j = 0; j < COPIES; ++j) {
+    const uint32_t k = k0 + dma_k[j];
+    const uint32_t off = dma_row[j] == kOutOfRange || k >= K ? kOutOfRange : dma_row[j] + 2u * k;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr)(dst + j * 1024), 16, off, 0, 0, 0);
+  }
+}
+
+// Batch kernel: 17 to 32 activation rows (small batches through gemm).  The
+// split kernel's geometry -- one workgroup per 64-column strip and K split,
+// its 4 waves taking the split's quant groups round-robin -- and its
+// arithmetic: per group the same pre-scaled activations, correction MFMA,
+// decode and MFMA sequence, the same per-group scaling into fp32 totals, the
+// same wave and split reduction order.  A launch with the split kernel's
+// plan returns the split kernel's bits.
+//
+// What differs is where the activations come from.  The split kernel loads
+// a 16-byte activation chunk per lane per MFMA -- 2 x GROUP / 32 loads per
+// group beside GROUP / 32 weight loads, each touching 16 rows -- and holds
+// them in registers for the two groups in flight.  Here the 4 groups the
+// waves take in one step form one K window of the activations, which
+// STAGERS staging waves (waves 4..) copy once into an LDS ring slot by
+// LDS-DMA (1 KiB per instruction, whole rows; rows past M are not read); the
+// MFMA operands are ds_read_b128s, and the registers hold DEPTH steps of
+// weight loads.  The copies are the staging waves' only vector-memory
+// operations, so the compute waves' waits cover their own weight loads
+// alone (vmcnt completes in order: copies interleaved with the weight loads
+// would make every wait for a copy also wait for the older weight loads).
+//
+// Ring protocol, per step i (one workgroup barrier a step):
+//   barrier B(i) -- a staging wave arrives once its copies of step i have
+//     landed, the compute waves once they are done with step i - 1's slot;
+//   staging waves: their copies of step i + RING - 1 into step i - 1's slot
+//     (past the last step: out-of-range offsets), then wait until only their
+//     newest RING - 2 slots' copies are in flight (step i + 1's have landed);
+//   compute waves: step i from its slot and the weights loaded DEPTH steps
+//     ago, then the weight loads of step i + DEPTH (past the last step:
+//     out-of-range offsets, no memory access).
+// A slot row is the window's 4 x GROUP k; 16-byte unit u of row r is stored
+// at unit u ^ (r % 16), so the 16 rows a ds_read_b128 quarter-wave reads
+// fall in 16 different bank groups.  After the loop the ring holds the wave
+// totals.  Rows past M hold whatever the ring held: MFMA row m of the output
+// depends on activation row m alone, and those rows are never written.
+//
+// Moving the activations into a CU costs about as much per byte as the
+// weight stream, by either path (per-lane loads or LDS-DMA): measured with
+// the split kernel at 4096 x 14336, M = 32, the texture-address unit was
+// 64-78% busy, half of that stalled by the L1.  The copies here are whole
+// 1 KiB rows issued by STAGERS waves that do nothing else, so they flow
+// beside the weight loads instead of in the compute waves' own queues.
+template <int GROUP, int DEPTH, int RING, int STAGERS, bool STREAM>
+__global__ __launch_bounds__((4 + STAGERS) * 64) void gemv_batch_kernel(GemvArgs a) {
+  constexpr int MT = 32;
+  constexpr int kWaves = 4;
+  constexpr int THREADS = (kWaves + STAGERS) * 64;
+  constexpr int kWPolicy = STREAM ? 2 : 0;
+  constexpr int kPolicySc1 = 16;                  // agent-coherent: misses a stale L2 line
+  constexpr int CPG = GROUP / 32;
+  constexpr int TILES = MT / 16;
+  constexpr uint32_t UPR = kWaves * GROUP / 8;    // 16-byte units per slot row
+  constexpr uint32_t SLOT_BYTES = MT * UPR * 16;
+  constexpr int COPIES = MT * UPR / 64 / STAGERS;  // each staging wave's loads per slot
+  constexpr int WAIT_X = (RING - 2) * COPIES;
+  constexpr int QUADS = kStripCols / 4;
+  static_assert(UPR >= 16 && (MT * UPR) % (64 * STAGERS) == 0, "swizzle within a row, whole copies");
+  static_assert(RING >= 2 && WAIT_X <= 63, "vmcnt range");
+  static_assert(kWaves * MT * 16 * 16 <= RING * SLOT_BYTES, "the wave totals fit the ring");
+  extern __shared__ __attribute__((aligned(16))) unsigned char ring[];
+  __shared__ int s_last;
+
+  const uint32_t lane = threadIdx.x & 63u;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const bool stager = wave >= kWaves;
+  const int strip = blockIdx.x;
+  const int split = blockIdx.y;
+  const int m_base = blockIdx.z * MT;
+  const int mrows = min(MT, a.M - m_base);
+  const uint32_t K = static_cast<uint32_t>(a.K);
+  const uint32_t q = lane & 15u, kb = lane >> 4;
+  const int col = strip * kStripCols + 4 * static_cast<int>(q);
+  const bool col_ok = col < a.N;
+  const uint32_t row_bytes = a.L.w_row;
+
+  const int total_groups = a.K / GROUP;
+  const int gb = split * a.groups_per_split;
+  const int ge = min(gb + a.groups_per_split, total_groups);
+  const int steps = (ge - gb + kWaves - 1) / kWaves;
+
+  f4_t tot[TILES][4];
+#pragma unroll
+  for (int t = 0; t < TILES; ++t)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) tot[t][j] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+  if (stager) {
+    // Lane unit of copy j: slot row r, window unit u stored at u ^ (r % 16).
+    const uint32_t xbytes = static_cast<uint32_t>(a.M) * K * 2u;
+    uint32_t dma_k[COPIES], dma_row[COPIES];
+#pragma unroll
+    for (int j = 0; j < COPIES; ++j) {
+      const uint32_t e = static_cast<uint32_t>((wave - kWaves) * COPIES + j) * 64u + lane;
+      const uint32_t r = e / UPR, pos = e % UPR;
+      dma_k[j] = 8u * (pos ^ (r & 15u));
+      dma_row[j] = static_cast<int>(r) < mrows ? (static_cast<uint32_t>(m_base) + r) * K * 2u
+                                               : kOutOfRange;
+    }
+    auto copy = [&](int step, uint32_t slot) {
+      copy_window<COPIES>(a.X, xbytes, ring + slot * SLOT_BYTES + (wave - kWaves) * COPIES * 1024,
+                          static_cast<uint32_t>(gb + step * kWaves) * GROUP, K, dma_k, dma_row);
+    };
+#pragma unroll
+    for (int s = 0; s < RING - 1; ++s) copy(s, s);
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(WAIT_X));
+    uint32_t slot = 0;
+    for (int i = 0; i < steps; ++i) {
+      lds_barrier();  // B(i)
+      copy(i + RING - 1, slot == 0 ? RING - 1 : slot - 1);
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(WAIT_X));
+      slot = slot == RING - 1 ? 0 : slot + 1;
+    }
+    // Every copy (including those past the last step) has landed before the
+    // ring is reused for the totals.
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+  } else {
+    const __amdgpu_buffer_rsrc_t rw =
+        make_rsrc(a.Wq, static_cast<uint32_t>(a.K / 8) * static_cast<uint32_t>(a.N) * 4u);
+    const __amdgpu_buffer_rsrc_t rs =
+        make_rsrc(a.S, static_cast<uint32_t>(a.K / GROUP) * static_cast<uint32_t>(a.N) * 2u);
+    const uint32_t voff_w = col_ok ? kb * row_bytes + a.L.wcol(col) : kOutOfRange;
+    const uint32_t voff_s = col_ok ? a.L.scol(col) : kOutOfRange;
+    struct WStage {
+      u4_t w[CPG];
+      h4_t s;
+    };
+    auto load = [&](WStage& st, int step) {
+      const int g = gb + step * kWaves + wave;
+      const bool in = step < steps && g < ge;
+      const uint32_t vw = in ? voff_w : kOutOfRange;
+      const uint32_t kw = in ? static_cast<uint32_t>(g) * (GROUP / 8) * row_bytes : 0u;
+#pragma unroll
+      for (int c = 0; c < CPG; ++c)
+        st.w[c] = __builtin_bit_cast(
+            u4_t, __builtin_amdgcn_raw_buffer_load_b128(rw, vw, kw + c * 4 * row_bytes, kWPolicy));
+      st.s = __builtin_bit_cast(
+          h4_t, __builtin_amdgcn_raw_buffer_load_b64(rs, in ? voff_s : kOutOfRange,
+                                                     in ? static_cast<uint32_t>(g) * a.L.s_row : 0u,
+                                                     kWPolicy));
+    };
+    const DecodeConsts dk = decode_consts();
+    const h8_t xscale = biased_x_scale();
+    const h8_t bcorr = biased_correction();
+    // gemv_mfma_kernel's compute, the activations read from the slot.
+    auto compute = [&](const WStage& st, const unsigned char* base) {
+      h8_t xs[TILES][CPG];
+      f4_t acc[TILES][4];
+#pragma unroll
+      for (int t = 0; t < TILES; ++t) {
+        const uint32_t r = 16u * t + q;
+        f4_t corr = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int c = 0; c < CPG; ++c) {
+          const uint32_t u = static_cast<uint32_t>(wave * (GROUP / 8) + 4 * c) + kb;
+          xs[t][c] = *reinterpret_cast<const h8_t*>(base + (r * UPR + (u ^ q)) * 16u) * xscale;
+          corr = mfma16(xs[t][c], bcorr, corr);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[t][j] = corr;
+      }
+#pragma unroll
+      for (int c = 0; c < CPG; ++c)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const h8_t b = decode8_biased(st.w[c][j], dk);
+#pragma unroll
+          for (int t = 0; t < TILES; ++t) acc[t][j] = mfma16(xs[t][c], b, acc[t][j]);
+        }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float sj = static_cast<float>(st.s[j]);
+#pragma unroll
+        for (int t = 0; t < TILES; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) tot[t][j][i] = __builtin_fmaf(sj, acc[t][j][i], tot[t][j][i]);
+      }
+    };
+
+    WStage st[DEPTH];
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      load(st[d], d);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    uint32_t slot = 0;  // step i's slot: i % RING
+    auto step = [&](WStage& sd, int i) {
+      lds_barrier();  // B(i)
+      if (gb + i * kWaves + wave < ge) compute(sd, ring + slot * SLOT_BYTES);
+      __builtin_amdgcn_sched_barrier(0);
+      load(sd, i + DEPTH);
+      slot = slot == RING - 1 ? 0 : slot + 1;
+    };
+    // Whole blocks of DEPTH steps, then the rest: a loop whose body could
+    // leave early would reach its head with stage 0's loads possibly the
+    // newest, and the compiler would then drain every load there.
+    int i0 = 0;
+    for (; i0 + DEPTH <= steps; i0 += DEPTH) {
+#pragma unroll
+      for (int d = 0; d < DEPTH; ++d) step(st[d], i0 + d);
+    }
+#pragma unroll
+    for (int d = 0; d < DEPTH - 1; ++d)
+      if (i0 + d < steps) step(st[d], i0 + d);
+  }
+  lds_barrier();  // every copy has landed and every slot read is done
+
+  // Lane (q, kb) of compute wave w holds rows 16 t + 4 kb + i of columns
+  // 4 q + j: red[w][row][q], summed over the waves in order.
+  f4_t* const red = reinterpret_cast<f4_t*>(ring);
+  if (!stager) {
+#pragma unroll
+    for (int t = 0; t < TILES; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 16 * t + 4 * static_cast<int>(kb) + i;
+        red[(wave * MT + r) * 16 + q] = f4_t{tot[t][0][i], tot[t][1][i], tot[t][2][i], tot[t][3][i]};
+      }
+  }
+  __syncthreads();
+  auto wave_sum = [&](int r, int qq) {
+    f4_t v[kWaves];
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) v[w] = red[(w * MT + r) * 16 + qq];
+    __builtin_amdgcn_sched_barrier(0);
+    f4_t sum = v[0];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) {
+      sum[0] += v[w][0];
+      sum[1] += v[w][1];
+      sum[2] += v[w][2];
+      sum[3] += v[w][3];
+    }
+    return sum;
+  };
+  if (a.splits == 1) {
+    emit_outputs<MT, THREADS>(a, strip, m_base, mrows, wave_sum);
+    return;
+  }
+  // The split kernel's publication and last-workgroup reduction ("HARDWARE
+  // ASSUMPTION" in nibble_decode.h), with 16-byte agent-coherent accesses;
+  // the last workgroup issues every split's loads before the first add.
+  const uint32_t pbytes = static_cast<uint32_t>(a.splits) * static_cast<uint32_t>(a.M) *
+                          static_cast<uint32_t>(a.N) * 4u;
+  const __amdgpu_buffer_rsrc_t rp = make_rsrc(a.partial, pbytes);
+  auto poff = [&](int sp, int r, int qq) {
+    return ((static_cast<uint32_t>(sp) * a.M + m_base + r) * static_cast<uint32_t>(a.N) +
+            strip * kStripCols + 4 * qq) * 4u;
+  };
+  for (int e = threadIdx.x; e < MT * QUADS; e += THREADS) {
+    const int r = e / QUADS, qq = e % QUADS;
+    if (r >= mrows || strip * kStripCols + 4 * qq >= a.N) continue;
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4_t, wave_sum(r, qq)), rp,
+                                           poff(split, r, qq), 0, kPolicySc1);
+  }
+  wait_vm_stores();
+  __syncthreads();
+  uint32_t* counter = a.counters + blockIdx.z * gridDim.x + strip;
+  if (threadIdx.x == 0) {
+    const uint32_t prev =
+        __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = (prev == static_cast<uint32_t>(a.splits - 1));
+  }
+  __syncthreads();
+  if (!s_last) return;
+  constexpr int PER = (MT * QUADS + THREADS - 1) / THREADS;
+  constexpr int kSplitBatch = 8;
+  f4_t* const sums = red;  // [MT][QUADS]
+  f4_t acc[PER];
+#pragma unroll
+  for (int k = 0; k < PER; ++k) acc[k] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int sp0 = 0; sp0 < a.splits; sp0 += kSplitBatch) {
+    f4_t v[PER][kSplitBatch];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const int e = threadIdx.x + k * THREADS;
+      const int r = e / QUADS, qq = e % QUADS;
+      const bool ok = e < MT * QUADS && r < mrows && strip * kStripCols + 4 * qq < a.N;
+#pragma unroll
+      for (int b = 0; b < kSplitBatch; ++b)
+        v[k][b] = __builtin_bit_cast(
+            f4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                      rp, ok && sp0 + b < a.splits ? poff(sp0 + b, r, qq) : kOutOfRange, 0,
+                      kPolicySc1));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < PER; ++k)
+#pragma unroll
+      for (int b = 0; b < kSplitBatch; ++b)
+        if (sp0 + b < a.splits) {
+          acc[k][0] += v[k][b][0];
+          acc[k][1] += v[k][b][1];
+          acc[k][2] += v[k][b][2];
+          acc[k][3] += v[k][b][3];
+        }
+  }
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int e = threadIdx.x + k * THREADS;
+    if (e < MT * QUADS) sums[e] = acc[k];
+  }
+  __syncthreads();
+  emit_outputs<MT, THREADS>(a, strip, m_base, mrows,
+                            [&](int r, int qq) { return sums[r * QUADS + qq]; });
+  if (threadIdx.x == 0)
+    __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Column-strip decode kernel (M <= 8, one launch, no cross-workgroup
 // exchange).  A workgroup owns SW columns (16, 32 or 64) over the whole of K;
 // its WAVES waves take contiguous ranges of quant groups, and every wave
@@ -859,6 +1189,22 @@ int mt_for(int64_t M) {
 int max_waves_for(int mt) { return std::min(16, 256 / mt); }
 
 constexpr int kDefaultWaves = 4;
+// Batch kernel geometry: weight loads of 2 steps in flight per wave, 3 LDS
+// activation slots (96 KiB at GROUP = 128), 4 staging waves.  Measured on
+// MI355X, M = 17..32, graph replay, against the same kernel with 1 / 2 / 8
+// staging waves (32 / 16 / 4 copies each per slot): 14336 x 4096 M = 32
+// 12.3 us against 15.8 / 14.4 / 15.5, 4096 x 4096 8.4 against 9.9 / 9.2 /
+// 9.1 -- one wave issuing the copies (an LDS-DMA load each, at most 63 in
+// flight) was the bound; 8 staging waves put two on a compute wave's SIMD.
+// 3 steps of weights were 1-6% slower than 2, 2 slots 5-10% slower than 3.
+// It serves every single block of 17..32 rows (kBatchWorkgroups: the grid a
+// plan aims for, one workgroup per CU of an MI355X; the plan is host
+// arithmetic, the same on any device).
+constexpr int kBatchDepth = 2;
+constexpr int kBatchRing = 3;
+constexpr int kBatchStagers = 4;
+constexpr int kBatchWorkgroups = 256;
+constexpr int kBatchMaxSplits = 8;
 // Quant groups per wave a split aims for.  Measured on MI355X at M = 1 and 4:
 // one split is best up to K = 32 * 128 (the cross-workgroup reduction costs
 // more than it spreads), and larger K is split so each wave streams about
@@ -994,6 +1340,23 @@ hipError_t launch_strip_group(const GemvArgs& a, const StreamPlan& p, hipStream_
   }
 }
 
+// The batch kernel: 4 compute waves and a staging wave, RING activation
+// slots of 32 rows x (4 x GROUP) k in dynamic LDS (96 KiB at GROUP = 128).
+template <int GROUP>
+hipError_t launch_batch_group(const GemvArgs& a, const StreamPlan& p, hipStream_t stream) {
+  if (p.mt != 32 || p.waves != 4 || p.depth != kBatchDepth || p.ring != kBatchRing)
+    return hipErrorInvalidValue;
+  constexpr size_t kLds = static_cast<size_t>(kBatchRing) * 32 * (4 * GROUP / 8) * 16;
+  static_assert(kLds + 256 <= 160 * 1024, "a workgroup holds at most 160 KiB of LDS");
+  const dim3 grid(p.strips, p.splits, p.mblocks);
+  constexpr int kThreads = (4 + kBatchStagers) * 64;
+  if (p.mblocks == 1)
+    gemv_batch_kernel<GROUP, kBatchDepth, kBatchRing, kBatchStagers, true><<<grid, kThreads, kLds, stream>>>(a);
+  else
+    gemv_batch_kernel<GROUP, kBatchDepth, kBatchRing, kBatchStagers, false><<<grid, kThreads, kLds, stream>>>(a);
+  return hipGetLastError();
+}
+
 // Split heuristic: whole K in one workgroup per 64-column strip unless a wave
 // would have to stream more than kGroupsPerWave groups, in which case K is
 // split evenly.  Overrides follow the reference: splits are floor-then-trimmed
@@ -1094,7 +1457,29 @@ int plan_stream(int64_t M, int64_t K, int64_t N, int64_t G, bool split_k, int64_
   if (split_k && splits_override == 0 && threads_override == 0 &&
       plan_strip(M, K, N, G, fusion, p))
     return NIBBLE_OK;
-  return plan_split_kernel(M, K, N, G, split_k, splits_override, threads_override, p);
+  const int rc = plan_split_kernel(M, K, N, G, split_k, splits_override, threads_override, p);
+  if (rc != NIBBLE_OK || !split_k || splits_override != 0 || threads_override != 0 ||
+      p->mt != 32 || p->mblocks != 1 || p->waves != 4)
+    return rc;
+  // 17..32 rows run the batch kernel (the split kernel's bits for the same
+  // plan), with K split further where the strips alone leave CUs idle (at
+  // most kBatchMaxSplits, at least 4 groups a split).  Measured on MI355X,
+  // graph replay, M = 17 / 32, against the split kernel's own plan: 4096 x
+  // 14336 10.8 / 11.1 us against 11.0 / 13.5; 14336 x 4096 11.9 / 12.3
+  // against 14.0 / 18.4; 4096 x 4096 (4 splits) 8.2 / 8.4 against 9.3 /
+  // 12.4; 4096 x 1024 (8 splits) 6.9 / 7.1 against 9.0 / 11.9.
+  const int groups = static_cast<int>(K / G);
+  const int fill = std::min({kBatchMaxSplits, kBatchWorkgroups / std::max(1, p->strips), groups / 4});
+  if (fill > p->splits) {
+    p->groups_per_split = static_cast<int>(ceil_div(groups, fill));
+    p->splits = static_cast<int>(ceil_div(groups, p->groups_per_split));
+    p->counter_bytes = align_up(static_cast<size_t>(p->strips) * p->mblocks * 4, 256);
+    p->workspace_bytes = p->counter_bytes + static_cast<size_t>(p->splits) * M * N * 4;
+  }
+  p->kernel = kBatchKernel;
+  p->depth = kBatchDepth;
+  p->ring = kBatchRing;
+  return rc;
 }
 
 // Strip width for strip-major weights (the layout fixes it, so it is chosen
@@ -1196,6 +1581,8 @@ int launch_stream_split(const void* X, const void* Wq, const void* S, void* Y, i
     a.strips_per_xcd = static_cast<int>(ceil_div(p.strips, 8));
     a.stage_x = p.stage_x ? 1 : 0;
     e = G == 128 ? launch_strip_group<128>(a, p, stream) : launch_strip_group<64>(a, p, stream);
+  } else if (p.kernel == kBatchKernel) {
+    e = G == 128 ? launch_batch_group<128>(a, p, stream) : launch_batch_group<64>(a, p, stream);
   } else {
     e = G == 128 ? launch_group<128>(a, p, stream) : launch_group<64>(a, p, stream);
   }
@@ -1406,26 +1793,34 @@ int validate_fused(const void* X, int64_t x_rows, int64_t x_cols, const void* Wq
 // The workspace a fused launch may need does not depend on its epilogue: the
 // query answers for the split kernel, the larger of the two plans (the strip
 // kernel needs none), so one buffer serves every epilogue and prologue.
+namespace {
+// The fused entry's workspace covers both streaming plans of these operands
+// (the split kernel's, and the heuristic plan the launch takes), so one
+// buffer serves every epilogue and prologue.
+bool fused_plan_bytes(int64_t M, int64_t K, int64_t N, int64_t G, size_t* ws, size_t* counters) {
+  StreamPlan a, b;
+  if (M < 1 || M > kStreamMaxM || K <= 0 || N <= 0 || (G != 64 && G != 128) || K % G != 0 ||
+      plan_split_kernel(M, K, N, G, true, 0, 0, &a) != NIBBLE_OK ||
+      plan_stream(M, K, N, G, true, 0, 0, &b) != NIBBLE_OK)
+    return false;
+  *ws = std::max(a.workspace_bytes, b.workspace_bytes);
+  *counters = std::max(a.counter_bytes, b.counter_bytes);
+  return true;
+}
+}  // namespace
+
 extern "C" size_t nibble_matmul_fused_workspace_bytes(int64_t M, int64_t K, int64_t N,
                                                       int64_t group_size, void* stream) {
   (void)stream;
-  StreamPlan p;
-  if (M < 1 || M > kStreamMaxM || K <= 0 || N <= 0 || (group_size != 64 && group_size != 128) ||
-      K % group_size != 0 ||
-      plan_split_kernel(M, K, N, group_size, true, 0, 0, &p) != NIBBLE_OK)
-    return 0;
-  return p.workspace_bytes;
+  size_t ws = 0, counters = 0;
+  return fused_plan_bytes(M, K, N, group_size, &ws, &counters) ? ws : 0;
 }
 
 extern "C" size_t nibble_matmul_fused_counter_bytes(int64_t M, int64_t K, int64_t N,
                                                     int64_t group_size, void* stream) {
   (void)stream;
-  StreamPlan p;
-  if (M < 1 || M > kStreamMaxM || K <= 0 || N <= 0 || (group_size != 64 && group_size != 128) ||
-      K % group_size != 0 ||
-      plan_split_kernel(M, K, N, group_size, true, 0, 0, &p) != NIBBLE_OK)
-    return 0;
-  return p.counter_bytes;
+  size_t ws = 0, counters = 0;
+  return fused_plan_bytes(M, K, N, group_size, &ws, &counters) ? counters : 0;
 }
 
 extern "C" int nibble_matmul_w4a16_fused(const void* X, int64_t x_rows, int64_t x_cols,

@@ -188,4 +188,25 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 // touching memory.
 constexpr uint32_t kOutOfRange = 0x80000000u;
 
+// s_waitcnt immediate that waits for all but the newest n vector-memory
+// operations of the wave (gfx9 encoding: vmcnt[3:0] and [15:14], expcnt[6:4],
+// lgkmcnt[11:8]; the counters not named are left at their maxima), and the
+// one that waits for every LDS / scalar-memory operation (lgkmcnt 0).
+constexpr int waitcnt_vm(int n) { return (n & 0xF) | ((n >> 4) << 14) | 0x70 | 0xF00; }
+constexpr int kWaitLgkm0 = 0xC07F;
+
+// A workgroup barrier that orders LDS only: each arriving wave's own LDS
+// accesses are complete (lgkmcnt 0).  __syncthreads() would also wait for
+// every vector-memory access of the wave (vmcnt 0), draining whatever weight
+// loads it keeps in flight.  LDS written by LDS-DMA is ordered by explicit
+// vmcnt waits before the barrier instead.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 }  // namespace nibble

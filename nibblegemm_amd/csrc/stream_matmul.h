@@ -65,8 +65,13 @@ inline WeightLayout layout_for(int64_t K, int64_t N, int64_t G, int64_t strip_co
 // kStripKernel (M <= 8): `strip_cols`-column strips over the whole of K,
 // `waves` waves per workgroup on contiguous group ranges with `depth` groups
 // of loads in flight per wave; no workspace.
+// kBatchKernel (one block of 17..32 rows, K split): the split kernel's
+// geometry and arithmetic (so its bits), with each step's activation window
+// copied once into an LDS ring and `depth` steps of weight loads in flight
+// per wave.
 constexpr int kSplitKernel = 0;
 constexpr int kStripKernel = 1;
+constexpr int kBatchKernel = 2;
 
 // Launch geometry.  The split-K workspace (split kernel, splits > 1) is
 // `counter_bytes` of uint32 counters, one per (row block, strip), zero on
@@ -81,7 +86,8 @@ struct StreamPlan {
   int splits = 1;  // K splits (grid.y)
   int groups_per_split = 0;
   int strip_cols = 64;  // strip kernel: 16, 32 or 64
-  int depth = 2;        // strip kernel: groups in flight per wave
+  int depth = 2;        // strip / batch kernel: groups (steps) of weight loads in flight per wave
+  int ring = 3;         // batch kernel: LDS activation slots
   bool stage_x = true;  // strip kernel: activations copied to LDS (when they fit 64 KiB)
   size_t counter_bytes = 0;
   size_t workspace_bytes = 0;

@@ -3,7 +3,7 @@
 Both epilogues are defined as the unfused fp16 ops they replace, so the test
 is bit equality with those ops run separately on the GPU:
   * bias:   matmul(X, W) + bias               (the reference QuantLinear, ops.py:131-135)
-  * swiglu: silu(X W_gate) * (X W_up)         (the fp16 torch composition)
+  * swiglu: silu(G) * U, G | U the halves of X [W_gate | W_up]  (the fp16 torch composition)
 and, for SwiGLU, the north-star tolerance against an fp32 evaluation of the
 same MLP input from the oracle's products.
 """
@@ -21,7 +21,7 @@ pytestmark = pytest.mark.gpu
 
 SHAPES = [(1, 4096, 1024, 128), (4, 512, 260, 64), (8, 14336, 512, 128), (16, 1024, 4100, 128),
           (12, 4096, 14336, 128), (100, 2048, 640, 64), (128, 8192, 384, 128),
-          (64, 14336, 4096, 128)]
+          (64, 14336, 4096, 128), (17, 14336, 4096, 128), (24, 4096, 1028, 64), (32, 4096, 14336, 128)]
 
 
 @pytest.mark.parametrize("M,K,N,g", SHAPES)
@@ -35,7 +35,7 @@ def test_bias_epilogue_is_the_separate_add(M, K, N, g):
 
 
 SWIGLU = [(1, 4096, 1024, 128), (8, 14336, 512, 128), (16, 4096, 14336, 128), (33, 1024, 320, 64),
-          (128, 2048, 96, 128), (48, 4096, 14336, 128)]
+          (128, 2048, 96, 128), (48, 4096, 14336, 128), (24, 4096, 4096, 128), (32, 2048, 640, 64)]
 
 
 @pytest.mark.parametrize("M,K,Nh,g", SWIGLU)
@@ -45,15 +45,16 @@ def test_swiglu_epilogue_is_the_fp16_composition(M, K, Nh, g):
     qw = ng.interleave_swiglu(gate, up)
     fused = ng.matmul_swiglu(Xd, qw)
     assert fused.shape == (M, Nh)
-    if ng.extension().gemm_streams(M, K, 2 * Nh, g):
+    # The fused output is the fp16 SwiGLU of the gate|up product's halves.
+    yg, yu = split_swiglu(ng.matmul(Xd, qw))
+    assert torch.equal(fused, torch.nn.functional.silu(yg) * yu)
+    if M <= 16 and ng.extension().gemm_streams(M, K, 2 * Nh, g):
+        # Up to 16 rows the streaming plan splits K by K alone, so the gate
+        # and up products on their own sum in the same order.  (Larger
+        # batches split K by the strip or tile count too: there the
+        # products of N / 2 columns may sum in another order.)
         composed = torch.nn.functional.silu(ng.matmul(Xd, gate)) * ng.matmul(Xd, up)
-    else:
-        # large-weight batches take tiles split over K by the tile count, so
-        # the gate|up product sums in another order than the gate and up
-        # products alone: the bits are those of composing the one product
-        yg, yu = split_swiglu(ng.matmul(Xd, qw))
-        composed = torch.nn.functional.silu(yg) * yu
-    assert torch.equal(fused, composed)
+        assert torch.equal(fused, composed)
     # against fp32 arithmetic on the oracle's products of the same inputs:
     # 1e-2 of the RMS, plus, per element, the fp16 rounding of its own value
     # (the product's heavy tail puts its largest outputs ~30 RMS out, where
