@@ -501,13 +501,14 @@ __device__ __forceinline__ void copy_window(const void* X, uint32_t xbytes, unsi
   }
 }
 
-// Batch kernel: 17 to 32 activation rows (small batches through gemm).  The
-// split kernel's geometry -- one workgroup per 64-column strip and K split,
-// its 4 waves taking the split's quant groups round-robin -- and its
-// arithmetic: per group the same pre-scaled activations, correction MFMA,
-// decode and MFMA sequence, the same per-group scaling into fp32 totals, the
-// same wave and split reduction order.  A launch with the split kernel's
-// plan returns the split kernel's bits.
+// Batch kernel: 12 to 32 activation rows (small batches through gemm) in one
+// block of MT = 16 or 32 rows.  The split kernel's geometry -- one workgroup
+// per 64-column strip and K split, its 4 waves taking the split's quant
+// groups round-robin -- and its arithmetic: per group the same pre-scaled
+// activations, correction MFMA, decode and MFMA sequence, the same
+// per-group scaling into fp32 totals, the same wave and split reduction
+// order.  A launch with the split kernel's plan returns the split kernel's
+// bits.
 //
 // What differs is where the activations come from.  The split kernel loads
 // a 16-byte activation chunk per lane per MFMA -- 2 x GROUP / 32 loads per
@@ -543,9 +544,9 @@ __device__ __forceinline__ void copy_window(const void* X, uint32_t xbytes, unsi
 // 64-78% busy, half of that stalled by the L1.  The copies here are whole
 // 1 KiB rows issued by STAGERS waves that do nothing else, so they flow
 // beside the weight loads instead of in the compute waves' own queues.
-template <int GROUP, int DEPTH, int RING, int STAGERS, bool STREAM>
+template <int MT, int GROUP, int DEPTH, int RING, int STAGERS, bool STREAM>
 __global__ __launch_bounds__((4 + STAGERS) * 64) void gemv_batch_kernel(GemvArgs a) {
-  constexpr int MT = 32;
+  static_assert(MT == 16 || MT == 32, "16-row MFMA tiles");
   constexpr int kWaves = 4;
   constexpr int THREADS = (kWaves + STAGERS) * 64;
   constexpr int kWPolicy = STREAM ? 2 : 0;
@@ -1197,14 +1198,18 @@ constexpr int kDefaultWaves = 4;
 // 9.1 -- one wave issuing the copies (an LDS-DMA load each, at most 63 in
 // flight) was the bound; 8 staging waves put two on a compute wave's SIMD.
 // 3 steps of weights were 1-6% slower than 2, 2 slots 5-10% slower than 3.
-// It serves every single block of 17..32 rows (kBatchWorkgroups: the grid a
-// plan aims for, one workgroup per CU of an MI355X; the plan is host
-// arithmetic, the same on any device).
+// It serves single blocks of 12..32 rows outside the strip kernel's plans
+// (kBatchWorkgroups: the grid a plan aims for, one workgroup per CU of an
+// MI355X; the plan is host arithmetic, the same on any device).
 constexpr int kBatchDepth = 2;
 constexpr int kBatchRing = 3;
 constexpr int kBatchStagers = 4;
 constexpr int kBatchWorkgroups = 256;
 constexpr int kBatchMaxSplits = 8;
+// 16-row blocks run the batch kernel from this many rows: at 9 rows the
+// split kernel, whose activation loads scale with the rows, is as fast or
+// faster (4096 x 4096 7.0 against 7.7 us, 14336 x 4096 10.4 against 10.5).
+constexpr int kBatchMinRows = 12;
 // Quant groups per wave a split aims for.  Measured on MI355X at M = 1 and 4:
 // one split is best up to K = 32 * 128 (the cross-workgroup reduction costs
 // more than it spreads), and larger K is split so each wave streams about
@@ -1342,19 +1347,27 @@ hipError_t launch_strip_group(const GemvArgs& a, const StreamPlan& p, hipStream_
 
 // The batch kernel: 4 compute waves and a staging wave, RING activation
 // slots of 32 rows x (4 x GROUP) k in dynamic LDS (96 KiB at GROUP = 128).
-template <int GROUP>
-hipError_t launch_batch_group(const GemvArgs& a, const StreamPlan& p, hipStream_t stream) {
-  if (p.mt != 32 || p.waves != 4 || p.depth != kBatchDepth || p.ring != kBatchRing)
-    return hipErrorInvalidValue;
-  constexpr size_t kLds = static_cast<size_t>(kBatchRing) * 32 * (4 * GROUP / 8) * 16;
+template <int MT, int GROUP>
+hipError_t launch_batch_rows(const GemvArgs& a, const StreamPlan& p, hipStream_t stream) {
+  constexpr size_t kLds = static_cast<size_t>(kBatchRing) * MT * (4 * GROUP / 8) * 16;
   static_assert(kLds + 256 <= 160 * 1024, "a workgroup holds at most 160 KiB of LDS");
   const dim3 grid(p.strips, p.splits, p.mblocks);
   constexpr int kThreads = (4 + kBatchStagers) * 64;
   if (p.mblocks == 1)
-    gemv_batch_kernel<GROUP, kBatchDepth, kBatchRing, kBatchStagers, true><<<grid, kThreads, kLds, stream>>>(a);
+    gemv_batch_kernel<MT, GROUP, kBatchDepth, kBatchRing, kBatchStagers, true><<<grid, kThreads, kLds, stream>>>(a);
   else
-    gemv_batch_kernel<GROUP, kBatchDepth, kBatchRing, kBatchStagers, false><<<grid, kThreads, kLds, stream>>>(a);
+    gemv_batch_kernel<MT, GROUP, kBatchDepth, kBatchRing, kBatchStagers, false><<<grid, kThreads, kLds, stream>>>(a);
   return hipGetLastError();
+}
+
+template <int GROUP>
+hipError_t launch_batch_group(const GemvArgs& a, const StreamPlan& p, hipStream_t stream) {
+  if (p.waves != 4 || p.depth != kBatchDepth || p.ring != kBatchRing) return hipErrorInvalidValue;
+  switch (p.mt) {
+    case 16: return launch_batch_rows<16, GROUP>(a, p, stream);
+    case 32: return launch_batch_rows<32, GROUP>(a, p, stream);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 // Split heuristic: whole K in one workgroup per 64-column strip unless a wave
@@ -1459,15 +1472,18 @@ int plan_stream(int64_t M, int64_t K, int64_t N, int64_t G, bool split_k, int64_
     return NIBBLE_OK;
   const int rc = plan_split_kernel(M, K, N, G, split_k, splits_override, threads_override, p);
   if (rc != NIBBLE_OK || !split_k || splits_override != 0 || threads_override != 0 ||
-      p->mt != 32 || p->mblocks != 1 || p->waves != 4)
+      p->mblocks != 1 || p->waves != 4 || !(p->mt == 32 || (p->mt == 16 && M >= kBatchMinRows)))
     return rc;
-  // 17..32 rows run the batch kernel (the split kernel's bits for the same
+  // 12..32 rows (those the strip kernel does not take) run the batch kernel
+  // in one block of 16 or 32 rows (the split kernel's bits for the same
   // plan), with K split further where the strips alone leave CUs idle (at
   // most kBatchMaxSplits, at least 4 groups a split).  Measured on MI355X,
-  // graph replay, M = 17 / 32, against the split kernel's own plan: 4096 x
+  // graph replay, against the split kernel's own plan: M = 17 / 32 4096 x
   // 14336 10.8 / 11.1 us against 11.0 / 13.5; 14336 x 4096 11.9 / 12.3
   // against 14.0 / 18.4; 4096 x 4096 (4 splits) 8.2 / 8.4 against 9.3 /
-  // 12.4; 4096 x 1024 (8 splits) 6.9 / 7.1 against 9.0 / 11.9.
+  // 12.4; 4096 x 1024 (8 splits) 6.9 / 7.1 against 9.0 / 11.9; M = 12 / 16
+  // 14336 x 4096 10.5 / 10.6 against 11.1 / 12.2, 8192 x 8192 10.7 / 10.8
+  // against 11.8 / 13.1.
   const int groups = static_cast<int>(K / G);
   const int fill = std::min({kBatchMaxSplits, kBatchWorkgroups / std::max(1, p->strips), groups / 4});
   if (fill > p->splits) {

@@ -65,10 +65,10 @@ inline WeightLayout layout_for(int64_t K, int64_t N, int64_t G, int64_t strip_co
 // kStripKernel (M <= 8): `strip_cols`-column strips over the whole of K,
 // `waves` waves per workgroup on contiguous group ranges with `depth` groups
 // of loads in flight per wave; no workspace.
-// kBatchKernel (one block of 17..32 rows, K split): the split kernel's
-// geometry and arithmetic (so its bits), with each step's activation window
-// copied once into an LDS ring and `depth` steps of weight loads in flight
-// per wave.
+// kBatchKernel (one block of 12..32 rows): the split kernel's geometry and
+// arithmetic (so its bits), with each step's activation window copied once
+// into an LDS ring by staging waves and `depth` steps of weight loads in
+// flight per wave.
 constexpr int kSplitKernel = 0;
 constexpr int kStripKernel = 1;
 constexpr int kBatchKernel = 2;

@@ -76,12 +76,13 @@ def test_small_batch_config_gemm_leg(M):
     assert rms_err(y, oracle_y(X, packed, scales, 4096, 128)) <= RMS_TOL
 
 
-@pytest.mark.parametrize("M", [17, 24, 32])
+@pytest.mark.parametrize("M", [12, 16, 17, 24, 32])
 @pytest.mark.parametrize("K_,N", [(4096, 14336), (14336, 4096)])
 def test_batch_rows_full_size(M, K_, N):
-    """17..32 rows (the batch kernel: each step's activation window copied
-    into an LDS ring by staging waves) at the small-batch config's full
-    sizes, every output against the oracle; repeated calls bit-identical."""
+    """12..32 rows at the small-batch config's full sizes (the batch kernel:
+    each step's activation window copied into an LDS ring by staging waves;
+    12 and 16 rows at 4096 x 14336 take the 16-row strip kernel), every
+    output against the oracle; repeated calls bit-identical."""
     X, packed, scales, Xd, qw = synthetic(M, K_, N, 128, seed=700 + M + K_)
     y = ng.gemm(Xd, qw)
     assert torch.equal(ng.gemm(Xd, qw), y)
@@ -91,11 +92,12 @@ def test_batch_rows_full_size(M, K_, N):
 
 
 @pytest.mark.parametrize("M,K_,N,g", [(24, 14336, 4096, 128), (17, 4096, 1024, 128), (32, 2048, 1540, 64),
-                                      (20, 640, 196, 64)])
+                                      (20, 640, 196, 64), (14, 14336, 1024, 128), (12, 1024, 260, 64)])
 def test_batch_rows_replay_in_a_graph(M, K_, N, g):
-    """The batch kernel with K split (4, 8, 8 and 2 ways; the last two end in a
-    partial strip): its counters are reset by the kernel, so a captured call
-    replays with every replay equal to the eager call, eager work between."""
+    """The batch kernel with K split (4, 8, 8, 2, 8 and 4 ways; 32- and
+    16-row blocks; three end in a partial strip): its counters are reset by
+    the kernel, so a captured call replays with every replay equal to the
+    eager call, eager work between."""
     X, packed, scales, Xd, qw = synthetic(M, K_, N, g, seed=13 + M)
     ext = ng.extension()
     assert ext.gemm_workspace_bytes(M, K_, N, g, 6, None)[1] > 0  # this plan splits K
