@@ -30,9 +30,10 @@ one ``nibblegemm_amd.gemv`` call (M=1) over one batch of synthetic inputs
   the reference's CPU path) on this host on a bounded sample, and its
   ``per_shape`` table the same path at every other shape the line reports
   (decode sweep, small batches, prefill, dequant) on all of the job's cores.
-* ``small_batch`` (configs[2]: M = 2..32 through ``matmul``) and ``dequant``
-  (the standalone kernel at the same shape, bit-exact first) are graph-timed
-  over the same kind of rotation.
+* ``small_batch`` (configs[2]: M = 2..32 through ``matmul`` at the headline
+  shape, and M = 16, 24, 32 at 14336 x 4096) and ``dequant`` (the standalone
+  kernel at the headline shape, bit-exact first) are graph-timed over the
+  same kind of rotation.
 
 Prints ONE JSON line.  Only ``--gpus 1`` is supported (one GPU per box).
 """
@@ -72,7 +73,8 @@ def _cpu_model() -> str:
 #: and the prefill points.
 CPU_SHAPES = ([(1, k, n) for k, n in ((4096, 14336), (14336, 4096), (8192, 8192), (4096, 4096),
                                       (4096, 1024), (4096, 6144))]
-              + [(m, 4096, 14336) for m in (2, 4, 8, 16, 32)]
+              + [(m, 4096, 14336) for m in (2, 4, 8, 16, 17, 24, 32)]
+              + [(m, 14336, 4096) for m in (16, 24, 32)]
               + [(m, k, n) for m in (128, 512, 2048) for k, n in ((4096, 14336), (14336, 4096))])
 #: Rows of X the CPU matmul is timed on at most (scaled by M / rows above it).
 CPU_MAX_ROWS = 32
@@ -274,16 +276,23 @@ def main() -> int:
 
         torch.cuda.empty_cache()
         t0 = time.perf_counter()
-        qws, gen = BS._weights(K, N, G, seed=K + N)
         small = []
-        for m in (2, 4, 8, 16, 32):
-            Xm = torch.randn((m, K), generator=gen).to(torch.float16).cuda()
-            err = BS._check(ng.matmul(Xm, qws[0]), Xm, qws[0], f"matmul {m}x{K}x{N}")
-            t = H.bench_graph(lambda i: ng.matmul(Xm, qws[i]), reps=32, trials=10)
-            nb = H.total_bytes(m, K, N, G, 4)
-            small.append({"M": m, "us": round(t.median_ms * 1e3, 2),
-                          "gbps": round(H.achieved_gbps(nb, t.median_ms), 1),
-                          "max_err_rms": float(f"{err:.2e}")})
+        # the headline shape, then the down projection's (K and N swapped)
+        for (Ks, Ns), ms in (((K, N), (2, 4, 8, 16, 17, 24, 32)), ((N, K), (16, 24, 32))):
+            qws, gen = BS._weights(Ks, Ns, G, seed=Ks + Ns)
+            for m in ms:
+                Xm = torch.randn((m, Ks), generator=gen).to(torch.float16).cuda()
+                err = BS._check(ng.matmul(Xm, qws[0]), Xm, qws[0], f"matmul {m}x{Ks}x{Ns}")
+                t = H.bench_graph(lambda i: ng.matmul(Xm, qws[i]), reps=32, trials=10)
+                nb = H.total_bytes(m, Ks, Ns, G, 4)
+                small.append({"M": m, "K": Ks, "N": Ns, "us": round(t.median_ms * 1e3, 2),
+                              "gbps": round(H.achieved_gbps(nb, t.median_ms), 1),
+                              "max_err_rms": float(f"{err:.2e}")})
+            if (Ks, Ns) == (K, N):
+                qws_head = qws
+            else:
+                del qws
+        qws = qws_head
         host = quant.dequantize(qws[0].to("cpu"))
         if not torch.equal(ng.dequant(qws[0]).cpu().view(torch.int16), host.view(torch.int16)):
             raise RuntimeError("dequant differs from the host dequantize")
@@ -293,7 +302,7 @@ def main() -> int:
         dequant = {"K": K, "N": N, "us": round(t.median_ms * 1e3, 2), "gbps": round(dq_gbps, 1),
                    "pct_hbm_peak": round(100 * dq_gbps / H.HBM_PEAK_GBPS, 2), "bit_exact": True}
         del qws
-        log("small batch (matmul): " + "; ".join(f"M={r['M']} {r['us']} us" for r in small)
+        log("small batch (matmul): " + "; ".join(f"{r['K']}x{r['N']} M={r['M']} {r['us']} us" for r in small)
             + f"; dequant {dequant['us']} us {dequant['gbps']} GB/s; "
             f"{time.perf_counter() - t0:.1f} s")
 

@@ -5,7 +5,7 @@ bench/launch_overhead.py and bench/autotune.py, at the benchmark shapes).
     python3 -m nibblegemm_amd.bench_shapes decode      # configs 1-3: M <= 8 GEMV
     python3 -m nibblegemm_amd.bench_shapes prefill     # configs 3-4: M = 16 .. 2048
     python3 -m nibblegemm_amd.bench_shapes dequant     # standalone dequant
-    python3 -m nibblegemm_amd.bench_shapes crossover   # gemv vs gemm over M
+    python3 -m nibblegemm_amd.bench_shapes crossover   # gemv vs gemm over M (--shape K N)
     python3 -m nibblegemm_amd.bench_shapes launch      # eager vs graph-replayed matmul
     python3 -m nibblegemm_amd.bench_shapes autotune    # gemv splits x block_threads
     python3 -m nibblegemm_amd.bench_shapes attention   # decode-step attention over cache length
@@ -166,7 +166,7 @@ def dequant(args, rows):
 
 
 def crossover(args, rows):
-    K, N = 4096, 14336
+    K, N = args.shape
     qws, gen = _weights(K, N, args.group_size, seed=7)
     w16 = _fp16_baseline(qws[0])
     for M in args.M or [1, 2, 4, 8, 9, 16, 24, 32, 33, 48, 64, 96, 128]:
@@ -297,6 +297,8 @@ def main(argv=None) -> int:
     ap.add_argument("--M", type=int, nargs="*", help="batch sizes (default: the benchmark shapes)")
     ap.add_argument("--pos", type=int, nargs="*", default=[0, 127, 128, 511, 1023, 2047, 4095],
                     help="attention: cache positions of the decoded token")
+    ap.add_argument("--shape", type=int, nargs=2, metavar=("K", "N"), default=[4096, 14336],
+                    help="crossover: the weight shape (default 4096 14336)")
     ap.add_argument("--group-size", type=int, default=128)
     ap.add_argument("--trials", type=int, default=10)
     ap.add_argument("--markdown", action="store_true")
