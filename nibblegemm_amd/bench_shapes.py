@@ -6,6 +6,7 @@ bench/launch_overhead.py and bench/autotune.py, at the benchmark shapes).
     python3 -m nibblegemm_amd.bench_shapes prefill     # configs 3-4: M = 16 .. 2048
     python3 -m nibblegemm_amd.bench_shapes dequant     # standalone dequant
     python3 -m nibblegemm_amd.bench_shapes crossover   # gemv vs gemm over M (--shape K N)
+    python3 -m nibblegemm_amd.bench_shapes strips      # what bounds one decode launch
     python3 -m nibblegemm_amd.bench_shapes launch      # eager vs graph-replayed matmul
     python3 -m nibblegemm_amd.bench_shapes autotune    # gemv splits x block_threads
     python3 -m nibblegemm_amd.bench_shapes attention   # decode-step attention over cache length
@@ -186,6 +187,46 @@ def crossover(args, rows):
         _emit(rows, row)
 
 
+def strips(args, rows):
+    """What bounds one decode launch: the M = 1 GEMV at K = 4096 over N (one
+    64-column strip per workgroup, one workgroup per CU up to 256 strips),
+    then the streaming-read probe over the headline's bytes at a range of
+    workgroup counts.  A time flat in the strip count means each CU streams
+    its strip at a per-CU rate, whatever the others do."""
+    K = 4096
+    for N in args.N or [12288, 13312, 14336, 15360, 16384, 18432]:
+        qws, gen = _weights(K, N, args.group_size, seed=K + N)
+        X = torch.randn((1, K), generator=gen).to(torch.float16).cuda()
+        _check(ops.gemv(X, qws[0]), X, qws[0], f"gemv 1x{K}x{N}")
+        t = H.bench_graph(lambda i: ops.gemv(X, qws[i]), reps=64, trials=args.trials)
+        nb = H.total_bytes(1, K, N, args.group_size, 4)
+        us = t.median_ms * 1e3
+        _emit(rows, {"bench": "strips", "what": "gemv M=1", "K": K, "N": N, "workgroups": N // 64,
+                     "us": round(us, 2), "GB/s": round(nb / us / 1e3),
+                     "GB/s per busy CU": round(nb / min(N // 64, 256) / us / 1e3, 2), **_clock(t)})
+        del qws
+        torch.cuda.empty_cache()
+    fn = H._read_probe_fn()
+    nb = H.total_bytes(1, 4096, 14336, args.group_size, 4)
+    stride = (nb + 4095) // 4096 * 4096
+    copies = (1 << 30) // stride + 4  # > 1 GiB in rotation: every read streams from HBM
+    buf = torch.ones(stride * copies // 4, dtype=torch.int32, device="cuda")
+    sink = torch.zeros(1 << 16, dtype=torch.int32, device="cuda")
+    for wgs in (224, 256, 512, 1024, 4096):
+        def run(i):
+            rc = fn(buf.data_ptr() + (i % copies) * stride, nb, wgs, sink.data_ptr(),
+                    torch.cuda.current_stream().cuda_stream)
+            if rc:
+                raise RuntimeError(f"read probe failed ({rc})")
+        t = H.bench_graph(run, reps=64, trials=args.trials)
+        us = t.median_ms * 1e3
+        _emit(rows, {"bench": "strips", "what": "read probe", "K": 4096, "N": 14336, "workgroups": wgs,
+                     "us": round(us, 2), "GB/s": round(nb / us / 1e3),
+                     "GB/s per busy CU": round(nb / min(wgs, 256) / us / 1e3, 2), **_clock(t)})
+    del buf, sink
+    torch.cuda.empty_cache()
+
+
 LAUNCH_SHAPES = [(4096, 4096), (4096, 14336), (14336, 4096), (8192, 8192)]
 
 
@@ -293,7 +334,8 @@ def autotune(args, rows):
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("what", choices=["decode", "prefill", "dequant", "crossover", "launch",
-                                     "autotune", "attention"])
+                                     "autotune", "attention", "strips"])
+    ap.add_argument("--N", type=int, nargs="*", help="strips: the weight widths (K = 4096)")
     ap.add_argument("--M", type=int, nargs="*", help="batch sizes (default: the benchmark shapes)")
     ap.add_argument("--pos", type=int, nargs="*", default=[0, 127, 128, 511, 1023, 2047, 4095],
                     help="attention: cache positions of the decoded token")
@@ -311,7 +353,8 @@ def main(argv=None) -> int:
     print(f"# {H.device_summary()}", file=sys.stderr, flush=True)
     rows = []
     {"decode": decode, "prefill": prefill, "dequant": dequant, "crossover": crossover,
-     "launch": launch, "autotune": autotune, "attention": attention}[args.what](args, rows)
+     "launch": launch, "autotune": autotune, "attention": attention,
+     "strips": strips}[args.what](args, rows)
     if args.markdown and rows:
         cols = [k for k in rows[0] if k != "bench"]
         print(H.markdown_table(rows, cols), file=sys.stderr)
