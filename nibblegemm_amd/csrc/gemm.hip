@@ -1124,7 +1124,8 @@ namespace {
 bool gemm_streams(int64_t M, int64_t K, int64_t N, int64_t G) {
   if (!(M >= 1 && M <= kStreamMaxM && K > 0 && N > 0 && N % 4 == 0 && K % G == 0)) return false;
   const int64_t pass_bytes = K * N / 2;
-  return M <= 32 || K % 64 != 0 || ceil_div(M, 32) * pass_bytes < (int64_t(48) << 20);
+  return M <= 32 || K % 64 != 0 || ceil_div(M, 32) * pass_bytes < (int64_t(48) << 20) ||
+         batch_block_rows(M, K, N, G) == 64;  // 33..64 rows in one 64-row block
 }
 }  // namespace
 

@@ -501,8 +501,8 @@ __device__ __forceinline__ void copy_window(const void* X, uint32_t xbytes, unsi
   }
 }
 
-// Batch kernel: 12 to 32 activation rows (small batches through gemm) in one
-// block of MT = 16 or 32 rows.  The split kernel's geometry -- one workgroup
+// Batch kernel: 12 to 64 activation rows (small batches through gemm) in one
+// block of MT = 16, 32 or 64 rows.  The split kernel's geometry -- one workgroup
 // per 64-column strip and K split, its 4 waves taking the split's quant
 // groups round-robin -- and its arithmetic: per group the same pre-scaled
 // activations, correction MFMA, decode and MFMA sequence, the same
@@ -546,7 +546,7 @@ __device__ __forceinline__ void copy_window(const void* X, uint32_t xbytes, unsi
 // beside the weight loads instead of in the compute waves' own queues.
 template <int MT, int GROUP, int DEPTH, int RING, int STAGERS, bool STREAM>
 __global__ __launch_bounds__((4 + STAGERS) * 64) void gemv_batch_kernel(GemvArgs a) {
-  static_assert(MT == 16 || MT == 32, "16-row MFMA tiles");
+  static_assert(MT == 16 || MT == 32 || MT == 64, "16-row MFMA tiles");
   constexpr int kWaves = 4;
   constexpr int THREADS = (kWaves + STAGERS) * 64;
   constexpr int kWPolicy = STREAM ? 2 : 0;
@@ -646,8 +646,52 @@ __global__ __launch_bounds__((4 + STAGERS) * 64) void gemv_batch_kernel(GemvArgs
     const DecodeConsts dk = decode_consts();
     const h8_t xscale = biased_x_scale();
     const h8_t bcorr = biased_correction();
-    // gemv_mfma_kernel's compute, the activations read from the slot.
+    // gemv_mfma_kernel's compute, the activations read from the slot.  With
+    // 64 rows (4 row tiles) the activations of every chunk and tile would
+    // not fit the registers beside the accumulators: chunks are taken one
+    // at a time, the correction accumulated apart and added before the
+    // group's scaling (the sums' order differs from the 32-row form, which
+    // serves the split kernel's plans; nothing else runs 64-row blocks).
+    auto compute64 = [&](const WStage& st, const unsigned char* base) {
+      f4_t acc[TILES][4], corr[TILES];
+#pragma unroll
+      for (int t = 0; t < TILES; ++t) {
+        corr[t] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[t][j] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+#pragma unroll
+      for (int c = 0; c < CPG; ++c) {
+        h8_t xs[TILES];
+        const uint32_t u = static_cast<uint32_t>(wave * (GROUP / 8) + 4 * c) + kb;
+#pragma unroll
+        for (int t = 0; t < TILES; ++t) {
+          const uint32_t r = 16u * t + q;
+          xs[t] = *reinterpret_cast<const h8_t*>(base + (r * UPR + (u ^ q)) * 16u) * xscale;
+          corr[t] = mfma16(xs[t], bcorr, corr[t]);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const h8_t b = decode8_biased(st.w[c][j], dk);
+#pragma unroll
+          for (int t = 0; t < TILES; ++t) acc[t][j] = mfma16(xs[t], b, acc[t][j]);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float sj = static_cast<float>(st.s[j]);
+#pragma unroll
+        for (int t = 0; t < TILES; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            tot[t][j][i] = __builtin_fmaf(sj, acc[t][j][i] + corr[t][i], tot[t][j][i]);
+      }
+    };
     auto compute = [&](const WStage& st, const unsigned char* base) {
+      if constexpr (MT == 64) {
+        compute64(st, base);
+        return;
+      }
       h8_t xs[TILES][CPG];
       f4_t acc[TILES][4];
 #pragma unroll
@@ -1206,6 +1250,13 @@ constexpr int kBatchRing = 3;
 constexpr int kBatchStagers = 4;
 constexpr int kBatchWorkgroups = 256;
 constexpr int kBatchMaxSplits = 8;
+// 33..64 rows run one 64-row block only when its grid fills the CUs in one
+// round (224..256 workgroups).  Measured on MI355X against gemm's 64-row
+// tiles, M = 33 / 64: 4096 x 14336 17.1 / 17.6 us against 19.2 / 19.7,
+// 14336 x 4096 17.4 / 18.8 against 20.0 / 21.6, 4096 x 4096 11.0 / 11.0
+// against 11.9 / 12.4; 192 workgroups (4096 x 6144) 12.9 against 12.3, two
+// rounds (4096 x 28672) 29.9 against 26.2.
+constexpr int kBatch64MinWorkgroups = 224;
 // 16-row blocks run the batch kernel from this many rows: at 9 rows the
 // split kernel, whose activation loads scale with the rows, is as fast or
 // faster (4096 x 4096 7.0 against 7.7 us, 14336 x 4096 10.4 against 10.5).
@@ -1349,14 +1400,18 @@ hipError_t launch_strip_group(const GemvArgs& a, const StreamPlan& p, hipStream_
 // slots of 32 rows x (4 x GROUP) k in dynamic LDS (96 KiB at GROUP = 128).
 template <int MT, int GROUP>
 hipError_t launch_batch_rows(const GemvArgs& a, const StreamPlan& p, hipStream_t stream) {
-  constexpr size_t kLds = static_cast<size_t>(kBatchRing) * MT * (4 * GROUP / 8) * 16;
+  // 64-row slots (64 KiB at GROUP = 128) leave room for 2.
+  constexpr int kRing = MT == 64 ? 2 : kBatchRing;
+  constexpr size_t kSlots = static_cast<size_t>(kRing) * MT * (4 * GROUP / 8) * 16;
+  constexpr size_t kTotals = static_cast<size_t>(4) * MT * 16 * 16;
+  constexpr size_t kLds = kSlots > kTotals ? kSlots : kTotals;
   static_assert(kLds + 256 <= 160 * 1024, "a workgroup holds at most 160 KiB of LDS");
   const dim3 grid(p.strips, p.splits, p.mblocks);
   constexpr int kThreads = (4 + kBatchStagers) * 64;
   if (p.mblocks == 1)
-    gemv_batch_kernel<MT, GROUP, kBatchDepth, kBatchRing, kBatchStagers, true><<<grid, kThreads, kLds, stream>>>(a);
+    gemv_batch_kernel<MT, GROUP, kBatchDepth, kRing, kBatchStagers, true><<<grid, kThreads, kLds, stream>>>(a);
   else
-    gemv_batch_kernel<MT, GROUP, kBatchDepth, kBatchRing, kBatchStagers, false><<<grid, kThreads, kLds, stream>>>(a);
+    gemv_batch_kernel<MT, GROUP, kBatchDepth, kRing, kBatchStagers, false><<<grid, kThreads, kLds, stream>>>(a);
   return hipGetLastError();
 }
 
@@ -1366,6 +1421,7 @@ hipError_t launch_batch_group(const GemvArgs& a, const StreamPlan& p, hipStream_
   switch (p.mt) {
     case 16: return launch_batch_rows<16, GROUP>(a, p, stream);
     case 32: return launch_batch_rows<32, GROUP>(a, p, stream);
+    case 64: return launch_batch_rows<64, GROUP>(a, p, stream);
     default: return hipErrorInvalidValue;
   }
 }
@@ -1465,15 +1521,45 @@ bool plan_strip(int64_t M, int64_t K, int64_t N, int64_t G, StreamFusion fusion,
   return true;
 }
 
+namespace {
+// K splits of a batch-kernel plan: the split kernel's count, raised where the
+// strips alone leave CUs idle (at most kBatchMaxSplits, at least 4 groups a
+// split).
+int batch_splits(int strips, int groups, int heuristic) {
+  const int fill = std::min({kBatchMaxSplits, kBatchWorkgroups / std::max(1, strips), groups / 4});
+  return std::max(heuristic, fill);
+}
+}  // namespace
+
+int batch_block_rows(int64_t M, int64_t K, int64_t N, int64_t G) {
+  if (M < kBatchMinRows || M > 64 || K <= 0 || N <= 0 || (G != 64 && G != 128) || K % G != 0)
+    return 0;
+  if (M <= 16) {
+    StreamPlan strip;
+    return plan_strip(M, K, N, G, StreamFusion(), &strip) ? 0 : 16;
+  }
+  if (M <= 32) return 32;
+  // 33..64 rows: one 64-row block where its grid is one full round of the
+  // CUs; otherwise the tiles (or 32-row passes) of gemm's own plan.
+  StreamPlan sp;
+  if (plan_split_kernel(M, K, N, G, true, 0, 0, &sp) != NIBBLE_OK) return 0;
+  const int64_t grid = static_cast<int64_t>(sp.strips) *
+                       batch_splits(sp.strips, static_cast<int>(K / G), sp.splits);
+  return grid >= kBatch64MinWorkgroups && grid <= kBatchWorkgroups ? 64 : 0;
+}
+
 int plan_stream(int64_t M, int64_t K, int64_t N, int64_t G, bool split_k, int64_t splits_override,
                 int64_t threads_override, StreamPlan* p, StreamFusion fusion) {
   if (split_k && splits_override == 0 && threads_override == 0 &&
       plan_strip(M, K, N, G, fusion, p))
     return NIBBLE_OK;
   const int rc = plan_split_kernel(M, K, N, G, split_k, splits_override, threads_override, p);
-  if (rc != NIBBLE_OK || !split_k || splits_override != 0 || threads_override != 0 ||
-      p->mblocks != 1 || p->waves != 4 || !(p->mt == 32 || (p->mt == 16 && M >= kBatchMinRows)))
+  if (rc != NIBBLE_OK || !split_k || splits_override != 0 || threads_override != 0 || p->waves != 4)
     return rc;
+  const int rows = batch_block_rows(M, K, N, G);
+  if (rows == 0) return rc;
+  p->mt = rows;
+  p->mblocks = 1;
   // 12..32 rows (those the strip kernel does not take) run the batch kernel
   // in one block of 16 or 32 rows (the split kernel's bits for the same
   // plan), with K split further where the strips alone leave CUs idle (at
@@ -1485,13 +1571,14 @@ int plan_stream(int64_t M, int64_t K, int64_t N, int64_t G, bool split_k, int64_
   // 14336 x 4096 10.5 / 10.6 against 11.1 / 12.2, 8192 x 8192 10.7 / 10.8
   // against 11.8 / 13.1.
   const int groups = static_cast<int>(K / G);
-  const int fill = std::min({kBatchMaxSplits, kBatchWorkgroups / std::max(1, p->strips), groups / 4});
+  const int fill = batch_splits(p->strips, groups, p->splits);
   if (fill > p->splits) {
     p->groups_per_split = static_cast<int>(ceil_div(groups, fill));
     p->splits = static_cast<int>(ceil_div(groups, p->groups_per_split));
-    p->counter_bytes = align_up(static_cast<size_t>(p->strips) * p->mblocks * 4, 256);
-    p->workspace_bytes = p->counter_bytes + static_cast<size_t>(p->splits) * M * N * 4;
   }
+  p->counter_bytes = p->splits > 1 ? align_up(static_cast<size_t>(p->strips) * 4, 256) : 0;
+  p->workspace_bytes =
+      p->splits > 1 ? p->counter_bytes + static_cast<size_t>(p->splits) * M * N * 4 : 0;
   p->kernel = kBatchKernel;
   p->depth = kBatchDepth;
   p->ring = kBatchRing;
@@ -1812,16 +1899,30 @@ int validate_fused(const void* X, int64_t x_rows, int64_t x_cols, const void* Wq
 namespace {
 // The fused entry's workspace covers both streaming plans of these operands
 // (the split kernel's, and the heuristic plan the launch takes), so one
-// buffer serves every epilogue and prologue.
+// buffer serves every epilogue and prologue: a counter region as large as
+// either plan's, then room for either plan's partials.  The launch lays the
+// workspace out that way too (fused_layout), so a caller that keys buffers
+// by the reported counter region never finds partials inside it.
 bool fused_plan_bytes(int64_t M, int64_t K, int64_t N, int64_t G, size_t* ws, size_t* counters) {
   StreamPlan a, b;
   if (M < 1 || M > kStreamMaxM || K <= 0 || N <= 0 || (G != 64 && G != 128) || K % G != 0 ||
       plan_split_kernel(M, K, N, G, true, 0, 0, &a) != NIBBLE_OK ||
       plan_stream(M, K, N, G, true, 0, 0, &b) != NIBBLE_OK)
     return false;
-  *ws = std::max(a.workspace_bytes, b.workspace_bytes);
   *counters = std::max(a.counter_bytes, b.counter_bytes);
+  const size_t partials = std::max(a.workspace_bytes - a.counter_bytes,
+                                   b.workspace_bytes - b.counter_bytes);
+  *ws = partials > 0 ? *counters + partials : 0;
   return true;
+}
+
+// A split plan of the fused entry takes the reported layout: its counters
+// at the start of a region of the reported size, its partials after it.
+void fused_layout(int64_t M, int64_t K, int64_t N, int64_t G, StreamPlan* p) {
+  size_t ws = 0, counters = 0;
+  if (p->workspace_bytes == 0 || !fused_plan_bytes(M, K, N, G, &ws, &counters)) return;
+  p->workspace_bytes = counters + (p->workspace_bytes - p->counter_bytes);
+  p->counter_bytes = counters;
 }
 }  // namespace
 
@@ -1856,6 +1957,7 @@ extern "C" int nibble_matmul_w4a16_fused(const void* X, int64_t x_rows, int64_t 
   StreamPlan p;
   rc = plan_stream(M, K, N, group_size, true, 0, 0, &p, fusion);
   if (rc != NIBBLE_OK) return rc;
+  fused_layout(M, K, N, group_size, &p);
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   DeviceGuard guard;
   int dev = 0;

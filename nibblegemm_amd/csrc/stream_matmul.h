@@ -65,7 +65,7 @@ inline WeightLayout layout_for(int64_t K, int64_t N, int64_t G, int64_t strip_co
 // kStripKernel (M <= 8): `strip_cols`-column strips over the whole of K,
 // `waves` waves per workgroup on contiguous group ranges with `depth` groups
 // of loads in flight per wave; no workspace.
-// kBatchKernel (one block of 12..32 rows): the split kernel's geometry and
+// kBatchKernel (one block of 12..64 rows): the split kernel's geometry and
 // arithmetic (so its bits), with each step's activation window copied once
 // into an LDS ring by staging waves and `depth` steps of weight loads in
 // flight per wave.
@@ -79,7 +79,7 @@ constexpr int kBatchKernel = 2;
 // `workspace_bytes` is the total.
 struct StreamPlan {
   int kernel = kSplitKernel;
-  int mt = 1;      // compiled row count: 1, 2, 4, 8, 16 or 32
+  int mt = 1;      // compiled row count: 1, 2, 4, 8, 16 or 32 (64: batch kernel)
   int mblocks = 1; // blocks of mt rows (grid.z); more than one only above 32 rows
   int waves = 4;   // wave64s per workgroup
   int strips = 0;  // column strips (grid.x for the split kernel)
@@ -109,6 +109,12 @@ int plan_stream(int64_t M, int64_t K, int64_t N, int64_t G, bool split_k, int64_
 // The strip kernel's plan for these operands, if it serves them (M <= 8,
 // and the fusion it supports); returns false otherwise.  Pure host arithmetic.
 bool plan_strip(int64_t M, int64_t K, int64_t N, int64_t G, StreamFusion fusion, StreamPlan* p);
+
+// Rows of the one block the batch kernel takes these operands in (16, 32 or
+// 64), or 0 when the plan is another kernel's: 12..16 rows outside the strip
+// kernel's plans, 17..32 rows, and 33..64 rows where the 64-row block's grid
+// fills the CUs in one round.  Pure host arithmetic.
+int batch_block_rows(int64_t M, int64_t K, int64_t N, int64_t G);
 
 // Whether the streaming kernel can take these operands: N a multiple of 4,
 // 16-byte X and Wq, 8-byte S and Y, offsets within 31 bits.

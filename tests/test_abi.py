@@ -95,22 +95,25 @@ def test_gemv_threads_override_validated():
 
 
 def test_gemm_workspace_formula():
-    """Batches of M <= 32 run the streaming kernel (split-K workspace as for
-    gemv), as do M <= 128 whose passes over the weights (one per 32 rows) stay
-    under 48 MiB; otherwise tiles, split over K only when the tiles are few."""
+    """Batches of M <= 32 run the streaming kernels (split-K workspace as for
+    gemv), as do M <= 64 whose one 64-row block fills the CUs in one round
+    and M <= 128 whose passes over the weights (one per 32 rows) stay under
+    48 MiB; otherwise tiles, split over K only when the tiles are few."""
     ext = ng.extension()
     assert ext.gemm_workspace_bytes(16, 14336, 4096, 128, 6, None) == (256 + 4 * 16 * 4096 * 4, 256)
     assert ext.gemm_workspace_bytes(32, 4096, 14336, 128, 7, None) == (0, 0)
-    # M = 33 over 29.4 MB of weights would stream twice (58.7 MB): 64-row
-    # tiles instead, 32 of them split 8 ways (256 workgroups), both versions
-    assert ext.gemm_workspace_bytes(33, 14336, 4096, 128, 6, None) == (256 + 8 * 33 * 4096 * 4, 256)
-    assert ext.gemm_workspace_bytes(33, 14336, 4096, 128, 7, None) == (256 + 8 * 33 * 4096 * 4, 256)
-    # 4096 x 14336: 112 tiles split 2 ways at M = 64, 224 unsplit at M = 128
-    assert ext.gemm_workspace_bytes(64, 4096, 14336, 128, 6, None) == (512 + 2 * 64 * 14336 * 4, 512)
+    # M = 33..64 over 29.4 MB of weights: one 64-row block of the batch
+    # kernel, 64 strips split 4 ways (256 workgroups), both versions
+    assert ext.gemm_workspace_bytes(33, 14336, 4096, 128, 6, None) == (256 + 4 * 33 * 4096 * 4, 256)
+    assert ext.gemm_workspace_bytes(33, 14336, 4096, 128, 7, None) == (256 + 4 * 33 * 4096 * 4, 256)
+    # 4096 x 14336: 224 strips unsplit at M = 64 (one block), 224 unsplit
+    # 64-row tiles at M = 128
+    assert ext.gemm_workspace_bytes(64, 4096, 14336, 128, 6, None) == (0, 0)
     assert ext.gemm_workspace_bytes(128, 4096, 14336, 128, 6, None) == (0, 0)
-    # 4096 x 4096 (8.4 MB) keeps streaming up to M = 128 (4 passes, 33.6 MB):
-    # two 32-row blocks at M = 33, no split
-    assert ext.gemm_workspace_bytes(33, 4096, 4096, 128, 6, None) == (0, 0)
+    # 4096 x 4096: one 64-row block at M = 33, its 64 strips split 4 ways;
+    # 4096 x 6144 (192 workgroups at most) streams 32-row blocks, unsplit
+    assert ext.gemm_workspace_bytes(33, 4096, 4096, 128, 6, None) == (256 + 4 * 33 * 4096 * 4, 256)
+    assert ext.gemm_workspace_bytes(33, 4096, 6144, 128, 6, None) == (0, 0)
     # M > 128 runs the producer/consumer kernel; over a long K (224 steps of
     # 64) with 128 x 128 tiles split by their count: 2 x 32 = 64 tiles 4 ways
     # (both versions: the same plan, so the same bits)
@@ -368,12 +371,15 @@ def test_fused_workspace_matches_streaming_plan():
 
 def test_gemm_streams_query():
     """nibble_gemm_streams names the plan nibble_gemm_w4a16 takes: streaming
-    for M <= 32 and for 33..128 rows whose 32-row weight passes move under
-    48 MiB, tiles above (where the fused entry's plan differs from gemm's)."""
+    for M <= 32, for 33..64 rows whose one 64-row block makes one round of
+    the CUs, and for 33..128 rows whose 32-row weight passes move under
+    48 MiB; tiles otherwise (where the fused entry's plan differs from
+    gemm's)."""
     ext = ng.extension()
     for M, K, N, g, streams in [(1, 4096, 14336, 128, True), (32, 14336, 4096, 128, True),
-                                (33, 14336, 4096, 128, False), (33, 4096, 4096, 128, True),
-                                (64, 4096, 14336, 128, False), (128, 4096, 6144, 64, False),
+                                (33, 14336, 4096, 128, True), (33, 4096, 4096, 128, True),
+                                (64, 4096, 14336, 128, True), (65, 4096, 14336, 128, False),
+                                (40, 4096, 28672, 128, False), (128, 4096, 6144, 64, False),
                                 (64, 4096, 6144, 128, True), (128, 8192, 1024, 128, True),
                                 (129, 4096, 4096, 128, False), (8, 4096, 4096, 32, False),
                                 (8, 4096, 4098, 128, False), (0, 4096, 4096, 128, False)]:
@@ -382,17 +388,17 @@ def test_gemm_streams_query():
             fused = ext.matmul_fused_workspace_bytes(M, K, N, g, None)
             gemm = ext.gemm_workspace_bytes(M, K, N, g, 6, None)
             assert fused[0] >= gemm[0] and fused[1] >= gemm[1], (M, K, N, g)
-            if M > 16:
+            if 16 < M <= 32:
                 assert fused == gemm, (M, K, N, g)
 
 
 def test_gemm_streams_agrees_with_the_plans():
     """Over random batch shapes: where nibble_gemm_streams says the GEMM
     streams, the fused entry's workspace covers the GEMM's (it answers for
-    the split kernel, the larger of the two streaming plans, so one buffer
-    serves every epilogue; equal from 17 rows, where both run it); where it
-    does not, the batch is 33..128 rows over passes of 48 MiB or more (or
-    the operands cannot stream at all)."""
+    the split kernel's plan and the GEMM's, so one buffer serves every
+    epilogue; equal for 17..32 rows, where the batch kernel's plan is the
+    larger); where it does not, the batch is 33..128 rows over passes of
+    48 MiB or more (or the operands cannot stream at all)."""
     import random
     ext = ng.extension()
     rng = random.Random(7)
@@ -406,7 +412,7 @@ def test_gemm_streams_agrees_with_the_plans():
             fused = ext.matmul_fused_workspace_bytes(M, K, N, g, None)
             gemm = ext.gemm_workspace_bytes(M, K, N, g, 6, None)
             assert fused[0] >= gemm[0] and fused[1] >= gemm[1], (M, K, N, g)
-            if M > 16:
+            if 16 < M <= 32:
                 assert fused == gemm, (M, K, N, g)
         else:
             assert M > 128 or (M > 32 and ((M + 31) // 32) * K * N // 2 >= 48 << 20), (M, K, N, g)

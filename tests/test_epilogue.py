@@ -114,3 +114,26 @@ def test_fused_calls_replay_in_a_graph():
         assert torch.equal(out, ref)
         ng.matmul(Xd, qw)  # eager work between replays
         torch.cuda.synchronize()
+
+
+def test_fused_plans_sharing_a_workspace():
+    """The fused entry sizes its workspace for the larger of its two plans and
+    lays it out that way (counters, then partials), so plans whose own
+    counter regions differ can share the buffer the package keys by the
+    reported counter size: a 64-row bias call (64 strips split 4 ways) and
+    then a 24-row SwiGLU (128 strips split 2 ways) both report 512 counter
+    bytes; the second must not read the first's partials as counters."""
+    ext = ng.extension()
+    assert ext.matmul_fused_workspace_bytes(64, 14336, 4096, 128, None)[1] == \
+        ext.matmul_fused_workspace_bytes(24, 4096, 8192, 128, None)[1]
+    _, _, _, X1, w1 = synthetic(64, 14336, 4096, 128, seed=5)
+    bias = (torch.randn(4096, generator=torch.Generator().manual_seed(4)) * 0.5).half().cuda()
+    assert torch.equal(ng.matmul_bias(X1, w1, bias), ng.matmul(X1, w1) + bias)
+    _, _, _, X2, gate = quantized(24, 4096, 4096, 128, seed=1)
+    _, _, _, _, up = quantized(24, 4096, 4096, 128, seed=2)
+    qw = ng.interleave_swiglu(gate, up)
+    for _ in range(3):
+        fused = ng.matmul_swiglu(X2, qw)
+        yg, yu = split_swiglu(ng.matmul(X2, qw))
+        assert torch.equal(fused, torch.nn.functional.silu(yg) * yu)
+        assert torch.equal(ng.matmul_bias(X1, w1, bias), ng.matmul(X1, w1) + bias)

@@ -91,12 +91,45 @@ def test_batch_rows_full_size(M, K_, N):
     assert rel_err(host(y), ref) < REL_TOL
 
 
+@pytest.mark.parametrize("M,K_,N", [(M, K_, N) for M in (33, 48, 64)
+                                    for K_, N in ((4096, 14336), (14336, 4096), (8192, 8192))]
+                         + [(40, 4096, 4096), (57, 14336, 4036)])
+def test_batch_64_row_block(M, K_, N):
+    """33..64 rows whose one 64-row block makes one round of the CUs run the
+    batch kernel in that block: every output against an fp32 product of the
+    dequant kernel's weights, both versions and matmul the same bits,
+    repeated calls bit-identical.  The last shape ends in a partial strip."""
+    ext = ng.extension()
+    assert ext.gemm_streams(M, K_, N, 128)
+    _, _, _, Xd, qw = synthetic(M, K_, N, 128, seed=800 + M + N)
+    ref = Xd.float() @ ng.dequant(qw).float()
+    rms = ref.pow(2).mean().sqrt()
+    y = ng.gemm(Xd, qw, version=6)
+    assert torch.equal(ng.gemm(Xd, qw, version=7), y)
+    assert torch.equal(ng.gemm(Xd, qw), y)
+    assert torch.equal(ng.matmul(Xd, qw), y)
+    assert torch.isfinite(y.float()).all()
+    assert float((y.float() - ref).abs().max() / rms) <= RMS_TOL
+
+
+@pytest.mark.parametrize("M", [33, 64])
+def test_batch_64_row_block_against_the_oracle(M):
+    """The small-batch config's down projection (14336 x 4096) at 33 and 64
+    rows, every output against the CPU oracle."""
+    X, packed, scales, Xd, qw = synthetic(M, 14336, 4096, 128, seed=850 + M)
+    y = host(ng.gemm(Xd, qw))
+    ref = oracle_y(X, packed, scales, 14336, 128)
+    assert rms_err(y, ref) <= RMS_TOL
+    assert rel_err(y, ref) < REL_TOL
+
+
 @pytest.mark.parametrize("M,K_,N,g", [(24, 14336, 4096, 128), (17, 4096, 1024, 128), (32, 2048, 1540, 64),
-                                      (20, 640, 196, 64), (14, 14336, 1024, 128), (12, 1024, 260, 64)])
+                                      (20, 640, 196, 64), (14, 14336, 1024, 128), (12, 1024, 260, 64),
+                                      (48, 14336, 4096, 128)])
 def test_batch_rows_replay_in_a_graph(M, K_, N, g):
-    """The batch kernel with K split (4, 8, 8, 2, 8 and 4 ways; 32- and
-    16-row blocks; three end in a partial strip): its counters are reset by
-    the kernel, so a captured call replays with every replay equal to the
+    """The batch kernel with K split (4, 8, 8, 2, 8, 4 and 4 ways; 32-, 16-
+    and 64-row blocks; three end in a partial strip): its counters are reset
+    by the kernel, so a captured call replays with every replay equal to the
     eager call, eager work between."""
     X, packed, scales, Xd, qw = synthetic(M, K_, N, g, seed=13 + M)
     ext = ng.extension()
@@ -194,16 +227,18 @@ def test_small_batch_handover(M, K_, N, g):
         assert rel_err(y, ref) < REL_TOL, version
 
 
-@pytest.mark.parametrize("M,K_,N", [(M, K_, N) for M in (33, 64, 100, 128)
+@pytest.mark.parametrize("M,K_,N", [(M, K_, N) for M in (100, 128)
                                     for K_, N in ((4096, 14336), (14336, 4096), (8192, 8192))]
-                         + [(100, 14336, 4100), (47, 8192, 8200), (65, 4096, 14340)])
+                         + [(100, 14336, 4100), (47, 8192, 8200), (65, 4096, 14340),
+                            (40, 4096, 28672), (64, 8192, 14336)])
 def test_small_batch_tiles(M, K_, N):
     """Batches of 33..128 rows over large weights (32-row weight passes of
-    48 MiB or more) take 64-row producer/consumer tiles split over K instead
-    of streaming: every output, both versions (the same plan, so the same
+    48 MiB or more, where one 64-row block would not make one round of the
+    CUs) take 64-row producer/consumer tiles split over K instead of
+    streaming: every output, both versions (the same plan, so the same
     bits), repeated calls bit-identical, against an fp32 product of the
-    dequant kernel's weights on the GPU.  The last three shapes end in
-    partial row and column tiles."""
+    dequant kernel's weights on the GPU.  Three shapes end in partial row
+    and column tiles."""
     ext = ng.extension()
     assert not ext.gemm_streams(M, K_, N, 128)
     _, _, _, Xd, qw = synthetic(M, K_, N, 128, seed=400 + M + N)
