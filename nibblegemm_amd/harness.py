@@ -24,7 +24,6 @@ import os
 import re
 import statistics
 import threading
-import time
 from dataclasses import dataclass, field
 from typing import Callable, Dict, List, Optional, Sequence, Tuple
 
@@ -136,9 +135,12 @@ class ClockMonitor:
 
     def start(self) -> "ClockMonitor":
         tel = telemetry()
-        self.samples = [tel.sample()]
+        self.samples = []
 
+        # The thread takes the first sample too: a sysfs read on the caller's
+        # thread would hold back the first timed window while the GPU idles.
         def run():
+            self.samples.append(tel.sample())
             while not self._stop.wait(self.period):
                 self.samples.append(tel.sample())
 
@@ -237,14 +239,40 @@ def _time_windows(issue: Callable[[], None], trials: int, per_window: int):
     return tuple(out), mon.stop()
 
 
+def keep_busy(issue: Callable[[], None], seconds: float) -> None:
+    """Issues ``issue()`` back to back for about ``seconds`` and returns while
+    the last call is still running, so what is queued next starts at the
+    loaded clock.
+
+    After an idle of a few milliseconds MI355X runs its first millisecond or
+    so of full-HBM work at ~2.25 GHz, drops to ~1.6 GHz and climbs back over
+    the next ~25 ms (busy-cycle counts per dispatch stay constant while the
+    duration moves with the clock).  A timing that opens after such an idle
+    measures that dip, so the host waits on an event recorded before the last
+    call rather than sleeping for an estimate of the queue's length: a sleep
+    that outlasts the queue leaves the GPU idle and starts the dip again."""
+    start, end = _new_event(), _new_event()
+    start.record()
+    issue()
+    end.record()
+    end.synchronize()
+    per = max(start.elapsed_time(end) / 1e3, 1e-6)
+    for _ in range(max(1, math.ceil(seconds / per)) - 1):
+        issue()
+    before_last = _new_event()
+    before_last.record()
+    issue()
+    before_last.synchronize()
+
+
 def bench(fn: Callable[[int], object], *, reps: int = 32, trials: int = 20,
-          warmup: int = 5) -> Timing:
+          warmup: int = 5, warm_s: float = 0.05) -> Timing:
     """Eager timing of ``fn(i)``: windows of ``reps`` calls issued back to
-    back.  The call index keeps counting across windows, so a rotation of
-    weight copies advances through all of them."""
+    back, after ``warmup`` calls and ``warm_s`` seconds of untimed windows
+    (:func:`keep_busy`).  The call index keeps counting across windows, so a
+    rotation of weight copies advances through all of them."""
     for i in range(warmup):
         fn(i)
-    torch.cuda.synchronize()
     index = [0]
 
     def window():
@@ -252,6 +280,7 @@ def bench(fn: Callable[[int], object], *, reps: int = 32, trials: int = 20,
             fn(index[0])
             index[0] += 1
 
+    keep_busy(window, warm_s)
     windows, clocks = _time_windows(window, trials, reps)
     return Timing(windows, reps, clocks)
 
@@ -279,22 +308,9 @@ class GraphRunner:
         self.reps = reps
 
     def warm(self, seconds: float) -> None:
-        """Keeps the GPU busy with untimed replays for about ``seconds`` and
-        returns while the last of them is still running, so what is queued
-        next starts at the loaded clock.  MI355X drops its shader clock within
-        ~100 ms of going idle and takes a comparable time to raise it again; a
-        timing that starts from idle runs its first milliseconds slow."""
-        start = torch.cuda.Event(enable_timing=True)
-        end = torch.cuda.Event(enable_timing=True)
-        start.record()
-        self.graph.replay()
-        end.record()
-        end.synchronize()
-        per = max(start.elapsed_time(end) / 1e3, 1e-6)
-        n = max(1, math.ceil(seconds / per))
-        for _ in range(n):
-            self.graph.replay()
-        time.sleep(max(0.0, (n - 1) * per))
+        """Untimed replays for about ``seconds``; returns while the last one
+        is still running (:func:`keep_busy`)."""
+        keep_busy(self.graph.replay, seconds)
 
     def time(self, trials: int = 20, warm_s: float = 0.05) -> Timing:
         """``trials`` windows of one replay each, after :meth:`warm`."""
