@@ -50,7 +50,7 @@
 extern "C" {
 #endif
 
-#define NIBBLE_ABI_VERSION 11
+#define NIBBLE_ABI_VERSION 12
 
 #if defined(__GNUC__) || defined(__clang__)
 #define NIBBLE_API __attribute__((visibility("default")))
@@ -358,6 +358,15 @@ NIBBLE_API int nibble_chain_check(void* chain, void* stream);
 /* 0: workgroups, 1: rounds, 2: dynamic LDS bytes, 3: stages; -1 otherwise. */
 NIBBLE_API int64_t nibble_chain_info(void* chain, int64_t what);
 NIBBLE_API int nibble_chain_destroy(void* chain);
+/* The strip width at which a chain of independent M-row stages streams a
+ * [K, N] weight fastest: at least 32 columns where a one-stage chain of it has a plan
+ * (the LDS of the chain grows with K and the strip's scales), else
+ * nibble_strip_major_cols's width; 0 when neither has a chain plan.  A chain
+ * round costs a fixed allowance besides its bytes, so the chain wants fewer,
+ * wider strips than the per-projection launches, which want a workgroup per
+ * CU.  A weight converted at either width serves both.  Pure host
+ * computation. */
+NIBBLE_API int64_t nibble_chain_strip_cols(int64_t K, int64_t N, int64_t group_size, int64_t M);
 
 /*
  * Measurement: a streaming read of `bytes` (a positive multiple of 16) from

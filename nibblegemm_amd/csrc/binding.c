@@ -153,6 +153,16 @@ static PyObject* py_sm_cols(PyObject* self, PyObject* const* a, Py_ssize_t n) {
   return PyLong_FromLongLong((long long)nibble_strip_major_cols(K, N, g));
 }
 
+/* chain_strip_cols(K, N, g, M) */
+static PyObject* py_chain_cols(PyObject* self, PyObject* const* a, Py_ssize_t n) {
+  (void)self;
+  if (!nargs_is(n, 4, "chain_strip_cols")) return NULL;
+  long long K, N, g, M;
+  if (!take_i64(a[0], &K) || !take_i64(a[1], &N) || !take_i64(a[2], &g) || !take_i64(a[3], &M))
+    return NULL;
+  return PyLong_FromLongLong((long long)nibble_chain_strip_cols(K, N, g, M));
+}
+
 /* pack_strip_major(Wq, wr, wc, S, sr, sc, g, strip_cols, Wt, St, stream) */
 static PyObject* py_sm_pack(PyObject* self, PyObject* const* a, Py_ssize_t n) {
   (void)self;
@@ -374,6 +384,8 @@ static PyMethodDef kMethods[] = {
      "nibble_gemm_streams"},
     {"strip_major_cols", (PyCFunction)(void (*)(void))py_sm_cols, METH_FASTCALL,
      "nibble_strip_major_cols"},
+    {"chain_strip_cols", (PyCFunction)(void (*)(void))py_chain_cols, METH_FASTCALL,
+     "nibble_chain_strip_cols"},
     {"pack_strip_major", (PyCFunction)(void (*)(void))py_sm_pack, METH_FASTCALL,
      "nibble_pack_strip_major"},
     {"gemv_strip_major", (PyCFunction)(void (*)(void))py_sm_gemv, METH_FASTCALL,

@@ -626,6 +626,30 @@ Range range_of(const void* p, size_t bytes) {
 // CU's share of HBM bandwidth).
 constexpr double kRoundOverheadBytes = 32.0 * 1024;
 
+// LDS of a chain: the weight ring, double-buffered activations (mt rows of
+// the largest K), double-buffered scales (the largest round's), bias, and
+// the static partials.  Returns the dynamic part; *total adds the static.
+size_t chain_lds_bytes(int mt, int64_t kmax, size_t smax, size_t* total) {
+  const size_t xbuf_halves = static_cast<size_t>(mt) * static_cast<size_t>(kmax);
+  const size_t lds = kRingBytes + 2 * xbuf_halves * 2 + 2 * align_up(smax, 16) + 2 * kBiasBytes;
+  *total = lds + 2 * sizeof(float) * kComputeWaves * 64 * mt + 16;
+  return lds;
+}
+
+// Whether a one-stage chain of this weight has a plan: a strip-major plan
+// whose team shape the chain runs, and LDS within the CU's.
+bool chain_fits(int64_t M, int64_t K, int64_t N, int64_t G, int64_t SW) {
+  StreamPlan p;
+  if (SW <= 0 || N % SW != 0 || !plan_strip_major(M, K, N, G, SW, &p) ||
+      p.waves != chain_waves(static_cast<int>(SW)))
+    return false;
+  const int mt = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
+  const size_t smax = static_cast<size_t>(kComputeWaves / p.waves) * static_cast<size_t>(K / G * SW * 2);
+  size_t total = 0;
+  chain_lds_bytes(mt, K, smax, &total);
+  return total <= kLdsMax;
+}
+
 }  // namespace
 
 // Host-only plan construction, exposed for the C ABI below.
@@ -748,11 +772,11 @@ int chain_create(const nibble_chain_stage* stages, int64_t n, int64_t M, void* s
   NIBBLE_HIP(cu_count(dev, &cus));
   const size_t xbuf_halves = static_cast<size_t>(mt) * static_cast<size_t>(kmax);
   const size_t sbuf = align_up(smax, 16);
-  const size_t lds = kRingBytes + 2 * xbuf_halves * 2 + 2 * sbuf + 2 * kBiasBytes;
-  const size_t static_lds = 2 * sizeof(float) * kComputeWaves * 64 * mt + 16;
-  NIBBLE_CHECK(lds + static_lds <= kLdsMax,
+  size_t lds_total = 0;
+  const size_t lds = chain_lds_bytes(mt, kmax, smax, &lds_total);
+  NIBBLE_CHECK(lds_total <= kLdsMax,
                "chain needs %zu bytes of LDS (M=%lld, largest K=%lld); the limit is %zu",
-               lds + static_lds, (long long)M, (long long)kmax, kLdsMax);
+               lds_total, (long long)M, (long long)kmax, kLdsMax);
   const void* fn = chain_kernel_fn(mt, static_cast<int>(G));
   int per_cu = 0;
   NIBBLE_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kChainThreads, lds));
@@ -849,6 +873,17 @@ int chain_create(const nibble_chain_stage* stages, int64_t n, int64_t M, void* s
 }  // namespace nibble
 
 using namespace nibble;
+
+extern "C" int64_t nibble_chain_strip_cols(int64_t K, int64_t N, int64_t group_size, int64_t M) {
+  // A chain round costs a fixed allowance (barriers, partial sums, stores)
+  // besides its bytes, so fewer, wider strips win: at least 32 columns where
+  // the chain has a plan for them, else the launches' width.
+  const int64_t base = strip_major_cols(K, N, group_size);
+  if (base == 0 || M < 1 || M > 8) return 0;
+  const int64_t wide = std::max<int64_t>(base, 32);
+  if (wide != base && chain_fits(M, K, N, group_size, wide)) return wide;
+  return chain_fits(M, K, N, group_size, base) ? base : 0;
+}
 
 extern "C" int nibble_chain_create(const nibble_chain_stage* stages, int64_t n_stages, int64_t M,
                                    void* stream, void** chain) {

@@ -46,8 +46,10 @@ activation -- as ONE launch; ``persistent`` runs the fused strip-major step
 the same way: a
 :class:`~nibblegemm_amd.chain.DecodeChain` of the 128 projections, each still
 reading its fixed activation (the reference's semantics), whose workgroups
-stream weights across projection boundaries; the outputs are bit-identical to
-``fused_strips``.  ``dataflow`` is the real data flow of a decoder layer
+stream weights across projection boundaries.  Both run on strip-major copies
+at the chain's widths (:func:`~nibblegemm_amd.chain.chain_strip_cols`: o and
+down in 32-column strips where the launches take 16), and their outputs are
+bit-identical to the launches on the same copy.  ``dataflow`` is the real data flow of a decoder layer
 without attention and norms, one launch per projection on strip-major
 weights: the q|k|v product, o on its q part with the layer input added as
 the residual, gate|up through the SwiGLU epilogue, and down with o's output
@@ -77,7 +79,7 @@ from typing import Dict, List, Tuple
 import torch
 
 from . import harness as H
-from .chain import DecodeChain, stage
+from .chain import DecodeChain, chain_strip_cols, stage
 from .glue import attention_bytes, attention_decode, rmsnorm, rope_tables
 from .ops import (matmul, matmul_bias, matmul_swiglu, rmsnorm_matmul, strip_major_cols,
                   to_strip_major)
@@ -145,12 +147,16 @@ def fuse(layer: Dict[str, QuantizedWeight], swiglu: bool = False) -> Dict[str, Q
             ("gate_up_swiglu" if swiglu else "gate_up"): gate_up, "down": layer["down"]}
 
 
-def strips(layers: List[Dict[str, QuantizedWeight]]) -> list:
-    """Strip-major copies of every weight, each at its recommended width (at
-    least 32 columns for the SwiGLU weight, whose strips must hold whole
-    gate|up block pairs)."""
+def strips(layers: List[Dict[str, QuantizedWeight]], chain: bool = False) -> list:
+    """Strip-major copies of every weight, each at the width the launches
+    stream fastest (``strip_major_cols``) or, with ``chain``, the width a
+    decode chain does (``chain_strip_cols``: at least 32 columns where they
+    fit; MI355X, 8B step as one chain, 0.585 -> 0.552 ms with o and down at
+    32 columns instead of 16, while the 128 launches go 0.892 -> 0.955 ms).
+    The SwiGLU weight takes at least 32 columns either way: its strips must
+    hold whole gate|up block pairs."""
     def one(name, qw):
-        sw = strip_major_cols(qw.K, qw.N, qw.group_size)
+        sw = (chain_strip_cols if chain else strip_major_cols)(qw.K, qw.N, qw.group_size)
         return to_strip_major(qw, max(sw, 32) if name == "gate_up_swiglu" else sw)
     return [{name: one(name, qw) for name, qw in layer.items()} for layer in layers]
 
@@ -495,23 +501,27 @@ def run(n_layers: int = 32, group_size: int = 128, trials: int = 10, glue_pos: i
            "roofline_tok_s": round(H.HBM_PEAK_GBPS * 1e9 / nbytes, 1)}
     if "projections" in want:
         res["projections"] = measure(layers, trials)
-    if want & {"projections_strips", "persistent_projections"}:
+    # Launch variants run on copies at the launches' widths, chain variants on
+    # copies at the chain's: a model converts its one copy for the path it runs.
+    if "projections_strips" in want:
         ps = strips(layers)
-        if "projections_strips" in want:
-            res["projections_strips"] = measure(ps, trials)
-        if "persistent_projections" in want:
-            res["persistent_projections"] = measure_persistent(ps, trials, with_stages=with_stages)
+        res["projections_strips"] = measure(ps, trials)
+        del ps
+    if "persistent_projections" in want:
+        ps = strips(layers, chain=True)
+        res["persistent_projections"] = measure_persistent(ps, trials, with_stages=with_stages)
         del ps
     if want & {"fused", "fused_strips", "persistent"}:
         fused = [fuse(layer) for layer in layers]
         if "fused" in want:
             res["fused"] = measure(fused, trials)
-        if want & {"fused_strips", "persistent"}:
+        if "fused_strips" in want:
             fs = strips(fused)
-            if "fused_strips" in want:
-                res["fused_strips"] = measure(fs, trials)
-            if "persistent" in want:
-                res["persistent"] = measure_persistent(fs, trials, with_stages=with_stages)
+            res["fused_strips"] = measure(fs, trials)
+            del fs
+        if "persistent" in want:
+            fs = strips(fused, chain=True)
+            res["persistent"] = measure_persistent(fs, trials, with_stages=with_stages)
             del fs
         del fused
     swiglu_want = {"fused_swiglu", "glue", "fused_swiglu_strips", "glue_strips",
@@ -524,6 +534,9 @@ def run(n_layers: int = 32, group_size: int = 128, trials: int = 10, glue_pos: i
         if "glue" in want and glue_pos >= 0:
             res["glue"] = measure_glue(swiglu, glue_pos, trials)
         if want & (swiglu_want - {"fused_swiglu", "glue"}):
+            # The dependent data-flow chain stays on the launches' widths: each
+            # of its stages waits for the one before, so a stage's strip count
+            # sets how many CUs share it (32-column o and down: 1.628 -> 1.647 ms).
             swiglu_strips = strips(swiglu)
             del swiglu
             if "fused_swiglu_strips" in want:

@@ -605,8 +605,10 @@ class QuantLinear(torch.nn.Module):
 
     def prepare_decode(self, strip_cols: int = 0) -> "QuantLinear":
         """Convert the weight to the strip-major layout on its GPU, in place
-        (``strip_cols`` 0 picks :func:`strip_major_cols`); returns the
-        module.  The packed copy is released once converted."""
+        (``strip_cols`` 0 picks :func:`strip_major_cols`, the launches'
+        width; :func:`nibblegemm_amd.chain.chain_strip_cols` gives the width
+        a decode chain streams fastest); returns the module.  The packed copy
+        is released once converted."""
         if self.strip_cols:
             if strip_cols in (0, self.strip_cols):
                 return self

@@ -118,6 +118,47 @@ def _run(chain: C.DecodeChain):
     return [y.clone() for y in chain.outputs()]
 
 
+@pytest.mark.parametrize("K,N,g,M,want", [
+    (14336, 4096, 128, 1, 32),   # down: 16-column launches, 32-column chain rounds
+    (4096, 4096, 128, 1, 32),    # o
+    (4096, 1024, 128, 1, 32),    # k, v
+    (4096, 6144, 128, 1, 32),    # q|k|v: already the launches' width
+    (4096, 28672, 128, 1, 64),   # gate|up keeps the launches' 64
+    (4096, 1024, 64, 1, 32),
+    (4096, 16, 128, 1, 16),      # 16 columns hold no 32-column strip
+    (14336, 4096, 128, 2, 0),    # two rows of K = 14336 exceed the LDS at any width
+    (4096, 4096, 128, 8, 0),
+    (4096, 4096, 128, 9, 0),     # chains serve 1..8 rows
+    (4096, 40, 128, 1, 0),       # no strip-major layout
+])
+def test_chain_strip_width(K, N, g, M, want):
+    assert C.chain_strip_cols(K, N, g, M) == want
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("K,N,M", [(14336, 4096, 1), (4096, 4096, 1), (4096, 1024, 2),
+                                   (4096, 28672, 1), (14336, 4096, 2), (4096, 4096, 8)])
+def test_chain_strip_width_agrees_with_the_plan(K, N, M):
+    """A one-stage chain accepts the width the query gives; where the query
+    gives 0, the launches' width is rejected for its LDS."""
+    gen = torch.Generator().manual_seed(K + N + M)
+    codes = torch.randint(0, 16, (K, N), generator=gen, dtype=torch.uint8).numpy()
+    scales = (torch.rand((K // 128, N), generator=gen) * 0.01 + 0.001).to(torch.float16)
+    qw = quant.QuantizedWeight(torch.from_numpy(quant.pack_nibbles(codes)).cuda(), scales.cuda(),
+                               128, K, N)
+    X = torch.randn((M, K), generator=gen).to(torch.float16).cuda()
+    sw = C.chain_strip_cols(K, N, 128, M)
+    if sw:
+        sm = ng.to_strip_major(qw, sw)
+        chain = C.DecodeChain([C.stage(X, sm)], M=M)
+        got = _run(chain)[0]
+        assert torch.equal(got, ng.matmul(X, sm))
+        chain.close()
+    else:
+        with pytest.raises(RuntimeError, match="bytes of LDS"):
+            C.DecodeChain([C.stage(X, ng.to_strip_major(qw, ng.strip_major_cols(K, N, 128)))], M=M)
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("M", [1, 2, 5, 8])
 def test_independent_stages_have_the_strip_launch_bits(M):
@@ -245,11 +286,16 @@ def test_timestamps_follow_the_dependencies():
 
 
 @pytest.mark.gpu
-def test_persistent_step_matches_the_fused_launches():
+@pytest.mark.parametrize("chain_widths", [False, True])
+def test_persistent_step_matches_the_fused_launches(chain_widths):
     """The reference-semantics step (independent projections) of two full
-    layers as one chain: the bits of the fused strip-major launches."""
+    layers as one chain: the bits of the fused strip-major launches on the
+    same copy, at the launches' strip widths or at the chain's."""
     built = D.build_layers(2, seed=8)
-    fs = D.strips([D.fuse(layer) for layer in built])
+    fs = D.strips([D.fuse(layer) for layer in built], chain=chain_widths)
+    widths = {name: w.strip_cols for name, w in fs[0].items()}
+    assert widths == ({"qkv": 32, "o": 32, "gate_up": 64, "down": 32} if chain_widths
+                      else {"qkv": 32, "o": 16, "gate_up": 64, "down": 16})
     launches = D.DecodeStep(fs)
     chain = C.DecodeChain(D.chain_stages(fs, launches.acts))
     got = D.ChainStep(chain, D.weight_bytes(fs)).outputs()
