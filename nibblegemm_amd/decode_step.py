@@ -419,8 +419,9 @@ def stage_times(chain: DecodeChain, names: List[str], runs: int = 5) -> dict:
     projection name (the layer's stages in order), the median over ``runs``
     of the mean over layers of the time from the end of the stage before it
     to its own end, in us (its effective time in the step), and the step's
-    total.  Eager runs after a warm-up."""
-    chain.run()
+    total.  Eager runs after ~50 ms of untimed ones (:func:`harness.keep_busy`),
+    so they start at the loaded clock."""
+    H.keep_busy(chain.run, 0.05)
     chain.check()
     per = {n: [] for n in names}
     totals = []
