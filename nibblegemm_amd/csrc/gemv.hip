@@ -502,13 +502,14 @@ __device__ __forceinline__ void copy_window(const void* X, uint32_t xbytes, unsi
 }
 
 // Batch kernel: 12 to 64 activation rows (small batches through gemm) in one
-// block of MT = 16, 32 or 64 rows.  The split kernel's geometry -- one workgroup
-// per 64-column strip and K split, its 4 waves taking the split's quant
-// groups round-robin -- and its arithmetic: per group the same pre-scaled
-// activations, correction MFMA, decode and MFMA sequence, the same
-// per-group scaling into fp32 totals, the same wave and split reduction
-// order.  A launch with the split kernel's plan returns the split kernel's
-// bits.
+// block of MT = 16, 32 or 64 rows.  The split kernel's geometry -- one
+// workgroup per 64-column strip and K split, its 4 waves taking the split's
+// quant groups round-robin (SPW = 2: a workgroup takes two adjacent strips,
+// 4 waves each, sharing the activation copies) -- and its arithmetic: per
+// group the same pre-scaled activations, correction MFMA, decode and MFMA
+// sequence, the same per-group scaling into fp32 totals, the same wave and
+// split reduction order.  A launch with the split kernel's plan returns the
+// split kernel's bits.
 //
 // What differs is where the activations come from.  The split kernel loads
 // a 16-byte activation chunk per lane per MFMA -- 2 x GROUP / 32 loads per
@@ -544,11 +545,13 @@ __device__ __forceinline__ void copy_window(const void* X, uint32_t xbytes, unsi
 // 64-78% busy, half of that stalled by the L1.  The copies here are whole
 // 1 KiB rows issued by STAGERS waves that do nothing else, so they flow
 // beside the weight loads instead of in the compute waves' own queues.
-template <int MT, int GROUP, int DEPTH, int RING, int STAGERS, bool STREAM>
-__global__ __launch_bounds__((4 + STAGERS) * 64) void gemv_batch_kernel(GemvArgs a) {
+template <int MT, int GROUP, int DEPTH, int RING, int STAGERS, bool STREAM, int SPW = 1>
+__global__ __launch_bounds__((4 * SPW + STAGERS) * 64) void gemv_batch_kernel(GemvArgs a) {
   static_assert(MT == 16 || MT == 32 || MT == 64, "16-row MFMA tiles");
-  constexpr int kWaves = 4;
-  constexpr int THREADS = (kWaves + STAGERS) * 64;
+  static_assert(SPW == 1 || (SPW == 2 && MT != 64), "strips per workgroup: 1, or 2 below 64 rows");
+  constexpr int kWaves = 4;                // group waves: the quant groups of one step
+  constexpr int kCompute = kWaves * SPW;   // compute waves: kWaves per strip
+  constexpr int THREADS = (kCompute + STAGERS) * 64;
   constexpr int kWPolicy = STREAM ? 2 : 0;
   constexpr int kPolicySc1 = 16;                  // agent-coherent: misses a stale L2 line
   constexpr int CPG = GROUP / 32;
@@ -560,14 +563,19 @@ __global__ __launch_bounds__((4 + STAGERS) * 64) void gemv_batch_kernel(GemvArgs
   constexpr int QUADS = kStripCols / 4;
   static_assert(UPR >= 16 && (MT * UPR) % (64 * STAGERS) == 0, "swizzle within a row, whole copies");
   static_assert(RING >= 2 && WAIT_X <= 63, "vmcnt range");
-  static_assert(kWaves * MT * 16 * 16 <= RING * SLOT_BYTES, "the wave totals fit the ring");
+  static_assert(SPW * kWaves * MT * 16 * 16 <= RING * SLOT_BYTES, "the wave totals fit the ring");
   extern __shared__ __attribute__((aligned(16))) unsigned char ring[];
   __shared__ int s_last;
 
   const uint32_t lane = threadIdx.x & 63u;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const bool stager = wave >= kWaves;
-  const int strip = blockIdx.x;
+  const bool stager = wave >= kCompute;
+  // Compute wave w takes group slot gw of every step in strip sp of the
+  // workgroup's SPW adjacent strips; the activation window is copied once for
+  // all of them.
+  const int gw = wave % kWaves, sp = stager ? 0 : wave / kWaves;
+  const int tile = blockIdx.x;
+  const int strip = tile * SPW + sp;
   const int split = blockIdx.y;
   const int m_base = blockIdx.z * MT;
   const int mrows = min(MT, a.M - m_base);
@@ -594,14 +602,14 @@ __global__ __launch_bounds__((4 + STAGERS) * 64) void gemv_batch_kernel(GemvArgs
     uint32_t dma_k[COPIES], dma_row[COPIES];
 #pragma unroll
     for (int j = 0; j < COPIES; ++j) {
-      const uint32_t e = static_cast<uint32_t>((wave - kWaves) * COPIES + j) * 64u + lane;
+      const uint32_t e = static_cast<uint32_t>((wave - kCompute) * COPIES + j) * 64u + lane;
       const uint32_t r = e / UPR, pos = e % UPR;
       dma_k[j] = 8u * (pos ^ (r & 15u));
       dma_row[j] = static_cast<int>(r) < mrows ? (static_cast<uint32_t>(m_base) + r) * K * 2u
                                                : kOutOfRange;
     }
     auto copy = [&](int step, uint32_t slot) {
-      copy_window<COPIES>(a.X, xbytes, ring + slot * SLOT_BYTES + (wave - kWaves) * COPIES * 1024,
+      copy_window<COPIES>(a.X, xbytes, ring + slot * SLOT_BYTES + (wave - kCompute) * COPIES * 1024,
                           static_cast<uint32_t>(gb + step * kWaves) * GROUP, K, dma_k, dma_row);
     };
 #pragma unroll
@@ -630,7 +638,7 @@ __global__ __launch_bounds__((4 + STAGERS) * 64) void gemv_batch_kernel(GemvArgs
       h4_t s;
     };
     auto load = [&](WStage& st, int step) {
-      const int g = gb + step * kWaves + wave;
+      const int g = gb + step * kWaves + gw;
       const bool in = step < steps && g < ge;
       const uint32_t vw = in ? voff_w : kOutOfRange;
       const uint32_t kw = in ? static_cast<uint32_t>(g) * (GROUP / 8) * row_bytes : 0u;
@@ -663,7 +671,7 @@ __global__ __launch_bounds__((4 + STAGERS) * 64) void gemv_batch_kernel(GemvArgs
 #pragma unroll
       for (int c = 0; c < CPG; ++c) {
         h8_t xs[TILES];
-        const uint32_t u = static_cast<uint32_t>(wave * (GROUP / 8) + 4 * c) + kb;
+        const uint32_t u = static_cast<uint32_t>(gw * (GROUP / 8) + 4 * c) + kb;
 #pragma unroll
         for (int t = 0; t < TILES; ++t) {
           const uint32_t r = 16u * t + q;
@@ -700,7 +708,7 @@ __global__ __launch_bounds__((4 + STAGERS) * 64) void gemv_batch_kernel(GemvArgs
         f4_t corr = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int c = 0; c < CPG; ++c) {
-          const uint32_t u = static_cast<uint32_t>(wave * (GROUP / 8) + 4 * c) + kb;
+          const uint32_t u = static_cast<uint32_t>(gw * (GROUP / 8) + 4 * c) + kb;
           xs[t][c] = *reinterpret_cast<const h8_t*>(base + (r * UPR + (u ^ q)) * 16u) * xscale;
           corr = mfma16(xs[t][c], bcorr, corr);
         }
@@ -734,7 +742,7 @@ __global__ __launch_bounds__((4 + STAGERS) * 64) void gemv_batch_kernel(GemvArgs
     uint32_t slot = 0;  // step i's slot: i % RING
     auto step = [&](WStage& sd, int i) {
       lds_barrier();  // B(i)
-      if (gb + i * kWaves + wave < ge) compute(sd, ring + slot * SLOT_BYTES);
+      if (gb + i * kWaves + gw < ge) compute(sd, ring + slot * SLOT_BYTES);
       __builtin_amdgcn_sched_barrier(0);
       load(sd, i + DEPTH);
       slot = slot == RING - 1 ? 0 : slot + 1;
@@ -753,8 +761,8 @@ __global__ __launch_bounds__((4 + STAGERS) * 64) void gemv_batch_kernel(GemvArgs
   }
   lds_barrier();  // every copy has landed and every slot read is done
 
-  // Lane (q, kb) of compute wave w holds rows 16 t + 4 kb + i of columns
-  // 4 q + j: red[w][row][q], summed over the waves in order.
+  // Lane (q, kb) of compute wave (sp, gw) holds rows 16 t + 4 kb + i of
+  // columns 4 q + j of strip sp: red[sp][gw][row][q], summed over gw in order.
   f4_t* const red = reinterpret_cast<f4_t*>(ring);
   if (!stager) {
 #pragma unroll
@@ -762,14 +770,15 @@ __global__ __launch_bounds__((4 + STAGERS) * 64) void gemv_batch_kernel(GemvArgs
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int r = 16 * t + 4 * static_cast<int>(kb) + i;
-        red[(wave * MT + r) * 16 + q] = f4_t{tot[t][0][i], tot[t][1][i], tot[t][2][i], tot[t][3][i]};
+        red[((sp * kWaves + gw) * MT + r) * 16 + q] =
+            f4_t{tot[t][0][i], tot[t][1][i], tot[t][2][i], tot[t][3][i]};
       }
   }
   __syncthreads();
-  auto wave_sum = [&](int r, int qq) {
+  auto wave_sum = [&](int s, int r, int qq) {
     f4_t v[kWaves];
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) v[w] = red[(w * MT + r) * 16 + qq];
+    for (int w = 0; w < kWaves; ++w) v[w] = red[((s * kWaves + w) * MT + r) * 16 + qq];
     __builtin_amdgcn_sched_barrier(0);
     f4_t sum = v[0];
 #pragma unroll
@@ -782,7 +791,10 @@ __global__ __launch_bounds__((4 + STAGERS) * 64) void gemv_batch_kernel(GemvArgs
     return sum;
   };
   if (a.splits == 1) {
-    emit_outputs<MT, THREADS>(a, strip, m_base, mrows, wave_sum);
+#pragma unroll
+    for (int s = 0; s < SPW; ++s)
+      emit_outputs<MT, THREADS>(a, tile * SPW + s, m_base, mrows,
+                                [&](int r, int qq) { return wave_sum(s, r, qq); });
     return;
   }
   // The split kernel's publication and last-workgroup reduction ("HARDWARE
@@ -791,19 +803,26 @@ __global__ __launch_bounds__((4 + STAGERS) * 64) void gemv_batch_kernel(GemvArgs
   const uint32_t pbytes = static_cast<uint32_t>(a.splits) * static_cast<uint32_t>(a.M) *
                           static_cast<uint32_t>(a.N) * 4u;
   const __amdgpu_buffer_rsrc_t rp = make_rsrc(a.partial, pbytes);
-  auto poff = [&](int sp, int r, int qq) {
-    return ((static_cast<uint32_t>(sp) * a.M + m_base + r) * static_cast<uint32_t>(a.N) +
-            strip * kStripCols + 4 * qq) * 4u;
+  // Element e of the workgroup's outputs: strip e / (MT QUADS), then row and
+  // column quad.
+  auto poff = [&](int spl, int e) {
+    const int s = e / (MT * QUADS), r = e % (MT * QUADS) / QUADS, qq = e % QUADS;
+    return ((static_cast<uint32_t>(spl) * a.M + m_base + r) * static_cast<uint32_t>(a.N) +
+            (tile * SPW + s) * kStripCols + 4 * qq) * 4u;
   };
-  for (int e = threadIdx.x; e < MT * QUADS; e += THREADS) {
-    const int r = e / QUADS, qq = e % QUADS;
-    if (r >= mrows || strip * kStripCols + 4 * qq >= a.N) continue;
-    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4_t, wave_sum(r, qq)), rp,
-                                           poff(split, r, qq), 0, kPolicySc1);
+  auto in_range = [&](int e) {
+    const int s = e / (MT * QUADS), r = e % (MT * QUADS) / QUADS, qq = e % QUADS;
+    return e < SPW * MT * QUADS && r < mrows && (tile * SPW + s) * kStripCols + 4 * qq < a.N;
+  };
+  for (int e = threadIdx.x; e < SPW * MT * QUADS; e += THREADS) {
+    if (!in_range(e)) continue;
+    const int s = e / (MT * QUADS), r = e % (MT * QUADS) / QUADS, qq = e % QUADS;
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4_t, wave_sum(s, r, qq)), rp,
+                                           poff(split, e), 0, kPolicySc1);
   }
   wait_vm_stores();
   __syncthreads();
-  uint32_t* counter = a.counters + blockIdx.z * gridDim.x + strip;
+  uint32_t* counter = a.counters + blockIdx.z * gridDim.x + tile;
   if (threadIdx.x == 0) {
     const uint32_t prev =
         __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -811,9 +830,9 @@ __global__ __launch_bounds__((4 + STAGERS) * 64) void gemv_batch_kernel(GemvArgs
   }
   __syncthreads();
   if (!s_last) return;
-  constexpr int PER = (MT * QUADS + THREADS - 1) / THREADS;
+  constexpr int PER = (SPW * MT * QUADS + THREADS - 1) / THREADS;
   constexpr int kSplitBatch = 8;
-  f4_t* const sums = red;  // [MT][QUADS]
+  f4_t* const sums = red;  // [SPW][MT][QUADS]
   f4_t acc[PER];
 #pragma unroll
   for (int k = 0; k < PER; ++k) acc[k] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
@@ -822,13 +841,12 @@ __global__ __launch_bounds__((4 + STAGERS) * 64) void gemv_batch_kernel(GemvArgs
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
       const int e = threadIdx.x + k * THREADS;
-      const int r = e / QUADS, qq = e % QUADS;
-      const bool ok = e < MT * QUADS && r < mrows && strip * kStripCols + 4 * qq < a.N;
+      const bool ok = in_range(e);
 #pragma unroll
       for (int b = 0; b < kSplitBatch; ++b)
         v[k][b] = __builtin_bit_cast(
             f4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                      rp, ok && sp0 + b < a.splits ? poff(sp0 + b, r, qq) : kOutOfRange, 0,
+                      rp, ok && sp0 + b < a.splits ? poff(sp0 + b, e) : kOutOfRange, 0,
                       kPolicySc1));
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -846,11 +864,13 @@ __global__ __launch_bounds__((4 + STAGERS) * 64) void gemv_batch_kernel(GemvArgs
 #pragma unroll
   for (int k = 0; k < PER; ++k) {
     const int e = threadIdx.x + k * THREADS;
-    if (e < MT * QUADS) sums[e] = acc[k];
+    if (e < SPW * MT * QUADS) sums[e] = acc[k];
   }
   __syncthreads();
-  emit_outputs<MT, THREADS>(a, strip, m_base, mrows,
-                            [&](int r, int qq) { return sums[r * QUADS + qq]; });
+#pragma unroll
+  for (int s = 0; s < SPW; ++s)
+    emit_outputs<MT, THREADS>(a, tile * SPW + s, m_base, mrows,
+                              [&](int r, int qq) { return sums[(s * MT + r) * QUADS + qq]; });
   if (threadIdx.x == 0)
     __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -1396,28 +1416,40 @@ hipError_t launch_strip_group(const GemvArgs& a, const StreamPlan& p, hipStream_
   }
 }
 
-// The batch kernel: 4 compute waves and a staging wave, RING activation
-// slots of 32 rows x (4 x GROUP) k in dynamic LDS (96 KiB at GROUP = 128).
-template <int MT, int GROUP>
+// The batch kernel: 4 compute waves per strip (SPW strips per workgroup) and
+// kBatchStagers staging waves, RING activation slots of MT rows x (4 x GROUP)
+// k in dynamic LDS (96 KiB at 32 rows and GROUP = 128).
+template <int MT, int GROUP, int SPW = 1>
 hipError_t launch_batch_rows(const GemvArgs& a, const StreamPlan& p, hipStream_t stream) {
   // 64-row slots (64 KiB at GROUP = 128) leave room for 2.
   constexpr int kRing = MT == 64 ? 2 : kBatchRing;
   constexpr size_t kSlots = static_cast<size_t>(kRing) * MT * (4 * GROUP / 8) * 16;
-  constexpr size_t kTotals = static_cast<size_t>(4) * MT * 16 * 16;
+  constexpr size_t kTotals = static_cast<size_t>(SPW) * 4 * MT * 16 * 16;
   constexpr size_t kLds = kSlots > kTotals ? kSlots : kTotals;
   static_assert(kLds + 256 <= 160 * 1024, "a workgroup holds at most 160 KiB of LDS");
-  const dim3 grid(p.strips, p.splits, p.mblocks);
-  constexpr int kThreads = (4 + kBatchStagers) * 64;
+  const dim3 grid(static_cast<unsigned>(ceil_div(p.strips, SPW)), p.splits, p.mblocks);
+  constexpr int kThreads = (4 * SPW + kBatchStagers) * 64;
   if (p.mblocks == 1)
-    gemv_batch_kernel<MT, GROUP, kBatchDepth, kRing, kBatchStagers, true><<<grid, kThreads, kLds, stream>>>(a);
+    gemv_batch_kernel<MT, GROUP, kBatchDepth, kRing, kBatchStagers, true, SPW>
+        <<<grid, kThreads, kLds, stream>>>(a);
   else
-    gemv_batch_kernel<MT, GROUP, kBatchDepth, kRing, kBatchStagers, false><<<grid, kThreads, kLds, stream>>>(a);
+    gemv_batch_kernel<MT, GROUP, kBatchDepth, kRing, kBatchStagers, false, SPW>
+        <<<grid, kThreads, kLds, stream>>>(a);
   return hipGetLastError();
 }
 
 template <int GROUP>
 hipError_t launch_batch_group(const GemvArgs& a, const StreamPlan& p, hipStream_t stream) {
   if (p.waves != 4 || p.depth != kBatchDepth || p.ring != kBatchRing) return hipErrorInvalidValue;
+  if (p.pair == 2) {
+    // Two strips' totals need the 128-row-group ring (planned at GROUP = 128 only).
+    if constexpr (GROUP == 128) {
+      if (p.splits != 1 || p.mblocks != 1) return hipErrorInvalidValue;
+      if (p.mt == 16) return launch_batch_rows<16, GROUP, 2>(a, p, stream);
+      if (p.mt == 32) return launch_batch_rows<32, GROUP, 2>(a, p, stream);
+    }
+    return hipErrorInvalidValue;
+  }
   switch (p.mt) {
     case 16: return launch_batch_rows<16, GROUP>(a, p, stream);
     case 32: return launch_batch_rows<32, GROUP>(a, p, stream);
@@ -1582,6 +1614,17 @@ int plan_stream(int64_t M, int64_t K, int64_t N, int64_t G, bool split_k, int64_
   p->kernel = kBatchKernel;
   p->depth = kBatchDepth;
   p->ring = kBatchRing;
+  // Where pairs of adjacent strips still make one round of the CUs without a
+  // K split, a workgroup takes a pair and copies the activation window once
+  // for both (same arithmetic per output, so the same bits).  Measured on
+  // MI355X, graph replay, 4096 x 28672: M = 17 / 32 18.9 / 20.4 -> 16.7 /
+  // 17.5 us.  Where the pairs would need a K split to fill the CUs, the split
+  // epilogue costs more than the halved copies save (4096 x 14336 M = 32
+  // 11.1 -> 14.0 us with 2 splits).
+  const int64_t pairs = ceil_div(p->strips, 2);
+  if (p->splits == 1 && rows != 64 && G == 128 && pairs >= kBatch64MinWorkgroups &&
+      pairs <= kBatchWorkgroups)
+    p->pair = 2;
   return rc;
 }
 

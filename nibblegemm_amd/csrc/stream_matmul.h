@@ -88,6 +88,7 @@ struct StreamPlan {
   int strip_cols = 64;  // strip kernel: 16, 32 or 64
   int depth = 2;        // strip / batch kernel: groups (steps) of weight loads in flight per wave
   int ring = 3;         // batch kernel: LDS activation slots
+  int pair = 1;         // batch kernel: adjacent strips per workgroup (1 or 2)
   bool stage_x = true;  // strip kernel: activations copied to LDS (when they fit 64 KiB)
   size_t counter_bytes = 0;
   size_t workspace_bytes = 0;

@@ -21,7 +21,8 @@ pytestmark = pytest.mark.gpu
 
 SHAPES = [(1, 4096, 1024, 128), (4, 512, 260, 64), (8, 14336, 512, 128), (16, 1024, 4100, 128),
           (12, 4096, 14336, 128), (100, 2048, 640, 64), (128, 8192, 384, 128),
-          (64, 14336, 4096, 128), (17, 14336, 4096, 128), (24, 4096, 1028, 64), (32, 4096, 14336, 128)]
+          (64, 14336, 4096, 128), (17, 14336, 4096, 128), (24, 4096, 1028, 64), (32, 4096, 14336, 128),
+          (24, 4096, 28672, 128)]
 
 
 @pytest.mark.parametrize("M,K,N,g", SHAPES)
@@ -35,7 +36,8 @@ def test_bias_epilogue_is_the_separate_add(M, K, N, g):
 
 
 SWIGLU = [(1, 4096, 1024, 128), (8, 14336, 512, 128), (16, 4096, 14336, 128), (33, 1024, 320, 64),
-          (128, 2048, 96, 128), (48, 4096, 14336, 128), (24, 4096, 4096, 128), (32, 2048, 640, 64)]
+          (128, 2048, 96, 128), (48, 4096, 14336, 128), (24, 4096, 4096, 128), (32, 2048, 640, 64),
+          (20, 4096, 14336, 128)]
 
 
 @pytest.mark.parametrize("M,K,Nh,g", SWIGLU)

@@ -19,6 +19,7 @@ import pytest
 import torch
 
 import nibblegemm_amd as ng
+from nibblegemm_amd import quant
 from cases import host, oracle_y, oracle_y_rows, quantized, rel_err, rms_err, synthetic, to_dev_qw
 
 pytestmark = pytest.mark.gpu
@@ -121,6 +122,49 @@ def test_batch_64_row_block_against_the_oracle(M):
     ref = oracle_y(X, packed, scales, 14336, 128)
     assert rms_err(y, ref) <= RMS_TOL
     assert rel_err(y, ref) < REL_TOL
+
+
+@pytest.mark.parametrize("M,K_,N", [(17, 4096, 28672), (32, 4096, 28672), (24, 4096, 30720),
+                                    (20, 4096, 28736), (24, 4096, 32768)])
+def test_batch_strip_pairs(M, K_, N):
+    """Where pairs of adjacent strips make one round of the CUs without a K
+    split (448..512 strips), a workgroup takes a pair and copies the
+    activation window once for both.  Each output keeps its arithmetic: the
+    result has the bits of the two column halves computed apart (a cut
+    mid-strip included), matches the oracle (the fused gate|up shape) or an
+    fp32 product of the dequant kernel's weights, repeats its bits, and
+    replays from a graph.  28736 columns end in an unpaired strip."""
+    ext = ng.extension()
+    assert ext.gemm_workspace_bytes(M, K_, N, 128, 6, None) == (0, 0)  # no K split
+    X, packed, scales, Xd, qw = synthetic(M, K_, N, 128, seed=900 + M + N)
+    y = ng.gemm(Xd, qw)
+    assert torch.equal(ng.gemm(Xd, qw), y)
+    half = N // 2
+    parts = [ng.gemm(Xd, quant.QuantizedWeight(qw.qweight[:, a:b].contiguous(),
+                                               qw.scales[:, a:b].contiguous(), 128, K_, b - a))
+             for a, b in ((0, half), (half, N))]
+    assert torch.equal(torch.cat(parts, dim=1), y)
+    if N == 28672:
+        ref = oracle_y(X, packed, scales, K_, 128)
+        assert rms_err(host(y), ref) <= RMS_TOL
+        assert rel_err(host(y), ref) < REL_TOL
+    else:
+        ref = Xd.float() @ ng.dequant(qw).float()
+        assert float((y.float() - ref).abs().max() / ref.pow(2).mean().sqrt()) <= RMS_TOL
+    graph = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ng.gemm(Xd, qw)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        out = ng.gemm(Xd, qw)
+    for _ in range(3):
+        out.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, y)
 
 
 @pytest.mark.parametrize("M,K_,N,g", [(24, 14336, 4096, 128), (17, 4096, 1024, 128), (32, 2048, 1540, 64),
