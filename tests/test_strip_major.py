@@ -295,8 +295,12 @@ def test_batches_above_8_have_the_packed_bits(M, K, N):
 @pytest.mark.gpu
 @pytest.mark.parametrize("M,K,N,g,sw", [(9, 1024, 448, 128, 16), (40, 2048, 512, 64, 32),
                                         (200, 4096, 1024, 128, 16), (100, 1024, 4096, 64, 64),
-                                        (1000, 4096, 4096, 128, 32), (16, 4096, 28672, 128, 64)])
+                                        (1000, 4096, 4096, 128, 32), (16, 4096, 28672, 128, 64),
+                                        (24, 4096, 28672, 128, 64), (32, 4096, 28672, 128, 32)])
 def test_every_width_above_8_rows_has_the_packed_bits(M, K, N, g, sw):
+    """Every strip width from 9 rows: the packed weight's bits, with and
+    without the bias epilogue (4096 x 28672 at 24 and 32 rows takes strip
+    pairs in the batch kernel)."""
     _, _, _, Xd, qw, sm = strip_case(M, K, N, g, sw, seed=sw + M)
     assert torch.equal(ng.matmul(Xd, sm), ng.matmul(Xd, qw))
     bias = (torch.randn(N, generator=torch.Generator().manual_seed(2)) * 0.3).half().cuda()
