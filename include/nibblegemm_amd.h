@@ -359,13 +359,14 @@ NIBBLE_API int nibble_chain_check(void* chain, void* stream);
 NIBBLE_API int64_t nibble_chain_info(void* chain, int64_t what);
 NIBBLE_API int nibble_chain_destroy(void* chain);
 /* The strip width at which a chain of independent M-row stages streams a
- * [K, N] weight fastest: at least 32 columns where a one-stage chain of it has a plan
- * (the LDS of the chain grows with K and the strip's scales), else
- * nibble_strip_major_cols's width; 0 when neither has a chain plan.  A chain
- * round costs a fixed allowance besides its bytes, so the chain wants fewer,
- * wider strips than the per-projection launches, which want a workgroup per
- * CU.  A weight converted at either width serves both.  Pure host
- * computation. */
+ * [K, N] weight fastest: the widest of 64 and 32 columns for which a
+ * one-stage chain of it has a plan (the LDS of the chain grows with K and
+ * the strip's scales), else nibble_strip_major_cols's width; 0 when none has
+ * a chain plan.  A chain round costs a fixed allowance besides its bytes, so
+ * a chain of many stages wants fewer, wider strips than the per-projection
+ * launches, which want a workgroup per CU (a chain of one narrow weight may
+ * want more strips than this gives).  A weight converted at either width
+ * serves both.  Pure host computation. */
 NIBBLE_API int64_t nibble_chain_strip_cols(int64_t K, int64_t N, int64_t group_size, int64_t M);
 
 /*

@@ -45,12 +45,13 @@ _STAGE = struct.Struct("<5Q6q")
 
 def chain_strip_cols(K: int, N: int, group_size: int, M: int = 1) -> int:
     """The strip width a chain of independent ``M``-row stages streams a
-    ``[K, N]`` weight fastest at (``nibble_chain_strip_cols``): at least 32 columns where
-    the chain has a plan for them, else :func:`~nibblegemm_amd.ops.strip_major_cols`'s
-    width; 0 when neither fits a chain.  A chain round costs a fixed
-    allowance besides its bytes, so chains want fewer, wider strips than the
-    per-projection launches do; a weight converted at either width serves
-    both (``ops.to_strip_major(qw, chain_strip_cols(...))``)."""
+    ``[K, N]`` weight fastest at (``nibble_chain_strip_cols``): the widest of
+    64 and 32 columns the chain has a plan for, else
+    :func:`~nibblegemm_amd.ops.strip_major_cols`'s width; 0 when none fits a
+    chain.  A chain round costs a fixed allowance besides its bytes, so a
+    chain of many stages wants fewer, wider strips than the per-projection
+    launches do; a weight converted at either width serves both
+    (``ops.to_strip_major(qw, chain_strip_cols(...))``)."""
     return int(_native.binding().chain_strip_cols(K, N, group_size, M))
 
 

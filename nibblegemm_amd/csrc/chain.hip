@@ -876,13 +876,17 @@ using namespace nibble;
 
 extern "C" int64_t nibble_chain_strip_cols(int64_t K, int64_t N, int64_t group_size, int64_t M) {
   // A chain round costs a fixed allowance (barriers, partial sums, stores)
-  // besides its bytes, so fewer, wider strips win: at least 32 columns where
-  // the chain has a plan for them, else the launches' width.
+  // besides its bytes, so fewer, wider strips win: the widest of 64 and 32
+  // columns the chain has a plan for, else the launches' width.  Measured on
+  // MI355X, the 8B step as one chain: 0.585 -> 0.552 ms per token with o and
+  // down in 32-column strips instead of 16 (64-column o and q|k|v: the same;
+  // 64-column down does not fit the LDS); at one GPU's share of an 8-way
+  // split 0.124 ms with every weight in 32-column strips, 0.085 in 64.
   const int64_t base = strip_major_cols(K, N, group_size);
   if (base == 0 || M < 1 || M > 8) return 0;
-  const int64_t wide = std::max<int64_t>(base, 32);
-  if (wide != base && chain_fits(M, K, N, group_size, wide)) return wide;
-  return chain_fits(M, K, N, group_size, base) ? base : 0;
+  for (const int64_t sw : {int64_t(64), int64_t(32), base})
+    if (chain_fits(M, K, N, group_size, sw)) return sw;
+  return 0;
 }
 
 extern "C" int nibble_chain_create(const nibble_chain_stage* stages, int64_t n_stages, int64_t M,

@@ -150,9 +150,9 @@ def fuse(layer: Dict[str, QuantizedWeight], swiglu: bool = False) -> Dict[str, Q
 def strips(layers: List[Dict[str, QuantizedWeight]], chain: bool = False) -> list:
     """Strip-major copies of every weight, each at the width the launches
     stream fastest (``strip_major_cols``) or, with ``chain``, the width a
-    decode chain does (``chain_strip_cols``: at least 32 columns where they
-    fit; MI355X, 8B step as one chain, 0.585 -> 0.552 ms with o and down at
-    32 columns instead of 16, while the 128 launches go 0.892 -> 0.955 ms).
+    decode chain does (``chain_strip_cols``: 64 or 32 columns where they fit;
+    MI355X, 8B step as one chain, 0.585 -> 0.552 ms with o and down at 32
+    columns instead of 16, while the 128 launches go 0.892 -> 0.955 ms).
     The SwiGLU weight takes at least 32 columns either way: its strips must
     hold whole gate|up block pairs."""
     def one(name, qw):

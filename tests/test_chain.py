@@ -119,12 +119,14 @@ def _run(chain: C.DecodeChain):
 
 
 @pytest.mark.parametrize("K,N,g,M,want", [
-    (14336, 4096, 128, 1, 32),   # down: 16-column launches, 32-column chain rounds
-    (4096, 4096, 128, 1, 32),    # o
-    (4096, 1024, 128, 1, 32),    # k, v
-    (4096, 6144, 128, 1, 32),    # q|k|v: already the launches' width
-    (4096, 28672, 128, 1, 64),   # gate|up keeps the launches' 64
-    (4096, 1024, 64, 1, 32),
+    (14336, 4096, 128, 1, 32),   # down: 64-column strips of K = 14336 exceed the LDS
+    (4096, 4096, 128, 1, 64),    # o (the launches: 16)
+    (4096, 1024, 128, 1, 64),    # k, v
+    (4096, 6144, 128, 1, 64),    # q|k|v (the launches: 32)
+    (4096, 28672, 128, 1, 64),   # gate|up: already the launches' 64
+    (4096, 1024, 64, 1, 64),
+    (1792, 4096, 128, 1, 64),    # down at one GPU's share of an 8-way split
+    (4096, 96, 128, 1, 32),      # 96 columns hold no 64-column strip
     (4096, 16, 128, 1, 16),      # 16 columns hold no 32-column strip
     (14336, 4096, 128, 2, 0),    # two rows of K = 14336 exceed the LDS at any width
     (4096, 4096, 128, 8, 0),
@@ -294,7 +296,7 @@ def test_persistent_step_matches_the_fused_launches(chain_widths):
     built = D.build_layers(2, seed=8)
     fs = D.strips([D.fuse(layer) for layer in built], chain=chain_widths)
     widths = {name: w.strip_cols for name, w in fs[0].items()}
-    assert widths == ({"qkv": 32, "o": 32, "gate_up": 64, "down": 32} if chain_widths
+    assert widths == ({"qkv": 64, "o": 64, "gate_up": 64, "down": 32} if chain_widths
                       else {"qkv": 32, "o": 16, "gate_up": 64, "down": 16})
     launches = D.DecodeStep(fs)
     chain = C.DecodeChain(D.chain_stages(fs, launches.acts))
