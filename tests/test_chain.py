@@ -288,16 +288,17 @@ def test_timestamps_follow_the_dependencies():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("chain_widths", [False, True])
-def test_persistent_step_matches_the_fused_launches(chain_widths):
+@pytest.mark.parametrize("chain_widths,tp", [(False, 1), (True, 1), (True, 8)])
+def test_persistent_step_matches_the_fused_launches(chain_widths, tp):
     """The reference-semantics step (independent projections) of two full
-    layers as one chain: the bits of the fused strip-major launches on the
-    same copy, at the launches' strip widths or at the chain's."""
-    built = D.build_layers(2, seed=8)
+    layers -- or of one GPU's share of an 8-way split of them -- as one
+    chain: the bits of the fused strip-major launches on the same copy, at
+    the launches' strip widths or at the chain's."""
+    built = D.build_layers(2, seed=8, tp=tp)
     fs = D.strips([D.fuse(layer) for layer in built], chain=chain_widths)
     widths = {name: w.strip_cols for name, w in fs[0].items()}
-    assert widths == ({"qkv": 64, "o": 64, "gate_up": 64, "down": 32} if chain_widths
-                      else {"qkv": 32, "o": 16, "gate_up": 64, "down": 16})
+    assert widths == ({"qkv": 64, "o": 64, "gate_up": 64, "down": 32 if tp == 1 else 64}
+                      if chain_widths else {"qkv": 32, "o": 16, "gate_up": 64, "down": 16})
     launches = D.DecodeStep(fs)
     chain = C.DecodeChain(D.chain_stages(fs, launches.acts))
     got = D.ChainStep(chain, D.weight_bytes(fs)).outputs()
