@@ -50,7 +50,7 @@
 extern "C" {
 #endif
 
-#define NIBBLE_ABI_VERSION 12
+#define NIBBLE_ABI_VERSION 13
 
 #if defined(__GNUC__) || defined(__clang__)
 #define NIBBLE_API __attribute__((visibility("default")))
@@ -321,8 +321,13 @@ NIBBLE_API int nibble_dequant_w4_strip_major(const void* Wt, const void* St, int
  *
  * A stage is Y = X @ W (epilogue 0), fp16(fp16(X @ W) + bias) (1) or the
  * SwiGLU of an interleave_swiglu weight (2, strips of >= 32 columns), with
- * X [M, K] fp16, W strip-major (nibble_pack_strip_major at `strip_cols`),
- * Y [M, N] fp16 ([M, N / 2] for SwiGLU).  `after` names an earlier stage
+ * X [M, K] fp16 and Y [M, N] fp16 ([M, N / 2] for SwiGLU).  W is either
+ * strip-major (layout 0: nibble_pack_strip_major at `strip_cols`) or the
+ * packed [K/8, N] words and [K/G, N] scales of nibble_gemv_w4a16 (layout 1),
+ * read as strips of `strip_cols` columns; the two give the same bits (256-
+ * byte row pieces at 64 columns read as fast as contiguous strips).  No
+ * counterpart in the reference for the layout choice: its decode reads the
+ * packed layout, which layout 1 takes unconverted.  `after` names an earlier stage
  * (index) that must have finished before this one reads its X and bias, or
  * is -1.  Whatever a stage reads that another stage writes, and whatever two
  * stages both write, must be ordered by `after` links (directly or through a
@@ -337,6 +342,7 @@ typedef struct nibble_chain_stage {
   const void* bias;
   int64_t K, N, group_size, strip_cols, epilogue;
   int64_t after;
+  int64_t layout;  /* 0 strip-major, 1 packed */
 } nibble_chain_stage;
 
 /* Validates the stages, plans the launch (one workgroup per CU; every

@@ -83,23 +83,26 @@ constexpr int kWaitRingOldest = waitcnt_vm(kRing - 1);
 // One stage as the kernel reads it (built and checked on the host).
 struct ChainStage {
   const _Float16* X;     // [M, K]
-  const uint32_t* Wt;    // strip-major words: strip s at s * w_strip, row r at r * 4 sw
-  const _Float16* St;    // strip-major scales: strip s at s * s_strip
+  const uint32_t* Wt;    // words: strip s's packed row r at s * w_col + r * w_row
+  const _Float16* St;    // scales: strip s's group g at s * s_col + g * s_row
   _Float16* Y;           // [M, N] (SwiGLU: [M, N / 2])
   const _Float16* bias;  // [N] for the bias epilogue
   uint32_t K, N;
   uint32_t sw;           // strip columns: 16, 32 or 64
   uint32_t groups;       // K / GROUP
-  uint32_t w_strip, s_strip;  // bytes of one strip of Wt / St
+  uint32_t w_strip, s_strip;  // bytes of one strip's words / scales
   uint32_t wbytes, sbytes;    // bytes of Wt / St
   uint32_t xbytes;            // M * K * 2
   uint32_t epilogue;
   int32_t after;              // stage that must be complete before this one reads, or -1
   uint32_t after_items;       // round items of that stage
   uint32_t signal;            // count this stage's finished round items
-  uint32_t pad[3];
+  // Strides of the weight layout: strip-major (w_col = w_strip, w_row =
+  // 4 sw, s_col = s_strip, s_row = 2 sw) or packed (4 sw, 4 N, 2 sw, 2 N).
+  uint32_t w_col, w_row, s_col, s_row;
+  uint32_t pad;
 };
-static_assert(sizeof(ChainStage) == 104, "descriptor layout");
+static_assert(sizeof(ChainStage) == 112, "descriptor layout");
 
 struct ChainArgs {
   const ChainStage* stages;
@@ -328,9 +331,14 @@ __global__ __launch_bounds__(kChainThreads) void chain_kernel(ChainArgs a) {
   unsigned char* const bbuf = sbuf + 2 * a.sbuf_bytes;
 
   // ---- compute waves: the weight feed ------------------------------------
+  // A 1 KiB wave load is 256 / sw packed rows of a strip: lane l reads the
+  // 16 bytes at column quad l % (sw / 4) of row l / (sw / 4), so the slot
+  // holds the strip-major bytes whichever layout the words are in.
   int feed_r = r_begin - 1;  // round whose loads are being issued
   uint32_t feed_left = 0;    // this wave's loads left in it
-  uint32_t feed_off = 0;     // byte offset of the next one in the stage's Wt
+  uint32_t feed_off = 0;     // scalar byte offset of the next one in the stage's Wt
+  uint32_t feed_step = 0;    // scalar bytes from one load to the next
+  uint32_t feed_lane = 0;    // this lane's byte offset within a load
   __amdgpu_buffer_rsrc_t feed_rs = make_rsrc(a.stages, 0);
   auto plan_round = [&](int r) {
     feed_r = r;
@@ -344,8 +352,11 @@ __global__ __launch_bounds__(kChainThreads) void chain_kernel(ChainArgs a) {
     if (strip < 0) return;
     const uint32_t g0 = wt * st.groups / waves, g1 = (wt + 1) * st.groups / waves;
     const uint32_t chunk = GROUP * st.sw / 2;  // bytes of one quant group of a strip
+    const uint32_t lpr = st.sw / 4;            // lanes a packed row of the strip takes
     feed_left = (g1 - g0) * chunk / kSlotBytes;
-    feed_off = static_cast<uint32_t>(strip) * st.w_strip + g0 * chunk;
+    feed_off = static_cast<uint32_t>(strip) * st.w_col + g0 * (GROUP / 8) * st.w_row;
+    feed_step = (kSlotBytes / (4 * st.sw)) * st.w_row;
+    feed_lane = lane / lpr * st.w_row + lane % lpr * 16u;
     feed_rs = make_rsrc(st.Wt, st.wbytes);
   };
   // The next load of the wave's sequence into `slot`; past the last round a
@@ -354,10 +365,10 @@ __global__ __launch_bounds__(kChainThreads) void chain_kernel(ChainArgs a) {
     while (feed_left == 0 && feed_r < r_end) plan_round(feed_r + 1);
     const lds_ptr dst = (lds_ptr)(ring + (wave * kRing + slot) * kSlotBytes);
     const bool real = feed_left > 0;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(feed_rs, dst, 16, real ? lane * 16u : kOutOfRange,
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(feed_rs, dst, 16, real ? feed_lane : kOutOfRange,
                                              real ? feed_off : 0u, 0, kPolicyNt);
     if (real) {
-      feed_off += kSlotBytes;
+      feed_off += feed_step;
       --feed_left;
     }
   };
@@ -428,24 +439,27 @@ __global__ __launch_bounds__(kChainThreads) void chain_kernel(ChainArgs a) {
             (static_cast<uint32_t>(strip) * st.sw + 8 * part) * 2u, 0, 0, kPolicySc1);
     }
   };
-  // Scales of round r's strips into buffer b (read-only data: no waits).
+  // Scales of round r's strips into buffer b (read-only data: no waits),
+  // strip-major in LDS whichever layout they are in: 16-byte chunk ch is
+  // column piece ch % (sw / 8) of group row ch / (sw / 8).
   auto stage_scales = [&](int r, int b) {
     const int4 rd = rounds[r];
     const ChainStage st = stages[rd.x];
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(st.St, st.sbytes);
     const uint32_t chunks = st.s_strip / 16;
+    const uint32_t ppr = st.sw / 8;  // 16-byte pieces of a scale row of the strip
     unsigned char* const sd = sbuf + b * a.sbuf_bytes;
 #pragma unroll
     for (int team = 0; team < 2; ++team) {
       const int strip = team == 0 ? rd.y : rd.z;
       if (strip < 0) continue;
-      const uint32_t base = static_cast<uint32_t>(strip) * st.s_strip;
+      const uint32_t base = static_cast<uint32_t>(strip) * st.s_col;
       for (uint32_t blk = 0; blk * 64 < chunks; ++blk) {
         const uint32_t ch = blk * 64 + lane;
         if (ch < chunks)
           __builtin_amdgcn_raw_ptr_buffer_load_lds(
-              rs, (lds_ptr)(sd + team * st.s_strip + blk * kSlotBytes), 16, base + ch * 16u, 0, 0,
-              kPolicyNt);
+              rs, (lds_ptr)(sd + team * st.s_strip + blk * kSlotBytes), 16,
+              base + ch / ppr * st.s_row + ch % ppr * 16u, 0, 0, kPolicyNt);
       }
     }
   };
@@ -697,6 +711,9 @@ int chain_create(const nibble_chain_stage* stages, int64_t n, int64_t M, void* s
                  "stage %lld: X, Wt, St and bias need 16-byte alignment, Y 8-byte", (long long)i);
     NIBBLE_CHECK(s.after >= -1 && s.after < i, "stage %lld: `after` must name an earlier stage or be -1",
                  (long long)i);
+    NIBBLE_CHECK(s.layout == 0 || s.layout == 1,
+                 "stage %lld: layout must be 0 (strip-major) or 1 (packed), got %lld", (long long)i,
+                 (long long)s.layout);
     const size_t wbytes = static_cast<size_t>(K / 8) * N * 4, sbytes = static_cast<size_t>(K / G) * N * 2;
     NIBBLE_CHECK(static_cast<int64_t>(wbytes) < lim && M * K * 2 < lim,
                  "stage %lld: operands beyond 32-bit offsets", (long long)i);
@@ -712,6 +729,12 @@ int chain_create(const nibble_chain_stage* stages, int64_t n, int64_t M, void* s
     d.groups = static_cast<uint32_t>(K / G);
     d.w_strip = static_cast<uint32_t>(K / 8 * SW * 4);
     d.s_strip = static_cast<uint32_t>(K / G * SW * 2);
+    const bool packed = s.layout == 1;
+    d.w_col = packed ? static_cast<uint32_t>(SW * 4) : d.w_strip;
+    d.w_row = static_cast<uint32_t>((packed ? N : SW) * 4);
+    d.s_col = packed ? static_cast<uint32_t>(SW * 2) : d.s_strip;
+    d.s_row = static_cast<uint32_t>((packed ? N : SW) * 2);
+    d.pad = 0;
     d.wbytes = static_cast<uint32_t>(wbytes);
     d.sbytes = static_cast<uint32_t>(sbytes);
     d.xbytes = static_cast<uint32_t>(M * K * 2);

@@ -47,9 +47,11 @@ the same way: a
 :class:`~nibblegemm_amd.chain.DecodeChain` of the 128 projections, each still
 reading its fixed activation (the reference's semantics), whose workgroups
 stream weights across projection boundaries.  Both run on strip-major copies
-at the chain's widths (:func:`~nibblegemm_amd.chain.chain_strip_cols`: o and
-down in 32-column strips where the launches take 16), and their outputs are
-bit-identical to the launches on the same copy.  ``dataflow`` is the real data flow of a decoder layer
+at the chain's widths (:func:`~nibblegemm_amd.chain.chain_strip_cols`: 64
+columns, down 32, where the launches take 16 to 64), and their outputs are
+bit-identical to the launches on the same copy.  ``persistent_packed`` runs
+the fused step as one chain straight on the packed weights, the drop-in
+layout, unconverted (the bits of ``persistent``'s chain).  ``dataflow`` is the real data flow of a decoder layer
 without attention and norms, one launch per projection on strip-major
 weights: the q|k|v product, o on its q part with the layer input added as
 the residual, gate|up through the SwiGLU epilogue, and down with o's output
@@ -190,9 +192,10 @@ class DecodeStep:
 
 
 def chain_stages(layers: List[Dict[str, QuantizedWeight]], acts: Dict[int, torch.Tensor]) -> list:
-    """The projections of ``layers`` (strip-major weights) as independent
-    chain stages, each reading its fixed activation ``acts[K]`` (the
-    reference's decode-step semantics) and writing its own output."""
+    """The projections of ``layers`` (strip-major weights, or packed ones read
+    as strips of the chain's widths) as independent chain stages, each
+    reading its fixed activation ``acts[K]`` (the reference's decode-step
+    semantics) and writing its own output."""
     out = []
     for layer in layers:
         for name, w in layer.items():
@@ -459,6 +462,31 @@ def measure_persistent(layers_sm: List[Dict[str, QuantizedWeight]], trials: int 
     return r
 
 
+def measure_persistent_packed(layers: List[Dict[str, QuantizedWeight]], trials: int = 10,
+                              warmup: int = 3) -> dict:
+    """The step of ``layers`` as one chain reading the packed weights (the
+    reference's layout) unconverted, after checking its outputs bit for bit
+    against the same chain on strip-major copies at the same widths (raises
+    otherwise); the copies are freed before the timing."""
+    launches = DecodeStep(layers)
+    chain = DecodeChain(chain_stages(layers, launches.acts))
+    step = ChainStep(chain, weight_bytes(layers))
+    copies = strips(layers, chain=True)
+    ref = DecodeChain(chain_stages(copies, launches.acts))
+    same = _same(step.outputs(), ChainStep(ref, 0).outputs())
+    ref.check()
+    ref.close()
+    del ref, copies
+    if not same:
+        raise RuntimeError("persistent chain on packed weights differs from the strip-major chain")
+    chain.check()
+    r = measure_step(step, step.nbytes, trials, warmup, stages=len(chain.stages),
+                     workgroups=chain.workgroups, rounds=chain.rounds,
+                     equals_strip_major_chain=True)
+    chain.check()
+    return r
+
+
 def measure_dataflow(layers_sm: List[Dict[str, QuantizedWeight]], trials: int = 10,
                      warmup: int = 3, persistent: bool = True,
                      with_stages: bool = False) -> Dict[str, dict]:
@@ -485,7 +513,7 @@ def measure_dataflow(layers_sm: List[Dict[str, QuantizedWeight]], trials: int = 
 
 VARIANTS = ("projections", "fused", "fused_swiglu", "glue", "projections_strips", "fused_strips",
             "fused_swiglu_strips", "glue_strips", "persistent_projections", "persistent",
-            "dataflow_strips", "persistent_dataflow")
+            "persistent_packed", "dataflow_strips", "persistent_dataflow")
 
 
 def run(n_layers: int = 32, group_size: int = 128, trials: int = 10, glue_pos: int = 1023,
@@ -512,7 +540,7 @@ def run(n_layers: int = 32, group_size: int = 128, trials: int = 10, glue_pos: i
         ps = strips(layers, chain=True)
         res["persistent_projections"] = measure_persistent(ps, trials, with_stages=with_stages)
         del ps
-    if want & {"fused", "fused_strips", "persistent"}:
+    if want & {"fused", "fused_strips", "persistent", "persistent_packed"}:
         fused = [fuse(layer) for layer in layers]
         if "fused" in want:
             res["fused"] = measure(fused, trials)
@@ -524,6 +552,8 @@ def run(n_layers: int = 32, group_size: int = 128, trials: int = 10, glue_pos: i
             fs = strips(fused, chain=True)
             res["persistent"] = measure_persistent(fs, trials, with_stages=with_stages)
             del fs
+        if "persistent_packed" in want:
+            res["persistent_packed"] = measure_persistent_packed(fused, trials)
         del fused
     swiglu_want = {"fused_swiglu", "glue", "fused_swiglu_strips", "glue_strips",
                    "dataflow_strips", "persistent_dataflow"}

@@ -30,8 +30,9 @@ A = 1 << 20  # aligned fake device addresses, never dereferenced on the CPU tier
 W0, S0 = 1 << 40, 1 << 41  # fake weight addresses, far from the activations
 
 
-def _pack(X=A, Wt=W0, St=S0, Y=A * 4, bias=0, K=4096, N=4096, g=128, sw=16, ep=0, after=-1):
-    return struct.pack("<5Q6q", X, Wt, St, Y, bias, K, N, g, sw, ep, after)
+def _pack(X=A, Wt=W0, St=S0, Y=A * 4, bias=0, K=4096, N=4096, g=128, sw=16, ep=0, after=-1,
+          layout=0):
+    return struct.pack("<5Q7q", X, Wt, St, Y, bias, K, N, g, sw, ep, after, layout)
 
 
 def _create(stages, M=1):
@@ -68,6 +69,8 @@ def _create(stages, M=1):
     # a stage writes weights
     ([_pack(), _pack(X=A * 6, Y=W0 + 64, after=0)], 1, "weights"),
     ([_pack(Y=S0 + 1024)], 1, "weights"),
+    ([_pack(layout=2)], 1, "layout must be"),
+    ([_pack(layout=1, N=4000, sw=64)], 1, "no strip-major plan"),
 ])
 def test_create_rejections(stages, M, needle):
     rc, msg = _create(stages, M)
@@ -202,6 +205,73 @@ def test_independent_stages_have_the_strip_launch_bits(M):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("M", [1, 2, 5])
+def test_packed_stages_have_the_strip_major_bits(M):
+    """Stages on packed weights (the reference's layout, unconverted) read as
+    16-, 32- and 64-column strips, group sizes 128 and 64, the bias and SwiGLU
+    epilogues and long K, beside strip-major stages in one chain: every
+    output has the bits of the same stage on the strip-major copy at that
+    width, which are the strip launch's."""
+    kmax = {1: 14336, 2: 4096, 5: 1024}[M]
+    cases = [(4096, 4096, 128, 64), (4096, 1024, 128, 32), (1024, 448, 128, 16), (2048, 512, 64, 32),
+             (1024, 4096, 64, 64), (14336, 4096, 128, 32), (4096, 6144, 128, 64)]
+    stages, want = [], []
+    for i, (K, N, g, sw) in enumerate(cases):
+        if K > kmax:
+            continue
+        if g != 128:
+            continue  # a chain shares one group size: the group-64 stages go below
+        _, _, _, Xd, qw = synthetic(M, K, N, g, seed=70 + i + 10 * M)
+        sm = ng.to_strip_major(qw, sw)
+        stages.append(C.stage(Xd, qw, strip_cols=sw))
+        want.append(ng.matmul(Xd, sm))
+        stages.append(C.stage(Xd, sm))  # the same stage on the strip-major copy
+        want.append(want[-1])
+    ke = min(kmax, 4096)
+    _, _, _, Xd, qw = synthetic(M, ke, 1024, 128, seed=80)
+    bias = (torch.randn(1024, generator=torch.Generator().manual_seed(3)) * 0.3).half().cuda()
+    stages.append(C.stage(Xd, qw, bias=bias, strip_cols=64))
+    want.append(ng.matmul_bias(Xd, ng.to_strip_major(qw, 64), bias))
+    _, _, _, Xd, gate = synthetic(M, ke, 2048, 128, seed=81)
+    _, _, _, _, up = synthetic(M, ke, 2048, 128, seed=82)
+    gu = ng.interleave_swiglu(gate, up)
+    for sw in (32, 64):
+        stages.append(C.stage(Xd, gu, swiglu=True, strip_cols=sw))
+        want.append(ng.matmul_swiglu(Xd, ng.to_strip_major(gu, sw)))
+    got = _run(C.DecodeChain(stages, M=M))
+    for i, (a, b) in enumerate(zip(got, want)):
+        assert torch.equal(a, b), (M, i)
+    # group size 64
+    stages, want = [], []
+    for i, (K, N, g, sw) in enumerate(cases):
+        if g != 64 or K > kmax:
+            continue
+        _, _, _, Xd, qw = synthetic(M, K, N, g, seed=90 + i)
+        stages.append(C.stage(Xd, qw, strip_cols=sw))
+        want.append(ng.matmul(Xd, ng.to_strip_major(qw, sw)))
+    got = _run(C.DecodeChain(stages, M=M))
+    assert all(torch.equal(a, b) for a, b in zip(got, want))
+
+
+@pytest.mark.gpu
+def test_packed_dependent_stages():
+    """A dependent chain on packed weights (each stage reads the one before):
+    the bits of the same chain on strip-major copies."""
+    _, _, _, Xd, w1 = synthetic(1, 4096, 4096, 128, seed=91)
+    _, _, _, _, w2 = synthetic(1, 4096, 14336, 128, seed=92)
+    _, _, _, _, w3 = synthetic(1, 14336, 4096, 128, seed=93)
+    outs = []
+    for conv in (False, True):
+        ws = [ng.to_strip_major(w, C.chain_strip_cols(w.K, w.N, 128)) if conv else w
+              for w in (w1, w2, w3)]
+        s0 = C.stage(Xd, ws[0])
+        s1 = C.stage(s0.Y, ws[1], after=0)
+        s2 = C.stage(s1.Y, ws[2], after=1)
+        outs.append(_run(C.DecodeChain([s0, s1, s2])))
+    assert all(torch.equal(a, b) for a, b in zip(*outs))
+
+
+@pytest.mark.gpu
 def test_group_size_64_chain():
     stages, want = [], []
     for i, (K, N) in enumerate([(2048, 1024), (4096, 2048), (1024, 4096)]):
@@ -285,6 +355,20 @@ def test_timestamps_follow_the_dependencies():
     # each stage ends after the one it waited for
     assert all(b >= a for a, b in zip(ends, ends[1:]))
     assert ends[-1] < 1e4
+
+
+@pytest.mark.gpu
+def test_persistent_step_on_packed_weights():
+    """The reference-semantics step of two full layers as one chain straight
+    on the packed (drop-in) weights: the bits of the chain on strip-major
+    copies at the same widths."""
+    fused = [D.fuse(layer) for layer in D.build_layers(2, seed=9)]
+    launches = D.DecodeStep(fused)
+    packed = C.DecodeChain(D.chain_stages(fused, launches.acts))
+    fs = D.strips(fused, chain=True)
+    strip = C.DecodeChain(D.chain_stages(fs, launches.acts))
+    got, want = _run(packed), _run(strip)
+    assert len(got) == 8 and all(torch.equal(a, b) for a, b in zip(got, want))
 
 
 @pytest.mark.gpu
