@@ -253,7 +253,8 @@ def main() -> int:
             f"{decode['fused_swiglu_strips']['graph_tok_s']}, full step "
             f"{decode['glue_strips']['graph_tok_s']} tok/s; as one persistent launch: projections "
             f"{decode['persistent_projections']['graph_tok_s']}, fused "
-            f"{decode['persistent']['graph_tok_s']}, fused on the packed weights unconverted "
+            f"{decode['persistent']['graph_tok_s']}; on the packed weights unconverted: projections "
+            f"{decode['persistent_projections_packed']['graph_tok_s']}, fused "
             f"{decode['persistent_packed']['graph_tok_s']} tok/s; {time.perf_counter() - t0:.1f} s")
 
     prefill = None

@@ -49,9 +49,10 @@ reading its fixed activation (the reference's semantics), whose workgroups
 stream weights across projection boundaries.  Both run on strip-major copies
 at the chain's widths (:func:`~nibblegemm_amd.chain.chain_strip_cols`: 64
 columns, down 32, where the launches take 16 to 64), and their outputs are
-bit-identical to the launches on the same copy.  ``persistent_packed`` runs
-the fused step as one chain straight on the packed weights, the drop-in
-layout, unconverted (the bits of ``persistent``'s chain).  ``dataflow`` is the real data flow of a decoder layer
+bit-identical to the launches on the same copy.  ``persistent_packed`` and
+``persistent_projections_packed`` run the same chains straight on the packed
+weights, the drop-in layout, unconverted (the bits of the chains on
+strip-major copies).  ``dataflow`` is the real data flow of a decoder layer
 without attention and norms, one launch per projection on strip-major
 weights: the q|k|v product, o on its q part with the layer input added as
 the residual, gate|up through the SwiGLU epilogue, and down with o's output
@@ -512,8 +513,9 @@ def measure_dataflow(layers_sm: List[Dict[str, QuantizedWeight]], trials: int = 
 
 
 VARIANTS = ("projections", "fused", "fused_swiglu", "glue", "projections_strips", "fused_strips",
-            "fused_swiglu_strips", "glue_strips", "persistent_projections", "persistent",
-            "persistent_packed", "dataflow_strips", "persistent_dataflow")
+            "fused_swiglu_strips", "glue_strips", "persistent_projections",
+            "persistent_projections_packed", "persistent", "persistent_packed", "dataflow_strips",
+            "persistent_dataflow")
 
 
 def run(n_layers: int = 32, group_size: int = 128, trials: int = 10, glue_pos: int = 1023,
@@ -540,6 +542,8 @@ def run(n_layers: int = 32, group_size: int = 128, trials: int = 10, glue_pos: i
         ps = strips(layers, chain=True)
         res["persistent_projections"] = measure_persistent(ps, trials, with_stages=with_stages)
         del ps
+    if "persistent_projections_packed" in want:
+        res["persistent_projections_packed"] = measure_persistent_packed(layers, trials)
     if want & {"fused", "fused_strips", "persistent", "persistent_packed"}:
         fused = [fuse(layer) for layer in layers]
         if "fused" in want:

@@ -358,17 +358,21 @@ def test_timestamps_follow_the_dependencies():
 
 
 @pytest.mark.gpu
-def test_persistent_step_on_packed_weights():
-    """The reference-semantics step of two full layers as one chain straight
-    on the packed (drop-in) weights: the bits of the chain on strip-major
-    copies at the same widths."""
-    fused = [D.fuse(layer) for layer in D.build_layers(2, seed=9)]
-    launches = D.DecodeStep(fused)
-    packed = C.DecodeChain(D.chain_stages(fused, launches.acts))
-    fs = D.strips(fused, chain=True)
-    strip = C.DecodeChain(D.chain_stages(fs, launches.acts))
+@pytest.mark.parametrize("fused", [False, True])
+def test_persistent_step_on_packed_weights(fused):
+    """The reference-semantics step of two full layers (its 7 projections
+    each, or the fused 4) as one chain straight on the packed (drop-in)
+    weights: the bits of the chain on strip-major copies at the same widths."""
+    layers = D.build_layers(2, seed=9)
+    if fused:
+        layers = [D.fuse(layer) for layer in layers]
+    launches = D.DecodeStep(layers)
+    packed = C.DecodeChain(D.chain_stages(layers, launches.acts))
+    copies = D.strips(layers, chain=True)
+    strip = C.DecodeChain(D.chain_stages(copies, launches.acts))
     got, want = _run(packed), _run(strip)
-    assert len(got) == 8 and all(torch.equal(a, b) for a, b in zip(got, want))
+    assert len(got) == (8 if fused else 14)
+    assert all(torch.equal(a, b) for a, b in zip(got, want))
 
 
 @pytest.mark.gpu
