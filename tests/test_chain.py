@@ -373,6 +373,21 @@ def test_persistent_step_on_packed_weights(fused):
     got, want = _run(packed), _run(strip)
     assert len(got) == (8 if fused else 14)
     assert all(torch.equal(a, b) for a, b in zip(got, want))
+    # replayed from a HIP graph, with the strip-major chain run between replays
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        packed.run()
+    for _ in range(3):
+        for y in packed.outputs():
+            y.fill_(float("nan"))
+        strip.run()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert all(torch.equal(a, b) for a, b in zip(packed.outputs(), want))
+    packed.check()
 
 
 @pytest.mark.gpu
