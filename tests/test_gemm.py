@@ -2,8 +2,9 @@
 
 Edge cases follow the reference's tests/test_gemm.py (M on, just past and far
 past tile boundaries; N with masked columns), then the benchmark prefill and
-handover configs at full size -- checked on sampled rows, since the CPU oracle
-cannot do 2048 x 4096 x 14336 in seconds.
+handover configs at full size: sampled rows against the CPU oracle at every
+prefill point, every output against it at the bench's M = 2048 points (the
+C oracle takes a few seconds there on the host's cores).
 
 Bounds: north-star ``max|y - ref| <= 1e-2 * rms(ref)`` and the reference's
 ``max|y - ref| / mean|ref| < 3e-2`` (tests/test_gemm.py:34 there).  The LDS B
@@ -227,6 +228,19 @@ def test_prefill_configs_whole_output(M, K_, N):
         y = ng.gemm(Xd, qw, version=version).float()
         assert torch.isfinite(y).all()
         assert float((y - ref).abs().max() / rms) <= RMS_TOL, version
+
+
+@pytest.mark.parametrize("K_,N", [(4096, 14336), (14336, 4096)])
+def test_prefill_m2048_whole_output_against_the_oracle(K_, N):
+    """The bench's prefill points (M = 2048 at both config-4 shapes), every
+    output of both versions against the CPU oracle's reference path
+    (dequantize, fp32 matmul, fp16; ~3-5 s a shape on the host's cores)."""
+    X, packed, scales, Xd, qw = synthetic(2048, K_, N, 128, seed=2048 + K_)
+    ref = oracle_y(X, packed, scales, K_, 128)
+    for version in (6, 7):
+        y = host(ng.gemm(Xd, qw, version=version))
+        assert np.all(np.isfinite(y)), version
+        assert rms_err(y, ref) <= RMS_TOL, version
 
 
 def test_gemm_is_deterministic():
