@@ -50,7 +50,7 @@
 extern "C" {
 #endif
 
-#define NIBBLE_ABI_VERSION 13
+#define NIBBLE_ABI_VERSION 14
 
 #if defined(__GNUC__) || defined(__clang__)
 #define NIBBLE_API __attribute__((visibility("default")))
@@ -130,6 +130,24 @@ NIBBLE_API size_t nibble_gemv_workspace_bytes(int64_t M, int64_t K, int64_t N, i
 NIBBLE_API size_t nibble_gemv_counter_bytes(int64_t M, int64_t K, int64_t N, int64_t group_size,
                                  int64_t version, int64_t splits_override,
                                  int64_t threads_override, void* stream);
+
+/*
+ * Diagnostics; no counterpart in the reference (which has no in-kernel
+ * timing).  While `stamps` is non-NULL, every launch of this host thread that
+ * runs the strip kernel at M = 1 without the RMSNorm prologue (the decode
+ * GEMV, whichever entry point plans it) writes its timeline into `stamps` (device memory, `bytes` long, 8-byte
+ * aligned): per wave w of workgroup b, 8 uint64 at index (b * waves + w) * 8
+ * -- s_memrealtime ticks (100 MHz) at kernel entry, after the prologue's
+ * loads are issued, after the activation/scale copies have landed (workgroup
+ * barrier), after the first quant group is computed, after the last, after
+ * the partials are in LDS, after this wave's output stores are acknowledged
+ * -- then (b << 40) | (w << 36) | (XCC_ID << 32) | HW_ID.  Such a launch
+ * needs grid * waves * 64 bytes (grid = 8 * ceil(strips / 8)); a smaller
+ * buffer makes it fail with NIBBLE_ERR_INVALID_ARGUMENT before anything is
+ * launched.  NULL turns it off.  Other launches are unchanged; the outputs
+ * are the same bits either way.
+ */
+NIBBLE_API int nibble_gemv_timeline(void* stamps, int64_t bytes);
 
 /*
  * Prefill-regime matmul on CDNA4 MFMA (any M >= 1).  version 6 (default) or 7

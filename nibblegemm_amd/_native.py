@@ -10,7 +10,7 @@ import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIBRARY_PATH = os.path.join(_HERE, "lib", "libnibblegemm_amd.so")
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 _binding = None
 

@@ -153,6 +153,16 @@ static PyObject* py_sm_cols(PyObject* self, PyObject* const* a, Py_ssize_t n) {
   return PyLong_FromLongLong((long long)nibble_strip_major_cols(K, N, g));
 }
 
+/* gemv_timeline(stamps_ptr, bytes) */
+static PyObject* py_gemv_timeline(PyObject* self, PyObject* const* a, Py_ssize_t n) {
+  (void)self;
+  if (!nargs_is(n, 2, "gemv_timeline")) return NULL;
+  void* stamps;
+  long long bytes;
+  if (!take_ptr(a[0], &stamps) || !take_i64(a[1], &bytes)) return NULL;
+  return PyLong_FromLong(nibble_gemv_timeline(stamps, bytes));
+}
+
 /* chain_strip_cols(K, N, g, M) */
 static PyObject* py_chain_cols(PyObject* self, PyObject* const* a, Py_ssize_t n) {
   (void)self;
@@ -384,6 +394,8 @@ static PyMethodDef kMethods[] = {
      "nibble_gemm_streams"},
     {"strip_major_cols", (PyCFunction)(void (*)(void))py_sm_cols, METH_FASTCALL,
      "nibble_strip_major_cols"},
+    {"gemv_timeline", (PyCFunction)(void (*)(void))py_gemv_timeline, METH_FASTCALL,
+     "nibble_gemv_timeline"},
     {"chain_strip_cols", (PyCFunction)(void (*)(void))py_chain_cols, METH_FASTCALL,
      "nibble_chain_strip_cols"},
     {"pack_strip_major", (PyCFunction)(void (*)(void))py_sm_pack, METH_FASTCALL,

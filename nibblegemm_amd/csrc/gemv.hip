@@ -68,6 +68,9 @@ struct GemvArgs {
   int stage_x;            // strip kernel: copy the activations to LDS (if they fit 64 KiB)
   // Where the weights and scales of a column live (packed or strip-major).
   WeightLayout L;
+  // Strip kernel at M = 1 only (diagnostics): per wave 8 uint64, the
+  // timeline that nibble_gemv_timeline documents; null when off.
+  unsigned long long* stamps = nullptr;
 };
 
 __device__ __forceinline__ f4_t mfma16(h8_t a, h8_t b, f4_t c) {
@@ -909,8 +912,13 @@ __global__ __launch_bounds__((4 * SPW + STAGERS) * 64) void gemv_batch_kernel(Ge
 // the few lanes that hold real rows at M <= 8, and a per-lane scale load the
 // same for 8-byte scale quads.  NORM (RMSNorm prologue) fills the activation
 // rows itself and implies STAGED.
-template <int MT, int GROUP, int SW, int WAVES, int DEPTH, bool NORM, bool ONEPASS, bool STAGED>
+template <int MT, int GROUP, int SW, int WAVES, int DEPTH, bool NORM, bool ONEPASS, bool STAGED,
+          bool TIMELINE = false>
 __global__ __launch_bounds__(WAVES * 64) void gemv_strip_kernel(GemvArgs a) {
+  // TIMELINE: s_memrealtime ticks (100 MHz) at the points nibble_gemv_timeline
+  // lists; only that instantiation has them.
+  unsigned long long tl[7] = {};
+  if constexpr (TIMELINE) tl[0] = __builtin_amdgcn_s_memrealtime();
   constexpr int LPR = SW / 4;            // lanes per packed row
   constexpr int RPL = 64 / LPR;          // packed rows per wave load
   constexpr int P = RPL / 4;             // phases
@@ -1130,7 +1138,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_strip_kernel(GemvArgs a) {
   // barrier for the others').  The RMSNorm prologue then normalises the
   // staged rows in place: its inputs were copied ahead of the weight loads,
   // so its wait does not include them.
+  if constexpr (TIMELINE) tl[1] = __builtin_amdgcn_s_memrealtime();
   if constexpr (STAGED) __syncthreads();
+  if constexpr (TIMELINE) tl[2] = __builtin_amdgcn_s_memrealtime();
   if constexpr (NORM) norm_rows_in_lds<THREADS, MT>(a, mrows, xnorm, wn_lds);
   if constexpr (ONEPASS) {
     // Every group of the wave is already in flight (n <= DEPTH).
@@ -1145,6 +1155,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_strip_kernel(GemvArgs a) {
       if (d < n) {
         if constexpr (!STAGED) prep(st[d]);
         compute(st[d]);
+        if constexpr (TIMELINE)
+          if (d == 0) tl[3] = __builtin_amdgcn_s_memrealtime();
       }
     }
   } else {
@@ -1161,12 +1173,15 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_strip_kernel(GemvArgs a) {
             prep(st[d]);
           }
           compute(st[d]);
+          if constexpr (TIMELINE)
+            if (i0 + d == 0) tl[3] = __builtin_amdgcn_s_memrealtime();
         }
         __builtin_amdgcn_sched_barrier(0);
         load(st[d], i0 + d + DEPTH);
       }
     }
   }
+  if constexpr (TIMELINE) tl[4] = __builtin_amdgcn_s_memrealtime();
 
   // Lane (n = lane % 16, row block lane / 16) holds C rows 4 (lane / 16) + i
   // of each tile; it keeps the entries of its own phase.
@@ -1185,6 +1200,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_strip_kernel(GemvArgs a) {
       }
     }
   __syncthreads();
+  if constexpr (TIMELINE) tl[5] = __builtin_amdgcn_s_memrealtime();
   // Sum the WAVES * P partials of an output quad in (wave, phase) order.  The
   // reads go out in batches of up to 16 ahead of their adds (a scheduling
   // barrier keeps the compiler from interleaving each read with its add,
@@ -1212,6 +1228,20 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_strip_kernel(GemvArgs a) {
     return sum;
   };
   emit_outputs<MT, THREADS, SW>(a, strip, 0, mrows, strip_sum);
+  if constexpr (TIMELINE) {
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's output stores acknowledged
+    tl[6] = __builtin_amdgcn_s_memrealtime();
+    const unsigned hw_id = __builtin_amdgcn_s_getreg((31 << 11) | 4);  // HW_REG_HW_ID
+    const unsigned xcc = __builtin_amdgcn_s_getreg((15 << 11) | 20);   // HW_REG_XCC_ID
+    if (lane == 0) {
+      unsigned long long* const out = a.stamps + (static_cast<size_t>(blockIdx.x) * WAVES + wave) * 8;
+#pragma unroll
+      for (int k = 0; k < 7; ++k) out[k] = tl[k];
+      out[7] = (static_cast<unsigned long long>(blockIdx.x) << 40) |
+               (static_cast<unsigned long long>(wave) << 36) |
+               (static_cast<unsigned long long>(xcc & 0xFu) << 32) | hw_id;
+    }
+  }
 }
 
 // Versions 0 and 1: one thread per (m, n), scalar decode, fp32 weights
@@ -1370,6 +1400,22 @@ hipError_t launch_strip_geometry(const GemvArgs& a, hipStream_t stream) {
     const bool staged = a.norm_w != nullptr ||
                         (a.stage_x && (xbytes <= 65536 || (MT == 16 && kStaticLds + lds <= kLdsMax)));
     if (kStaticLds + (staged ? lds : 0) > kLdsMax) return hipErrorInvalidValue;
+    if constexpr (MT == 1) {
+      if (a.stamps != nullptr && a.norm_w == nullptr) {
+        if (staged) {
+          if (onepass)
+            gemv_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, false, true, true, true><<<grid, WAVES * 64, lds, stream>>>(a);
+          else
+            gemv_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, false, false, true, true><<<grid, WAVES * 64, lds, stream>>>(a);
+        } else {
+          if (onepass)
+            gemv_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, false, true, false, true><<<grid, WAVES * 64, 0, stream>>>(a);
+          else
+            gemv_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, false, false, false, true><<<grid, WAVES * 64, 0, stream>>>(a);
+        }
+        return hipGetLastError();
+      }
+    }
     if (a.norm_w != nullptr) {
       if (onepass)
         gemv_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, true, true, true><<<grid, WAVES * 64, lds, stream>>>(a);
@@ -1699,6 +1745,10 @@ int launch_stream(const void* X, const void* Wq, const void* S, void* Y, int64_t
                              epilogue, bias, norm_w, norm_eps, strip_cols);
 }
 
+// nibble_gemv_timeline's buffer for this host thread's launches (off: null).
+thread_local unsigned long long* t_timeline = nullptr;
+thread_local int64_t t_timeline_bytes = 0;
+
 int launch_stream_split(const void* X, const void* Wq, const void* S, void* Y, int64_t M,
                         int64_t K, int64_t N, int64_t G, const StreamPlan& p, void* counters,
                         void* partials, hipStream_t stream, const char* who, int epilogue,
@@ -1726,6 +1776,13 @@ int launch_stream_split(const void* X, const void* Wq, const void* S, void* Y, i
     a.strips = p.strips;
     a.strips_per_xcd = static_cast<int>(ceil_div(p.strips, 8));
     a.stage_x = p.stage_x ? 1 : 0;
+    if (t_timeline != nullptr && M == 1 && norm_w == nullptr) {
+      const int64_t need = int64_t(8) * a.strips_per_xcd * p.waves * 8 * 8;
+      NIBBLE_CHECK(need <= t_timeline_bytes,
+                   "%s: the timeline of this launch needs %lld bytes, the buffer holds %lld", who,
+                   (long long)need, (long long)t_timeline_bytes);
+      a.stamps = t_timeline;
+    }
     e = G == 128 ? launch_strip_group<128>(a, p, stream) : launch_strip_group<64>(a, p, stream);
   } else if (p.kernel == kBatchKernel) {
     e = G == 128 ? launch_batch_group<128>(a, p, stream) : launch_batch_group<64>(a, p, stream);
@@ -1796,6 +1853,15 @@ bool gemv_plannable(int64_t M, int64_t K, int64_t N, int64_t G, int64_t version)
          (G == 64 || G == 128) && K % G == 0;
 }
 }  // namespace
+
+extern "C" int nibble_gemv_timeline(void* stamps, int64_t bytes) {
+  NIBBLE_CHECK(stamps == nullptr || bytes > 0, "a timeline buffer needs a positive size");
+  NIBBLE_CHECK(stamps == nullptr || reinterpret_cast<uintptr_t>(stamps) % 8 == 0,
+               "the timeline buffer needs 8-byte alignment");
+  t_timeline = static_cast<unsigned long long*>(stamps);
+  t_timeline_bytes = stamps != nullptr ? bytes : 0;
+  return NIBBLE_OK;
+}
 
 extern "C" size_t nibble_gemv_workspace_bytes(int64_t M, int64_t K, int64_t N, int64_t group_size,
                                               int64_t version, int64_t splits_override,

@@ -242,6 +242,20 @@ def test_noalloc_gemv_rejects_plans_beyond_its_scratch():
     assert rc == INVALID and b"packed weight rows" in lib.nibble_last_error()
 
 
+def test_gemv_timeline_setter_checks_its_buffer():
+    """nibble_gemv_timeline (diagnostics) is host state only: it rejects a
+    misaligned or empty buffer and NULL turns it off; no device call."""
+    ext = ng.extension()
+    try:
+        assert ext.gemv_timeline(P + 4, 4096) == INVALID
+        assert "alignment" in ext.last_error()
+        assert ext.gemv_timeline(P, 0) == INVALID
+        assert "positive size" in ext.last_error()
+        assert ext.gemv_timeline(P, 4096) == OK
+    finally:
+        assert ext.gemv_timeline(None, 0) == OK
+
+
 def test_binding_rejects_wrong_arity():
     ext = ng.extension()
     with pytest.raises(TypeError):

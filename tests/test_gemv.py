@@ -205,3 +205,43 @@ def test_graph_capture_replays_match_eager():
         assert torch.equal(out, eager)
         ng.gemv(Xd, qw)  # eager work between replays
         torch.cuda.synchronize()
+
+
+def test_gemv_timeline():
+    """The decode GEMV's in-kernel timeline (nibble_gemv_timeline): every
+    wave of every workgroup with a strip records its 7 points in order and
+    its placement; the outputs keep their bits (packed and strip-major); a
+    buffer too small for the launch is refused before anything runs; M > 1
+    launches leave the buffer alone."""
+    ext = ng.extension()
+    _, _, _, Xd, qw = synthetic(1, 4096, 14336, 128, seed=12)
+    sm = ng.to_strip_major(qw, 64)
+    want, want_sm = ng.gemv(Xd, qw), ng.matmul(Xd, sm)
+    strips, waves = 224, 4  # 64-column strips, 4 waves (the decode plan at this shape)
+    stamps = torch.zeros(strips * waves * 8, dtype=torch.int64, device="cuda")
+    try:
+        assert ext.gemv_timeline(stamps.data_ptr(), stamps.numel() * 8) == 0
+        for fn, ref in ((lambda: ng.gemv(Xd, qw), want), (lambda: ng.matmul(Xd, sm), want_sm)):
+            stamps.zero_()
+            assert torch.equal(fn(), ref)
+            torch.cuda.synchronize()
+            t = stamps.view(strips, waves, 8).cpu().numpy()
+            times = t[:, :, :7]
+            assert (times > 0).all()
+            assert (np.diff(times, axis=2) >= 0).all()
+            assert (times[:, :, 6] - times[:, :, 0]).max() < 100_000  # < 1 ms at 100 MHz
+            xcc = (t[:, :, 7] >> 32) & 0xF
+            assert set(np.unique(xcc).tolist()) <= set(range(8))
+            assert ((t[:, :, 7] >> 40) == np.arange(strips)[:, None]).all()
+            assert (((t[:, :, 7] >> 36) & 0xF) == np.arange(waves)[None, :]).all()
+        stamps.zero_()
+        _, _, _, X2, _ = synthetic(2, 4096, 14336, 128, seed=13)
+        ng.gemv(X2, qw)
+        torch.cuda.synchronize()
+        assert int(stamps.abs().sum()) == 0
+        assert ext.gemv_timeline(stamps.data_ptr(), 1024) == 0
+        with pytest.raises(RuntimeError, match="timeline"):
+            ng.gemv(Xd, qw)
+    finally:
+        assert ext.gemv_timeline(None, 0) == 0
+    assert torch.equal(ng.gemv(Xd, qw), want)
