@@ -41,6 +41,9 @@ HIPCC_FLAGS = [
     "-Wall",
     # No packed-fp32 VALU ops (v_pk_add/mul/fma_f32) anywhere in device code.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # Leading scalar kernel arguments (up to 14 dwords) arrive preloaded in
+    # SGPRs instead of being fetched by each wave.
+    "-mllvm", "-amdgpu-kernarg-preload-count=14",
     "-I", INCLUDE,
 ]
 

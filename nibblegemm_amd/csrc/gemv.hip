@@ -73,6 +73,16 @@ struct GemvArgs {
   unsigned long long* stamps = nullptr;
 };
 
+// Whether a kernel that rebuilds the weight layout from w_row and the strip
+// shift (the strip kernel) sees the call's layout: every layout has
+// s_row = w_row / 2, w_strip = (K / 8) w_row and s_strip = (K / GROUP) s_row.
+inline bool layout_rebuilds(const GemvArgs& a, int group) {
+  const uint32_t K = static_cast<uint32_t>(a.K);
+  const bool packed = a.L.strip_shift == 31;  // one strip: the strip strides are unused
+  return a.L.s_row == a.L.w_row / 2 && (packed || a.L.w_strip == (K / 8) * a.L.w_row) &&
+         (packed || a.L.s_strip == (K / static_cast<uint32_t>(group)) * a.L.s_row);
+}
+
 __device__ __forceinline__ f4_t mfma16(h8_t a, h8_t b, f4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
@@ -912,9 +922,26 @@ __global__ __launch_bounds__((4 * SPW + STAGERS) * 64) void gemv_batch_kernel(Ge
 // the few lanes that hold real rows at M <= 8, and a per-lane scale load the
 // same for 8-byte scale quads.  NORM (RMSNorm prologue) fills the activation
 // rows itself and implies STAGED.
+//
+// Kernel arguments.  The fields the prologue needs before its first weight
+// load come first, as 14 scalar dwords (gfx950's limit), and the library is
+// built with kernel-argument preloading, so the command processor writes
+// them into SGPRs at wave launch: the copies and weight loads issue without
+// a kernel-argument fetch (~0.9 us at the headline shape).  The rest of the
+// call (outputs, epilogue, timeline buffer) stays in the GemvArgs block,
+// which is fetched while the weights stream.  The weight layout is rebuilt
+// from its row stride and strip shift (every layout has s_row = w_row / 2,
+// w_strip = (K / 8) w_row and s_strip = (K / GROUP) s_row; the launcher
+// checks that).  4096 x 14336 M = 1: 7.29 -> 7.00-7.07 us.  The split and
+// batch kernels take the block alone: preloading their prologue fields the
+// same way measured no change (14336 x 4096 M = 16..32, the 224-launch 8B
+// step).
 template <int MT, int GROUP, int SW, int WAVES, int DEPTH, bool NORM, bool ONEPASS, bool STAGED,
           bool TIMELINE = false>
-__global__ __launch_bounds__(WAVES * 64) void gemv_strip_kernel(GemvArgs a) {
+__global__ __launch_bounds__(WAVES * 64) void gemv_strip_kernel(
+    const _Float16* __restrict__ Xp, const uint32_t* __restrict__ Wqp, const _Float16* __restrict__ Sp,
+    const _Float16* __restrict__ norm_wp, uint32_t Mp, uint32_t Kp, uint32_t Np, uint32_t strips_p,
+    uint32_t w_row_p, uint32_t strip_shift_p, GemvArgs a) {
   // TIMELINE: s_memrealtime ticks (100 MHz) at the points nibble_gemv_timeline
   // lists; only that instantiation has them.
   unsigned long long tl[7] = {};
@@ -947,23 +974,29 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_strip_kernel(GemvArgs a) {
   // fetches ahead of the first weight load instead of one.
   // Unsigned index arithmetic throughout (divisions by powers of two become
   // shifts); every kernel argument the weight loads need is read up front.
-  const uint32_t K = static_cast<uint32_t>(a.K), N = static_cast<uint32_t>(a.N);
-  const uint32_t strip = (blockIdx.x & 7u) * static_cast<uint32_t>(a.strips_per_xcd) + (blockIdx.x >> 3);
+  const uint32_t K = Kp, N = Np;
+  WeightLayout L;
+  L.strip_shift = strip_shift_p;
+  L.w_row = w_row_p;
+  L.s_row = w_row_p >> 1;
+  L.w_strip = (K >> 3) * w_row_p;
+  L.s_strip = (K / GROUP) * L.s_row;
+  const uint32_t strip = (blockIdx.x & 7u) * ((strips_p + 7u) >> 3) + (blockIdx.x >> 3);
   const uint32_t lane = threadIdx.x & 63u;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int mrows = min(MT, a.M);
+  const int mrows = min(MT, static_cast<int>(Mp));
   const uint32_t total_groups = K / GROUP;
 
   // B side: lane (c, r).
   const uint32_t c = lane % LPR, r = lane / LPR;
   const uint32_t col = strip * SW + 4 * c;
-  const bool col_ok = strip < static_cast<uint32_t>(a.strips) && col < N;
-  const uint32_t row_bytes = a.L.w_row, s_row = a.L.s_row;
-  const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.Wq, (K / 8) * N * 4u);
-  const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.X, static_cast<uint32_t>(a.M) * K * 2u);
-  const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.S, total_groups * N * 2u);
-  const uint32_t voff_w = col_ok ? r * row_bytes + a.L.wcol(col) : kOutOfRange;
-  const uint32_t voff_s = col_ok ? a.L.scol(col) : kOutOfRange;
+  const bool col_ok = strip < strips_p && col < N;
+  const uint32_t row_bytes = L.w_row, s_row = L.s_row;
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(Wqp, (K / 8) * N * 4u);
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(Xp, Mp * K * 2u);
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(Sp, total_groups * N * 2u);
+  const uint32_t voff_w = col_ok ? r * row_bytes + L.wcol(col) : kOutOfRange;
+  const uint32_t voff_s = col_ok ? L.scol(col) : kOutOfRange;
   // A side: lane (m', kb) holds row m' = RPT p + mm of each tile at k block
   // kb, i.e. the 8 k of packed row P kb + p of a wave load.
   const uint32_t mq = lane & 15u, kb = lane >> 4;
@@ -993,7 +1026,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_strip_kernel(GemvArgs a) {
       }
     }
     if constexpr (NORM) {
-      const __amdgpu_buffer_rsrc_t rn = make_rsrc(a.norm_w, K * 2u);
+      const __amdgpu_buffer_rsrc_t rn = make_rsrc(norm_wp, K * 2u);
       const uint32_t chunks = K / 8;
       for (uint32_t blk = wave; blk * 64 < chunks; blk += WAVES) {
         const uint32_t ch = blk * 64 + lane;
@@ -1012,7 +1045,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_strip_kernel(GemvArgs a) {
       if (ch < chunks)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
             rs, (lds_ptr)(s_lds + blk * 512), 16,
-            strip < static_cast<uint32_t>(a.strips) && scol < N ? a.L.scol(scol) + g * s_row
+            strip < strips_p && scol < N ? L.scol(scol) + g * s_row
                                                                 : kOutOfRange,
             0, 0, 0);
     }
@@ -1123,7 +1156,10 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_strip_kernel(GemvArgs a) {
   // the compiler drained every load there.
   // The LDS-DMA copies go first: the barrier before the first compute then
   // waits for them alone (wait counts are in issue order), not for every
-  // weight load in flight.
+  // weight load in flight.  Issuing the first group's weights ahead of the
+  // copies (the barrier then waits for that group, which the first compute
+  // needs anyway) measured slower: 4096 x 14336 M = 1 7.17 against 7.00 us,
+  // the copies landing ~0.6 us after the barrier is reached.
   if constexpr (STAGED) {
     stage_to_lds();
     __builtin_amdgcn_sched_barrier(0);
@@ -1373,6 +1409,12 @@ hipError_t launch_group(const GemvArgs& a, const StreamPlan& p, hipStream_t stre
   }
 }
 
+// The strip kernel's preloaded scalar arguments, then the argument block.
+#define NIBBLE_STRIP_ARGS(a)                                                                   \
+  (a).X, (a).Wq, (a).S, (a).norm_w, static_cast<uint32_t>((a).M), static_cast<uint32_t>((a).K), \
+      static_cast<uint32_t>((a).N), static_cast<uint32_t>((a).strips), (a).L.w_row,            \
+      (a).L.strip_shift, (a)
+
 // The strip kernel at one geometry.  The grid is rounded up to a whole
 // number of XCD runs (8 workgroups per strip-per-XCD).
 template <int MT, int GROUP, int SW, int WAVES, int DEPTH>
@@ -1382,6 +1424,10 @@ hipError_t launch_strip_geometry(const GemvArgs& a, hipStream_t stream) {
   } else if constexpr (MT > 16) {
     return hipErrorInvalidValue;
   } else {
+    // The kernel rebuilds the layout from w_row and the strip shift, and
+    // derives the per-XCD strip count from the strip count.
+    if (!layout_rebuilds(a, GROUP) || a.strips_per_xcd != (a.strips + 7) / 8)
+      return hipErrorInvalidValue;
     const dim3 grid(8 * a.strips_per_xcd);
     // A dispatch asking for more LDS than a workgroup can hold (160 KiB on
     // gfx950) aborts the queue: every launch below is checked against it.
@@ -1404,33 +1450,33 @@ hipError_t launch_strip_geometry(const GemvArgs& a, hipStream_t stream) {
       if (a.stamps != nullptr && a.norm_w == nullptr) {
         if (staged) {
           if (onepass)
-            gemv_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, false, true, true, true><<<grid, WAVES * 64, lds, stream>>>(a);
+            gemv_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, false, true, true, true><<<grid, WAVES * 64, lds, stream>>>(NIBBLE_STRIP_ARGS(a));
           else
-            gemv_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, false, false, true, true><<<grid, WAVES * 64, lds, stream>>>(a);
+            gemv_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, false, false, true, true><<<grid, WAVES * 64, lds, stream>>>(NIBBLE_STRIP_ARGS(a));
         } else {
           if (onepass)
-            gemv_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, false, true, false, true><<<grid, WAVES * 64, 0, stream>>>(a);
+            gemv_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, false, true, false, true><<<grid, WAVES * 64, 0, stream>>>(NIBBLE_STRIP_ARGS(a));
           else
-            gemv_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, false, false, false, true><<<grid, WAVES * 64, 0, stream>>>(a);
+            gemv_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, false, false, false, true><<<grid, WAVES * 64, 0, stream>>>(NIBBLE_STRIP_ARGS(a));
         }
         return hipGetLastError();
       }
     }
     if (a.norm_w != nullptr) {
       if (onepass)
-        gemv_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, true, true, true><<<grid, WAVES * 64, lds, stream>>>(a);
+        gemv_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, true, true, true><<<grid, WAVES * 64, lds, stream>>>(NIBBLE_STRIP_ARGS(a));
       else
-        gemv_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, true, false, true><<<grid, WAVES * 64, lds, stream>>>(a);
+        gemv_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, true, false, true><<<grid, WAVES * 64, lds, stream>>>(NIBBLE_STRIP_ARGS(a));
     } else if (staged) {
       if (onepass)
-        gemv_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, false, true, true><<<grid, WAVES * 64, lds, stream>>>(a);
+        gemv_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, false, true, true><<<grid, WAVES * 64, lds, stream>>>(NIBBLE_STRIP_ARGS(a));
       else
-        gemv_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, false, false, true><<<grid, WAVES * 64, lds, stream>>>(a);
+        gemv_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, false, false, true><<<grid, WAVES * 64, lds, stream>>>(NIBBLE_STRIP_ARGS(a));
     } else {
       if (onepass)
-        gemv_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, false, true, false><<<grid, WAVES * 64, 0, stream>>>(a);
+        gemv_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, false, true, false><<<grid, WAVES * 64, 0, stream>>>(NIBBLE_STRIP_ARGS(a));
       else
-        gemv_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, false, false, false><<<grid, WAVES * 64, 0, stream>>>(a);
+        gemv_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, false, false, false><<<grid, WAVES * 64, 0, stream>>>(NIBBLE_STRIP_ARGS(a));
     }
     return hipGetLastError();
   }
