@@ -1159,7 +1159,12 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_strip_kernel(
   // weight load in flight.  Issuing the first group's weights ahead of the
   // copies (the barrier then waits for that group, which the first compute
   // needs anyway) measured slower: 4096 x 14336 M = 1 7.17 against 7.00 us,
-  // the copies landing ~0.6 us after the barrier is reached.
+  // the copies landing ~0.6 us after the barrier is reached.  So did a fifth
+  // wave issuing the copies while the four compute waves issue their weights
+  // at entry (8.17 us): a CU returns the copies' data behind the weights
+  // already queued, 1.3 us after issue.  Workgroup-uniform address bases with
+  // 24-bit row products left the prologue's ~0.8 us (mostly the issue of 44
+  // 1 KiB requests per CU) unchanged.
   if constexpr (STAGED) {
     stage_to_lds();
     __builtin_amdgcn_sched_barrier(0);
