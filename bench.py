@@ -13,14 +13,17 @@ one ``nibblegemm_amd.gemv`` call (M=1) over one batch of synthetic inputs
 * Inputs are resident in HBM before timing.  Each step reads a different copy
   of the packed weights and scales from a rotation spanning >= 1 GiB, so no
   step is served from the 256 MiB Infinity Cache or the L2s.
-* ``--warmup W`` eager steps run untimed, then the K timed steps are captured
-  into one HIP graph (capture executes nothing), replayed untimed for ~0.25 s
+* ``--warmup W`` eager steps run untimed, then the timed steps are captured
+  into one HIP graph (capture executes nothing) of C = max(K,
+  ``--min-graph-calls``) calls (1000: each graph launch adds ~3.6 us of its
+  own between replays, 3% of a 20-call replay), replayed untimed for ~0.25 s
   so the timed window starts at the loaded shader clock, and then replayed
   R times back to back between two events on the replay stream, bracketed by
   ``torch.cuda.synchronize()``.  R is the smallest count whose window lasts
   at least ``--min-window-ms`` (30 ms), whatever K is, so the figure does not
   depend on K and the sysfs clock / power sampler (10 ms period) sees the
-  window: ``ms_per_step`` = window / (R * K), and ``timed_replays`` = R.
+  window: ``ms_per_step`` = window / (R * C), ``timed_replays`` = R and
+  ``calls_per_replay`` = C.
   ``clock`` holds the shader clock at the window's start and end, min /
   mean / max over it, and the reference's ``throttled`` test (the clock
   moving by more than 5%).
@@ -143,7 +146,9 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--min-window-ms", type=float, default=30.0,
-                    help="shortest timed window; the K-step graph is replayed until it is reached")
+                    help="shortest timed window; the graph is replayed until it is reached")
+    ap.add_argument("--min-graph-calls", type=int, default=1000,
+                    help="fewest calls captured in the timed graph (at least --steps)")
     ap.add_argument("--no-cpu-shapes", action="store_true",
                     help="time the CPU path at the headline shape only")
     ap.add_argument("--skip-extras", action="store_true",
@@ -191,8 +196,9 @@ def main() -> int:
         ng.gemv(X, variants[i])
     torch.cuda.synchronize()
 
-    # ---- K timed steps: one HIP graph of K calls -------------------------------
-    runner = H.GraphRunner(lambda i: ng.gemv(X, variants[i]), reps=steps, warmup=0)
+    # ---- timed steps: one HIP graph of max(K, --min-graph-calls) calls ----------
+    calls = max(steps, args.min_graph_calls)
+    runner = H.GraphRunner(lambda i: ng.gemv(X, variants[i]), reps=calls, warmup=0)
     runner.graph.replay()  # untimed: first replay uploads the graph
     torch.cuda.synchronize()
     ms_per_step, replays, clocks = runner.time_window(min_ms=args.min_window_ms, warm_s=0.25)
@@ -334,7 +340,8 @@ def main() -> int:
         "steps": steps,
         "warmup": warmup,
         "timed_replays": replays,
-        "timed_window_ms": round(ms_per_step * replays * steps, 3),
+        "calls_per_replay": calls,
+        "timed_window_ms": round(ms_per_step * replays * calls, 3),
         "ms_per_step": round(ms_per_step, 6),
         "higher_is_better": True,
         "scaling": "weak",
