@@ -923,11 +923,13 @@ __global__ __launch_bounds__((4 * SPW + STAGERS) * 64) void gemv_batch_kernel(Ge
 // same for 8-byte scale quads.  NORM (RMSNorm prologue) fills the activation
 // rows itself and implies STAGED.
 //
-// Kernel arguments.  The fields the prologue needs before its first weight
-// load come first, as 14 scalar dwords (gfx950's limit), and the library is
-// built with kernel-argument preloading, so the command processor writes
-// them into SGPRs at wave launch: the copies and weight loads issue without
-// a kernel-argument fetch (~0.9 us at the headline shape).  The rest of the
+// Kernel arguments.  The body takes the fields the prologue needs before its
+// first weight load as scalars.  The packed-weight entry (gemv_strip_kernel)
+// receives them as its first 14 scalar dwords (gfx950's limit), and the
+// library is built with kernel-argument preloading, so the command processor
+// writes them into SGPRs at wave launch: the copies and weight loads issue
+// without a kernel-argument fetch.  The strip-major entry
+// (gemv_strip_kernel_block) reads them from its argument block.  The rest of the
 // call (outputs, epilogue, timeline buffer) stays in the GemvArgs block,
 // which is fetched while the weights stream.  The weight layout is rebuilt
 // from its row stride and strip shift (every layout has s_row = w_row / 2,
@@ -937,11 +939,11 @@ __global__ __launch_bounds__((4 * SPW + STAGERS) * 64) void gemv_batch_kernel(Ge
 // same way measured no change (14336 x 4096 M = 16..32, the 224-launch 8B
 // step).
 template <int MT, int GROUP, int SW, int WAVES, int DEPTH, bool NORM, bool ONEPASS, bool STAGED,
-          bool TIMELINE = false>
-__global__ __launch_bounds__(WAVES * 64) void gemv_strip_kernel(
-    const _Float16* __restrict__ Xp, const uint32_t* __restrict__ Wqp, const _Float16* __restrict__ Sp,
-    const _Float16* __restrict__ norm_wp, uint32_t Mp, uint32_t Kp, uint32_t Np, uint32_t strips_p,
-    uint32_t w_row_p, uint32_t strip_shift_p, GemvArgs a) {
+          bool TIMELINE>
+__device__ __forceinline__ void strip_body(
+    const _Float16* Xp, const uint32_t* Wqp, const _Float16* Sp,
+    const _Float16* norm_wp, uint32_t Mp, uint32_t Kp, uint32_t Np, uint32_t strips_p,
+    uint32_t w_row_p, uint32_t strip_shift_p, const GemvArgs& a) {
   // TIMELINE: s_memrealtime ticks (100 MHz) at the points nibble_gemv_timeline
   // lists; only that instantiation has them.
   unsigned long long tl[7] = {};
@@ -1285,6 +1287,37 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_strip_kernel(
   }
 }
 
+// The strip kernel on packed weights: its prologue's fields preloaded.
+template <int MT, int GROUP, int SW, int WAVES, int DEPTH, bool NORM, bool ONEPASS, bool STAGED,
+          bool TIMELINE = false>
+__global__ __launch_bounds__(WAVES * 64) void gemv_strip_kernel(
+    const _Float16* Xp, const uint32_t* Wqp, const _Float16* Sp,
+    const _Float16* norm_wp, uint32_t Mp, uint32_t Kp, uint32_t Np, uint32_t strips_p,
+    uint32_t w_row_p, uint32_t strip_shift_p, GemvArgs a) {
+  strip_body<MT, GROUP, SW, WAVES, DEPTH, NORM, ONEPASS, STAGED, TIMELINE>(
+      Xp, Wqp, Sp, norm_wp, Mp, Kp, Np, strips_p, w_row_p, strip_shift_p, a);
+}
+
+// The strip kernel on strip-major weights: every field from the argument
+// block, as its waves fetch it.  Measured on MI355X (graph replay, M = 1,
+// same-box A/B against the kernel before preloading): preloaded fields gain
+// on packed weights (4096 x 14336 7.40-7.46 -> 7.24-7.28 us, 8192 x 8192
+// 9.09-9.10 -> 8.79-8.84, 4096 x 6144 5.43-5.52 -> 5.32-5.42) but cost the
+// strip-major 8192 x 8192 plan 8% (7.96-8.02 -> 8.61-8.71; through this entry
+// 7.88-7.94), the other strip-major shapes within noise either way.
+//
+// The operand pointers carry no __restrict__: with it the compiler treated
+// the buffer loads as invariant and re-issued the first group's loads inside
+// the one-pass compute branch, draining the ring there (strip-major 4096 x
+// 4096 4.0 -> 4.35 us).
+template <int MT, int GROUP, int SW, int WAVES, int DEPTH, bool NORM, bool ONEPASS, bool STAGED,
+          bool TIMELINE = false>
+__global__ __launch_bounds__(WAVES * 64) void gemv_strip_kernel_block(GemvArgs a) {
+  strip_body<MT, GROUP, SW, WAVES, DEPTH, NORM, ONEPASS, STAGED, TIMELINE>(
+      a.X, a.Wq, a.S, a.norm_w, static_cast<uint32_t>(a.M), static_cast<uint32_t>(a.K),
+      static_cast<uint32_t>(a.N), static_cast<uint32_t>(a.strips), a.L.w_row, a.L.strip_shift, a);
+}
+
 // Versions 0 and 1: one thread per (m, n), scalar decode, fp32 weights
 // (n - 8) * s and fp32 accumulation.  REUSE = false reloads the packed word for
 // every k (v0), REUSE = true uses each word for its 8 k (v1).
@@ -1420,6 +1453,19 @@ hipError_t launch_group(const GemvArgs& a, const StreamPlan& p, hipStream_t stre
       static_cast<uint32_t>((a).N), static_cast<uint32_t>((a).strips), (a).L.w_row,            \
       (a).L.strip_shift, (a)
 
+// A strip-kernel launch: the preloaded-argument entry on packed weights,
+// the argument-block entry on strip-major weights.
+template <int MT, int GROUP, int SW, int WAVES, int DEPTH, bool NORM, bool ONEPASS, bool STAGED,
+          bool TIMELINE = false>
+void launch_strip_kernel(dim3 grid, int threads, size_t lds, hipStream_t stream, const GemvArgs& a) {
+  if (a.L.strip_shift == 31)
+    gemv_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, NORM, ONEPASS, STAGED, TIMELINE>
+        <<<grid, threads, lds, stream>>>(NIBBLE_STRIP_ARGS(a));
+  else
+    gemv_strip_kernel_block<MT, GROUP, SW, WAVES, DEPTH, NORM, ONEPASS, STAGED, TIMELINE>
+        <<<grid, threads, lds, stream>>>(a);
+}
+
 // The strip kernel at one geometry.  The grid is rounded up to a whole
 // number of XCD runs (8 workgroups per strip-per-XCD).
 template <int MT, int GROUP, int SW, int WAVES, int DEPTH>
@@ -1455,33 +1501,33 @@ hipError_t launch_strip_geometry(const GemvArgs& a, hipStream_t stream) {
       if (a.stamps != nullptr && a.norm_w == nullptr) {
         if (staged) {
           if (onepass)
-            gemv_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, false, true, true, true><<<grid, WAVES * 64, lds, stream>>>(NIBBLE_STRIP_ARGS(a));
+            launch_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, false, true, true, true>(grid, WAVES * 64, lds, stream, a);
           else
-            gemv_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, false, false, true, true><<<grid, WAVES * 64, lds, stream>>>(NIBBLE_STRIP_ARGS(a));
+            launch_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, false, false, true, true>(grid, WAVES * 64, lds, stream, a);
         } else {
           if (onepass)
-            gemv_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, false, true, false, true><<<grid, WAVES * 64, 0, stream>>>(NIBBLE_STRIP_ARGS(a));
+            launch_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, false, true, false, true>(grid, WAVES * 64, 0, stream, a);
           else
-            gemv_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, false, false, false, true><<<grid, WAVES * 64, 0, stream>>>(NIBBLE_STRIP_ARGS(a));
+            launch_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, false, false, false, true>(grid, WAVES * 64, 0, stream, a);
         }
         return hipGetLastError();
       }
     }
     if (a.norm_w != nullptr) {
       if (onepass)
-        gemv_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, true, true, true><<<grid, WAVES * 64, lds, stream>>>(NIBBLE_STRIP_ARGS(a));
+        launch_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, true, true, true>(grid, WAVES * 64, lds, stream, a);
       else
-        gemv_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, true, false, true><<<grid, WAVES * 64, lds, stream>>>(NIBBLE_STRIP_ARGS(a));
+        launch_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, true, false, true>(grid, WAVES * 64, lds, stream, a);
     } else if (staged) {
       if (onepass)
-        gemv_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, false, true, true><<<grid, WAVES * 64, lds, stream>>>(NIBBLE_STRIP_ARGS(a));
+        launch_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, false, true, true>(grid, WAVES * 64, lds, stream, a);
       else
-        gemv_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, false, false, true><<<grid, WAVES * 64, lds, stream>>>(NIBBLE_STRIP_ARGS(a));
+        launch_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, false, false, true>(grid, WAVES * 64, lds, stream, a);
     } else {
       if (onepass)
-        gemv_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, false, true, false><<<grid, WAVES * 64, 0, stream>>>(NIBBLE_STRIP_ARGS(a));
+        launch_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, false, true, false>(grid, WAVES * 64, 0, stream, a);
       else
-        gemv_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, false, false, false><<<grid, WAVES * 64, 0, stream>>>(NIBBLE_STRIP_ARGS(a));
+        launch_strip_kernel<MT, GROUP, SW, WAVES, DEPTH, false, false, false>(grid, WAVES * 64, 0, stream, a);
     }
     return hipGetLastError();
   }
